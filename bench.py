@@ -1,0 +1,571 @@
+"""Benchmark of the m3 HIP execution provider on one MI355X.
+
+A step is one ``m3_session_run`` of a graph built through the public API
+(include/m3.h), with its inputs already resident in HBM. The headline
+workload is last-axis softmax F32 on an attention-score tensor
+[16, 1024, 1024] (logits ~ N(0, 3), strict upper triangle -inf); the other
+op classes (broadcast MUL, the four casts, Snake1d, the 30-step Euler CFG
+graph) are measured the same way and reported under ``op_classes``.
+
+For every class:
+  * ms_per_run    wall time of m3_session_run (includes the softmax NaN
+                  scan, launches and the closing stream synchronize);
+  * kernel_us     average duration of the dominant kernel from HIP events
+                  recorded on the session's own stream around each launch;
+  * GB/s          algorithmic bytes (unique tensor bytes read + written)
+                  divided by those times; peak HBM is 8.0 TB/s.
+Sessions rotate so that the data a run reads was last touched several runs
+earlier (working sets larger than the 256 MB Infinity Cache).
+
+The CPU baseline times the reference's own CPU provider (compiled from its
+sources into oracle/_ref when the reference tree was present) or, without
+it, the oracle restatement, single-threaded as the reference is, on the
+sample stated in the output. Every class is also checked bit for bit
+against that CPU result.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PEAK_GBPS = 8000.0
+METRIC = ("achieved HBM GB/s (% of MI355X peak) per op class; "
+          "ms per m3_session_run")
+
+
+def _package():
+    spec = importlib.util.spec_from_file_location(
+        "m3c_amd", os.path.join(ROOT, "m3.c_amd", "__init__.py"))
+    module = importlib.util.module_from_spec(spec)
+    sys.modules["m3c_amd"] = module
+    spec.loader.exec_module(module)
+    return module
+
+
+m3 = _package()
+
+
+def log(*parts):
+    print(*parts, file=sys.stderr, flush=True)
+
+
+# ---- CPU baseline (checker side: oracle/_ref or oracle) -------------------
+
+class CpuBaseline:
+    """The reference CPU provider (kind "reference") or the oracle ("port")."""
+
+    def __init__(self):
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import harness  # noqa: E402  (checker, loaded only for this leg)
+        self.harness = harness
+        self.kind = "reference" if harness.ref_available() else "port"
+
+    def run(self, kind, storages, views):
+        if self.kind == "reference":
+            return self.harness.run_ref(kind, storages, views)
+        return self.harness.run_oracle(kind, storages, views)
+
+    def timed(self, kind, storages, views):
+        start = time.perf_counter()
+        status, out = self.run(kind, storages, views)
+        return status, out, time.perf_counter() - start
+
+
+# ---- workloads -------------------------------------------------------------
+
+def softmax_input(rows_per_matrix=1024, matrices=16, seed=0):
+    n = rows_per_matrix
+    s = m3.rng_fill("normal", matrices * n * n, seed=seed, a=3.0)
+    s = s.reshape(matrices, n, n)
+    mask = np.triu(np.ones((n, n), dtype=bool), k=1)
+    s[:, mask] = -np.inf
+    return s
+
+
+def cast_inputs(n=4096, seed=0):
+    rng = m3.rng_new(seed, 0)
+    t = m3.rng_fill("normal", n * n, seed=seed, a=1000.0, rng=rng)
+    pick = m3.rng_fill("uniform", n * n, seed=seed, rng=rng)
+    special_kind = m3.rng_fill("uniform", n * n, seed=seed, a=0.0, b=6.0,
+                               rng=rng)
+    payload = (m3.rng_fill("uniform", n * n, seed=seed, a=0.0,
+                           b=float(1 << 22), rng=rng)).astype(np.uint32)
+    bits = t.view(np.uint32).copy()
+    special = pick < 0.05
+    kinds = special_kind.astype(np.uint32)
+    table = [
+        payload & 0x7fffff,                       # subnormal
+        np.zeros_like(payload),                   # +0
+        np.full_like(payload, 0x80000000),        # -0
+        np.full_like(payload, 0x7f800000),        # +inf
+        np.full_like(payload, 0xff800000),        # -inf
+        0x7f800000 | (payload | 1),               # NaN payloads (q and s)
+    ]
+    chosen = np.choose(np.minimum(kinds, 5), table).astype(np.uint32)
+    signs = (payload & 1).astype(np.uint32) << 31
+    chosen = np.where(kinds == 5, chosen | signs, chosen)
+    bits[special] = chosen[special]
+    t = bits.view(np.float32).reshape(n, n)
+    half = t.astype(np.float16).view(np.uint16)
+    brain = (t.view(np.uint32) >> 16).astype(np.uint16)
+    return t, half, brain
+
+
+class Workload:
+    """One graph, `rotate` independent sessions of it, and its CPU check."""
+
+    def __init__(self, name, build, inputs, algorithmic_bytes, kernel,
+                 rotate, cpu):
+        self.name = name
+        self.algorithmic_bytes = algorithmic_bytes
+        self.kernel = kernel
+        self.sessions = []
+        self.outputs = None
+        self.cpu = cpu
+        for _ in range(rotate):
+            graph, feeds, outputs = build()
+            session = m3.Session(graph)
+            graph.free()
+            for value, array in feeds:
+                session.write(value, array)
+            self.sessions.append(session)
+            self.outputs = outputs
+        for session in self.sessions:
+            for node in range(session.plan().node_count):
+                if session.provider(node) != m3.PROVIDER_HIP:
+                    raise RuntimeError("%s: node %d is not on the HIP "
+                                       "provider" % (name, node))
+        self.inputs = inputs
+
+    def measure(self, steps, warmup):
+        for i in range(warmup):
+            self.sessions[i % len(self.sessions)].run()
+        for session in self.sessions:
+            session.timing_reset()
+            session.timing_enable(False)
+        start = time.perf_counter()
+        for i in range(steps):
+            self.sessions[i % len(self.sessions)].run()
+        wall = (time.perf_counter() - start) / steps
+        for session in self.sessions:
+            session.timing_enable(True)
+        for i in range(steps):
+            self.sessions[i % len(self.sessions)].run()
+        launches = 0
+        total_ms = 0.0
+        per_kernel = {}
+        for session in self.sessions:
+            for name, (count, ms) in session.timing_read().items():
+                previous = per_kernel.get(name, (0, 0.0))
+                per_kernel[name] = (previous[0] + count, previous[1] + ms)
+                session.timing_enable(False)
+        for name in self.kernel:
+            count, ms = per_kernel.get(name, (0, 0.0))
+            launches += count
+            total_ms += ms
+        kernel_us = 1000.0 * total_ms / max(launches, 1)
+        runs_kernel_ms = sum(ms for _, ms in per_kernel.values()) / steps
+        return wall * 1000.0, kernel_us, launches // steps, per_kernel, \
+            runs_kernel_ms
+
+    def read_output(self, index=0):
+        value, shape, dtype = self.outputs
+        out = np.empty(shape, dtype=dtype)
+        return self.sessions[index].read(value, out)
+
+    def free(self):
+        for session in self.sessions:
+            session.free()
+        self.sessions = []
+
+
+def build_softmax(s):
+    def build():
+        graph = m3.Graph()
+        vin = graph.add_value(m3.INPUT, m3.F32, s.shape)
+        vout = graph.add_value(m3.OUTPUT, m3.F32, s.shape)
+        graph.add_node(m3.OP_SOFTMAX, [vin], [vout])
+        return graph, [(vin, s)], (vout, s.shape, np.float32)
+    return build
+
+
+def build_mul(x, c):
+    def build():
+        graph = m3.Graph()
+        vx = graph.add_value(m3.INPUT, m3.F32, x.shape)
+        vc = graph.add_value(m3.CONSTANT, m3.F32, c.shape)
+        vy = graph.add_value(m3.OUTPUT, m3.F32, x.shape)
+        graph.set_constant(vc, c)
+        graph.add_node(m3.OP_MUL, [vx, vc], [vy])
+        return graph, [(vx, x)], (vy, x.shape, np.float32)
+    return build
+
+
+def build_cast(src, src_dtype, dst_dtype, dst_np):
+    def build():
+        graph = m3.Graph()
+        vin = graph.add_value(m3.INPUT, src_dtype, src.shape)
+        vout = graph.add_value(m3.OUTPUT, dst_dtype, src.shape)
+        graph.add_node(m3.OP_CAST, [vin], [vout])
+        return graph, [(vin, src)], (vout, src.shape, dst_np)
+    return build
+
+
+def build_snake(x, alpha):
+    def build():
+        graph = m3.Graph()
+        vx = graph.add_value(m3.INPUT, m3.F32, x.shape)
+        va = graph.add_value(m3.CONSTANT, m3.F32, alpha.shape)
+        vy = graph.add_value(m3.OUTPUT, m3.F32, x.shape)
+        graph.set_constant(va, alpha)
+        graph.add_node(m3.OP_SNAKE1D, [vx, va], [vy])
+        return graph, [(vx, x)], (vy, x.shape, np.float32)
+    return build
+
+
+def build_euler(x, vus, vcs, scale=3.0, dt=1.0 / 30.0):
+    """30-step CFG + Euler graph in the reference's op order
+    (src/m3_flow_solver_math.c:36-135): a = vu*(-1); a = vc + a; a = a*s;
+    v = vu + a; b = v*dt; x = x + b."""
+    def build():
+        graph = m3.Graph()
+        shape = x.shape
+        vx = graph.add_value(m3.INPUT, m3.F32, shape)
+        consts = {}
+        for name, value in (("minus_one", -1.0), ("scale", scale),
+                            ("dt", dt)):
+            vid = graph.add_value(m3.CONSTANT, m3.F32, (1,))
+            graph.set_constant(vid, np.array([value], np.float32))
+            consts[name] = vid
+        current = vx
+        steps = len(vus)
+        for k in range(steps):
+            vu = graph.add_value(m3.CONSTANT, m3.F32, shape)
+            vc = graph.add_value(m3.CONSTANT, m3.F32, shape)
+            graph.set_constant(vu, vus[k])
+            graph.set_constant(vc, vcs[k])
+            t = [graph.add_value(m3.TEMPORARY, m3.F32, shape)
+                 for _ in range(5)]
+            nxt = graph.add_value(m3.OUTPUT if k == steps - 1
+                                  else m3.TEMPORARY, m3.F32, shape)
+            graph.add_node(m3.OP_MUL, [vu, consts["minus_one"]], [t[0]])
+            graph.add_node(m3.OP_ADD, [vc, t[0]], [t[1]])
+            graph.add_node(m3.OP_MUL, [t[1], consts["scale"]], [t[2]])
+            graph.add_node(m3.OP_ADD, [vu, t[2]], [t[3]])
+            graph.add_node(m3.OP_MUL, [t[3], consts["dt"]], [t[4]])
+            graph.add_node(m3.OP_ADD, [current, t[4]], [nxt])
+            current = nxt
+        return graph, [(vx, x)], (current, shape, np.float32)
+    return build
+
+
+def spec(storage, dtype, shape, strides=None):
+    return baseline_harness().ViewSpec(storage, dtype, tuple(shape), strides)
+
+
+_HARNESS = None
+
+
+def baseline_harness():
+    global _HARNESS
+    if _HARNESS is None:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import harness
+        _HARNESS = harness
+    return _HARNESS
+
+
+def as_bytes(array):
+    return np.ascontiguousarray(array).view(np.uint8).reshape(-1).copy()
+
+
+def result_entry(name, workload, wall_ms, kernel_us, launches, bytes_total,
+                 kernel_bytes, parity, cpu_seconds=None, cpu_bytes=None):
+    kernel_gbps = kernel_bytes / (kernel_us * 1e-6) / 1e9 if kernel_us else 0
+    entry = {
+        "op_class": name,
+        "algorithmic_bytes_per_run": bytes_total,
+        "ms_per_run": round(wall_ms, 4),
+        "run_GBps": round(bytes_total / (wall_ms * 1e-3) / 1e9, 1),
+        "kernel": workload.kernel[0],
+        "kernel_launches_per_run": launches,
+        "kernel_us": round(kernel_us, 3),
+        "kernel_GBps": round(kernel_gbps, 1),
+        "kernel_frac_of_peak": round(kernel_gbps / PEAK_GBPS, 4),
+        "parity": parity,
+    }
+    if cpu_seconds is not None:
+        entry["cpu_GBps"] = round(cpu_bytes / cpu_seconds / 1e9, 4)
+    return entry
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--rotate", type=int, default=4)
+    parser.add_argument("--classes", default="softmax,mul,cast,snake,euler",
+                        help="comma-separated op classes to run")
+    parser.add_argument("--no-cpu", action="store_true",
+                        help="skip the CPU baseline and CPU parity check")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this provider has no multi-GPU "
+              "path (each op shards with zero exchange; see the design "
+              "notes). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    m3.load()
+    if m3.hip_device_count() == 0:
+        print("no HIP device visible: the HIP provider cannot run",
+              file=sys.stderr)
+        return 1
+    classes = [c for c in args.classes.split(",") if c]
+    cpu = None if args.no_cpu else CpuBaseline()
+    results = {}
+    headline = None
+    cpu_line = None
+
+    if "softmax" in classes:
+        log("softmax: generating [16,1024,1024] logits")
+        s = softmax_input()
+        nbytes = 2 * s.nbytes
+        w = Workload("softmax", build_softmax(s), [s], nbytes,
+                     ["m3_softmax_rows"], args.rotate, cpu)
+        wall, kus, launches, kernels, _ = w.measure(args.steps, args.warmup)
+        parity = None
+        cpu_seconds = None
+        if cpu is not None:
+            out = w.read_output()
+            status, storages, cpu_seconds = cpu.timed(
+                m3.OP_SOFTMAX, [as_bytes(s), np.zeros(s.nbytes, np.uint8)],
+                [spec(0, m3.F32, s.shape), spec(1, m3.F32, s.shape)])
+            ref = storages[1].view(np.float32).reshape(s.shape)
+            mismatches = int(np.count_nonzero(ref.view(np.uint32) !=
+                                              out.view(np.uint32)))
+            parity = "bit-exact" if mismatches == 0 else \
+                "%d of %d elements differ" % (mismatches, s.size)
+            cpu_line = {"value": round(nbytes / cpu_seconds / 1e9, 4),
+                        "unit": "GB/s", "cores": 1, "kind": cpu.kind,
+                        "sample": "the full [16,1024,1024] softmax, one "
+                                  "run of the single-threaded CPU provider"}
+        results["softmax"] = result_entry("softmax", w, wall, kus, launches,
+                                          nbytes, nbytes, parity, cpu_seconds,
+                                          nbytes)
+        results["softmax"]["kernels"] = {k: v[1] / max(v[0], 1) * 1000
+                                         for k, v in kernels.items()}
+        headline = (w, wall, kus, nbytes)
+        w.free()
+        log("softmax:", json.dumps(results["softmax"]))
+
+    if "mul" in classes:
+        log("mul: generating x[8,1024,1536], c[1536]")
+        rng = m3.rng_new(0, 0)
+        x = m3.rng_fill("uniform", 8 * 1024 * 1536, seed=0, a=-1.0, b=1.0,
+                        rng=rng).reshape(8, 1024, 1536)
+        c = m3.rng_fill("normal", 1536, seed=0, a=1.0, rng=rng)
+        nbytes = 2 * x.nbytes + c.nbytes
+        w = Workload("mul", build_mul(x, c), [x, c], nbytes,
+                     ["m3_binary_mul"], args.rotate, cpu)
+        wall, kus, launches, _, _ = w.measure(args.steps, args.warmup)
+        parity = None
+        cpu_seconds = None
+        if cpu is not None:
+            out = w.read_output()
+            status, storages, cpu_seconds = cpu.timed(
+                m3.OP_MUL, [as_bytes(x), as_bytes(c),
+                            np.zeros(x.nbytes, np.uint8)],
+                [spec(0, m3.F32, x.shape), spec(1, m3.F32, c.shape),
+                 spec(2, m3.F32, x.shape)])
+            ref = storages[2].view(np.uint32)
+            mismatches = int(np.count_nonzero(ref != out.view(np.uint32)
+                                              .reshape(-1)))
+            parity = "bit-exact" if mismatches == 0 else \
+                "%d elements differ" % mismatches
+        results["mul"] = result_entry("mul", w, wall, kus, launches, nbytes,
+                                      nbytes, parity, cpu_seconds, nbytes)
+        w.free()
+        log("mul:", json.dumps(results["mul"]))
+
+    if "cast" in classes:
+        log("cast: generating [4096,4096] with 5% specials")
+        t, half, brain = cast_inputs()
+        pairs = [("cast_f32_f16", t, m3.F32, m3.F16, np.uint16,
+                  "m3_cast_f32_f16"),
+                 ("cast_f16_f32", half, m3.F16, m3.F32, np.float32,
+                  "m3_cast_f16_f32"),
+                 ("cast_f32_bf16", t, m3.F32, m3.BF16, np.uint16,
+                  "m3_cast_f32_bf16"),
+                 ("cast_bf16_f32", brain, m3.BF16, m3.F32, np.float32,
+                  "m3_cast_bf16_f32")]
+        for name, src, sd, dd, dnp, kernel in pairs:
+            out_bytes = src.size * np.dtype(dnp).itemsize
+            nbytes = src.nbytes + out_bytes
+            w = Workload(name, build_cast(src, sd, dd, dnp), [src], nbytes,
+                         [kernel], args.rotate, cpu)
+            wall, kus, launches, _, _ = w.measure(args.steps, args.warmup)
+            parity = None
+            cpu_seconds = None
+            if cpu is not None:
+                out = w.read_output()
+                status, storages, cpu_seconds = cpu.timed(
+                    m3.OP_CAST, [as_bytes(src), np.zeros(out_bytes,
+                                                         np.uint8)],
+                    [spec(0, sd, src.shape), spec(1, dd, src.shape)])
+                mismatches = int(np.count_nonzero(
+                    storages[1] != out.view(np.uint8).reshape(-1)))
+                parity = "bit-exact" if mismatches == 0 else \
+                    "%d bytes differ" % mismatches
+            results[name] = result_entry(name, w, wall, kus, launches,
+                                         nbytes, nbytes, parity, cpu_seconds,
+                                         nbytes)
+            w.free()
+            log(name + ":", json.dumps(results[name]))
+
+    if "snake" in classes:
+        log("snake: generating x[2,1536,65536], alpha[1,1536,1]")
+        rng = m3.rng_new(0, 0)
+        x = m3.rng_fill("normal", 2 * 1536 * 65536, seed=0, a=1.0,
+                        rng=rng).reshape(2, 1536, 65536)
+        alpha = m3.rng_fill("uniform", 1536, seed=0, a=0.1, b=2.0,
+                            rng=rng).reshape(1, 1536, 1)
+        nbytes = 2 * x.nbytes + alpha.nbytes
+        w = Workload("snake", build_snake(x, alpha), [x, alpha], nbytes,
+                     ["m3_snake1d"], 1, cpu)
+        wall, kus, launches, _, _ = w.measure(max(args.steps // 4, 3),
+                                              args.warmup)
+        parity = None
+        cpu_seconds = None
+        if cpu is not None:
+            out = w.read_output()
+            sample = x[:, :96, :]  # 96 channels of both batches (1/16)
+            status, storages, cpu_seconds = cpu.timed(
+                m3.OP_SNAKE1D, [as_bytes(sample), as_bytes(alpha[:, :96]),
+                                np.zeros(sample.nbytes, np.uint8)],
+                [spec(0, m3.F32, sample.shape),
+                 spec(1, m3.F32, (1, 96, 1)),
+                 spec(2, m3.F32, sample.shape)])
+            ref = storages[2].view(np.uint32).reshape(sample.shape)
+            mismatches = int(np.count_nonzero(
+                ref != out[:, :96, :].view(np.uint32)))
+            parity = ("bit-exact on the CPU sample (channels 0-95)"
+                      if mismatches == 0 else
+                      "%d of %d sampled elements differ" %
+                      (mismatches, sample.size))
+        results["snake"] = result_entry(
+            "snake", w, wall, kus, launches, nbytes, nbytes, parity,
+            cpu_seconds, 2 * x[:, :96, :].nbytes)
+        w.free()
+        log("snake:", json.dumps(results["snake"]))
+
+    if "euler" in classes:
+        log("euler: generating x and 30 x (vu, vc) [2,4096,1536]")
+        shape = (2, 4096, 1536)
+        count = int(np.prod(shape))
+        rng = m3.rng_new(0, 0)
+        x = m3.rng_fill("normal", count, seed=0, a=1.0,
+                        rng=rng).reshape(shape)
+        vus, vcs = [], []
+        for _ in range(30):
+            vus.append(m3.rng_fill("normal", count, seed=0, a=1.0,
+                                   rng=rng).reshape(shape))
+            vcs.append(m3.rng_fill("normal", count, seed=0, a=1.0,
+                                   rng=rng).reshape(shape))
+        tensor = x.nbytes
+        nbytes = 15 * tensor * 30
+        w = Workload("euler", build_euler(x, vus, vcs), [x], nbytes,
+                     ["m3_binary_add", "m3_binary_mul"], 1, cpu)
+        wall, kus, launches, kernels, run_kernel_ms = w.measure(
+            max(args.steps // 4, 3), args.warmup)
+        parity = None
+        cpu_seconds = None
+        if cpu is not None:
+            out = w.read_output()
+            parity = euler_parity(cpu, x, vus, vcs, out)
+        entry = result_entry("euler", w, wall, kus, launches, nbytes,
+                             nbytes / 180.0, parity)
+        entry["kernel_time_per_run_ms"] = round(run_kernel_ms, 4)
+        entry["fused_lower_bound_bytes"] = 4 * tensor * 30
+        entry["slots"] = None
+        results["euler"] = entry
+        w.free()
+        log("euler:", json.dumps(results["euler"]))
+
+    if headline is None:
+        print(json.dumps({"metric": METRIC, "op_classes": results}))
+        return 0
+    w, wall, kus, nbytes = headline
+    achieved = nbytes / (kus * 1e-6) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(nbytes / (wall * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (PCG32 seed 0, the reference generator)",
+        "config": {"workload": "softmax F32 [16,1024,1024], logits ~N(0,3), "
+                               "causal -inf upper triangle, one "
+                               "m3_session_run per step",
+                   "rotating_sessions": args.rotate},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu_line,
+        "op_classes": results,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+def euler_parity(cpu, x, vus, vcs, out):
+    """Replays the 30-step graph on the CPU provider for the first 96 rows
+    of the latent (the op sequence is elementwise, so any slice is exact)."""
+    rows = 96
+    xs = np.ascontiguousarray(x[:, :rows, :])
+    shape = xs.shape
+    scalars = {"m1": np.array([-1.0], np.float32),
+               "s": np.array([3.0], np.float32),
+               "dt": np.array([1.0 / 30.0], np.float32)}
+
+    def op(kind, a, b):
+        status, storages = cpu.run(
+            kind, [as_bytes(a), as_bytes(b), np.zeros(a.nbytes, np.uint8)],
+            [spec(0, m3.F32, a.shape), spec(1, m3.F32, b.shape),
+             spec(2, m3.F32, a.shape)])
+        return storages[2].view(np.float32).reshape(a.shape)
+
+    current = xs
+    for k in range(len(vus)):
+        vu = np.ascontiguousarray(vus[k][:, :rows, :])
+        vc = np.ascontiguousarray(vcs[k][:, :rows, :])
+        a = op(m3.OP_MUL, vu, scalars["m1"])
+        a = op(m3.OP_ADD, vc, a)
+        a = op(m3.OP_MUL, a, scalars["s"])
+        v = op(m3.OP_ADD, vu, a)
+        b = op(m3.OP_MUL, v, scalars["dt"])
+        current = op(m3.OP_ADD, current, b)
+    got = out[:, :rows, :]
+    mismatches = int(np.count_nonzero(current.view(np.uint32) !=
+                                      got.view(np.uint32)))
+    return ("bit-exact on the CPU sample (rows 0-95)" if mismatches == 0
+            else "%d of %d sampled elements differ" % (mismatches,
+                                                       current.size))
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,186 @@
+/*
+ * m3_hip.h - thin C ABI over the HIP runtime and the gfx950 kernels of the
+ * m3 HIP execution provider.
+ *
+ * This is the boundary the C11 host code binds. It takes plain pointers,
+ * sizes and POD view blocks; no m3 or torch types cross it. Every function
+ * returns an m3_hip_code and, on failure, writes a NUL-terminated message of
+ * at most `capacity` bytes into `message` (which may be NULL).
+ *
+ * Each entry point replaces one piece of the Metal provider of
+ * taconotsandwich/m3.c:
+ *   m3_hip_device_open/close     <- m3_backend_create_metal and
+ *                                   m3_metal_destroy (src/m3_backend_metal.m:
+ *                                   234-296, :44-58): device, queue, library
+ *   m3_hip_arena_reserve/release <- m3_metal_allocate/m3_metal_free
+ *                                   (src/m3_backend_metal.m:60-96); one
+ *                                   hipMalloc per session instead of one
+ *                                   shared MTLBuffer per slot
+ *   m3_hip_copy_h2d/d2h          <- memcpy into shared storage in
+ *                                   m3_storage_write/read (src/m3_backend.c:
+ *                                   319-366); unified memory does not exist
+ *                                   here, so these are the explicit copies
+ *   m3_hip_launch_binary         <- m3_metal_encode_binary
+ *                                   (src/m3_backend_metal_basic.m:354-395),
+ *                                   kernels m3_add/m3_mul (:66-104)
+ *   m3_hip_launch_cast/copy      <- m3_metal_encode_unary (:326-352),
+ *                                   kernels m3_cast/m3_copy (:29-63)
+ *   m3_hip_launch_softmax        <- m3_metal_encode_softmax (:397-433),
+ *                                   kernel m3_softmax (:105-147)
+ *   m3_hip_launch_snake1d        <- m3_metal_encode_snake1d, kernel
+ *                                   m3_snake1d (:150-177)
+ *   m3_hip_scan_views            <- the host data preflight Metal runs on
+ *                                   shared memory before commit
+ *                                   (src/m3_backend_metal_basic.m:274-302,
+ *                                   src/m3_op_data_preflight.c:8-64)
+ *   m3_hip_synchronize           <- commit + waitUntilCompleted
+ *                                   (src/m3_backend_metal.m:210-216)
+ *
+ * All launches of one device go to that device's single HIP stream, in call
+ * order, so a command list executes in order and m3_hip_synchronize waits
+ * for all of it. A device handle is not thread-safe.
+ */
+#ifndef M3_HIP_H
+#define M3_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define M3_HIP_MAX_RANK 8U
+
+typedef enum {
+    M3_HIP_OK = 0,
+    M3_HIP_INVALID = 1,      /* malformed argument or view block */
+    M3_HIP_NO_DEVICE = 2,    /* no usable HIP device */
+    M3_HIP_OUT_OF_MEMORY = 3,
+    M3_HIP_RUNTIME = 4,      /* the HIP runtime reported an error */
+    M3_HIP_UNSUPPORTED = 5   /* valid request this build cannot run */
+} m3_hip_code;
+
+/* Element types; values equal m3_dtype. */
+typedef enum {
+    M3_HIP_F32 = 0,
+    M3_HIP_F16 = 1,
+    M3_HIP_BF16 = 2,
+    M3_HIP_I32 = 3
+} m3_hip_dtype;
+
+typedef enum {
+    M3_HIP_ADD = 0,
+    M3_HIP_MUL = 1,
+    M3_HIP_SUB = 2,
+    M3_HIP_DIV = 3
+} m3_hip_binary_op;
+
+typedef enum {
+    M3_HIP_SCAN_NAN = 0,        /* flag when any element is NaN */
+    M3_HIP_SCAN_I32_RANGE = 1   /* flag when any element is non-finite or
+                                   outside [-2^31, 2^31) */
+} m3_hip_scan_kind;
+
+/* A strided tensor view over device memory. Element (i0, ..., ir-1) lives at
+ * base + byte_offset + sum(ik * byte_strides[k]). element_count is the
+ * product of shape[0..rank). Output views must be contiguous. The layout
+ * matches M3ViewParameters of the reference (src/m3_backend_metal_helpers.h:
+ * 12-19) plus the base pointer. */
+typedef struct {
+    void *base;
+    uint64_t byte_offset;
+    uint64_t element_count;
+    uint64_t shape[M3_HIP_MAX_RANK];
+    uint64_t byte_strides[M3_HIP_MAX_RANK];
+    uint32_t rank;
+    uint32_t dtype;
+} m3_hip_view;
+
+typedef struct m3_hip_device m3_hip_device;
+
+/* Per-kernel timing gathered with HIP events on the device stream. */
+typedef struct {
+    char name[48];
+    uint64_t launches;
+    double total_ms;
+} m3_hip_kernel_time;
+
+int m3_hip_device_count(int *count, char *message, size_t capacity);
+int m3_hip_device_open(int ordinal, m3_hip_device **device,
+                       char *message, size_t capacity);
+void m3_hip_device_close(m3_hip_device *device);
+int m3_hip_device_properties(const m3_hip_device *device, char *name,
+                             size_t name_capacity, uint64_t *total_bytes,
+                             uint32_t *compute_units, char *message,
+                             size_t capacity);
+
+/* One hipMalloc of byte_count bytes (256-byte aligned). */
+int m3_hip_arena_reserve(m3_hip_device *device, size_t byte_count,
+                         void **base, char *message, size_t capacity);
+void m3_hip_arena_release(m3_hip_device *device, void *base);
+
+/* Stream-ordered copies. Both return once the host buffer may be reused
+ * (h2d) or holds the data (d2h). */
+int m3_hip_copy_h2d(m3_hip_device *device, void *device_destination,
+                    const void *host_source, size_t byte_count,
+                    char *message, size_t capacity);
+int m3_hip_copy_d2h(m3_hip_device *device, void *host_destination,
+                    const void *device_source, size_t byte_count,
+                    char *message, size_t capacity);
+/* Fills device memory with zero bytes using a kernel (no memset node). */
+int m3_hip_fill_zero(m3_hip_device *device, void *device_destination,
+                     size_t byte_count, char *message, size_t capacity);
+
+/* out = left (op) right with right-aligned broadcasting, computed in F32
+ * and rounded once to the output dtype. Inputs F32/F16/BF16, any strides;
+ * output contiguous; an output may alias an input of the same shape exactly. */
+int m3_hip_launch_binary(m3_hip_device *device, uint32_t op,
+                         const m3_hip_view *left, const m3_hip_view *right,
+                         const m3_hip_view *output, char *message,
+                         size_t capacity);
+/* Element conversion between any two of F32/F16/BF16/I32 (same dtype is a
+ * copy). Float to I32 truncates; callers scan the input first. */
+int m3_hip_launch_cast(m3_hip_device *device, const m3_hip_view *input,
+                       const m3_hip_view *output, char *message,
+                       size_t capacity);
+/* Byte copy of a strided input into a contiguous output of the same dtype. */
+int m3_hip_launch_copy(m3_hip_device *device, const m3_hip_view *input,
+                       const m3_hip_view *output, char *message,
+                       size_t capacity);
+/* Last-axis softmax of a float tensor without NaN. */
+int m3_hip_launch_softmax(m3_hip_device *device, const m3_hip_view *input,
+                          const m3_hip_view *output, char *message,
+                          size_t capacity);
+/* Snake1d on rank-3 F32: y = x + (1/(a+eps)) * sin(a*x)^2, a per channel. */
+int m3_hip_launch_snake1d(m3_hip_device *device, const m3_hip_view *input,
+                          const m3_hip_view *alpha,
+                          const m3_hip_view *output, char *message,
+                          size_t capacity);
+
+/* Scans view i for the condition kinds[i] (an m3_hip_scan_kind), waits, and
+ * writes flags[i] = 1 when view i holds an offending element, else 0. */
+int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
+                      const m3_hip_view *views, size_t count,
+                      uint32_t *flags, char *message, size_t capacity);
+
+/* Waits for all work on the device stream and reports any kernel error. */
+int m3_hip_synchronize(m3_hip_device *device, char *message,
+                       size_t capacity);
+
+/* Measurement support: when enabled, every launch is bracketed by HIP events
+ * on the device stream; m3_hip_timing_read synchronizes, folds completed
+ * event pairs into per-kernel totals, and copies up to `capacity` entries. */
+int m3_hip_timing_enable(m3_hip_device *device, int enabled);
+int m3_hip_timing_reset(m3_hip_device *device);
+int m3_hip_timing_read(m3_hip_device *device, m3_hip_kernel_time *entries,
+                       size_t capacity, size_t *count, char *message,
+                       size_t message_capacity);
+/* The device's hipStream_t, for callers that order their own work with it. */
+void *m3_hip_stream(m3_hip_device *device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

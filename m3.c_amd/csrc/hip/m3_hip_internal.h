@@ -1,0 +1,142 @@
+/*
+ * m3_hip_internal.h - state and helpers shared by the HIP translation units
+ * of the m3 execution provider (gfx950).
+ */
+#ifndef M3_HIP_INTERNAL_H
+#define M3_HIP_INTERNAL_H
+
+#include "m3_hip.h"
+#include "m3_numeric.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+/* One timed launch: events recorded around a kernel on the device stream. */
+struct m3_hip_pending_time {
+    const char *name;
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+
+struct m3_hip_time_total {
+    std::string name;
+    uint64_t launches;
+    double total_ms;
+};
+
+struct m3_hip_device {
+    int ordinal;
+    hipStream_t stream;
+    char name[256];
+    uint64_t total_bytes;
+    uint32_t compute_units;
+    /* device flags for data scans and their host mirror */
+    uint32_t *scan_flags;
+    size_t scan_capacity;
+    uint32_t *host_flags;
+    bool timing;
+    std::vector<m3_hip_pending_time> pending;
+    std::vector<hipEvent_t> spare_events;
+    std::vector<m3_hip_time_total> totals;
+};
+
+/* Writes a formatted message into a caller buffer (which may be NULL). */
+int m3_hip_fail(char *message, size_t capacity, int code, const char *format,
+                ...) __attribute__((format(printf, 4, 5)));
+/* Maps a HIP error to an m3_hip_code with a message naming `what`. */
+int m3_hip_check(hipError_t status, const char *what, char *message,
+                 size_t capacity);
+
+/* Timing bracket around one kernel launch (no-ops when timing is off). */
+int m3_hip_time_begin(m3_hip_device *device, const char *name,
+                      m3_hip_pending_time *slot);
+void m3_hip_time_end(m3_hip_device *device, m3_hip_pending_time *slot);
+
+/* Launch helper: records timing events, launches, checks the launch. */
+template <typename Launch>
+int m3_hip_launch(m3_hip_device *device, const char *name, Launch launch,
+                  char *message, size_t capacity)
+{
+    m3_hip_pending_time slot = {name, nullptr, nullptr};
+    int code = m3_hip_time_begin(device, name, &slot);
+
+    if (code != M3_HIP_OK) {
+        return m3_hip_fail(message, capacity, code,
+                           "cannot record timing events for %s", name);
+    }
+    launch();
+    hipError_t status = hipGetLastError();
+    m3_hip_time_end(device, &slot);
+    return m3_hip_check(status, name, message, capacity);
+}
+
+/* Unsigned 32-bit division by an invariant divisor d >= 1:
+ * q = (umulhi(n, mul) + n) >> shift with shift = ceil(log2 d) and
+ * mul = floor(2^32 (2^shift - d) / d) + 1; the sum is formed in 64 bits,
+ * so the quotient is exact for every 32-bit n. */
+struct m3_fast_div {
+    uint32_t divisor;
+    uint32_t mul;
+    uint32_t shift;
+};
+
+static inline m3_fast_div m3_fast_div_make(uint32_t divisor)
+{
+    m3_fast_div d;
+    uint32_t shift = 0U;
+
+    while (shift < 32U && (1ULL << shift) < divisor) {
+        ++shift;
+    }
+    d.divisor = divisor;
+    d.shift = shift;
+    d.mul = (uint32_t)((((1ULL << shift) - divisor) << 32U) / divisor + 1U);
+    return d;
+}
+
+__host__ __device__ __forceinline__ uint32_t m3_fast_div_q(m3_fast_div d,
+                                                          uint32_t n)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t hi = __umulhi(n, d.mul);
+#else
+    uint32_t hi = (uint32_t)(((uint64_t)n * d.mul) >> 32U);
+#endif
+    return (uint32_t)(((uint64_t)hi + n) >> d.shift);
+}
+
+/* Byte strides of an operand over the (coalesced) output index space. */
+struct m3_index_plan {
+    uint32_t rank;               /* coalesced rank, >= 1 */
+    uint64_t shape[M3_HIP_MAX_RANK];
+    int64_t strides[3][M3_HIP_MAX_RANK]; /* per operand, bytes */
+};
+
+/* Builds the output index space of `output` with the given operands mapped
+ * onto it by right-aligned broadcasting (a size-1 operand axis has stride
+ * 0), then merges adjacent axes that are contiguous for every operand and
+ * drops size-1 axes. operand_count <= 3; operand 0 is usually the output. */
+void m3_plan_index_space(const m3_hip_view *output,
+                         const m3_hip_view *const *operands,
+                         uint32_t operand_count, m3_index_plan *plan);
+
+bool m3_view_is_valid(const m3_hip_view *view);
+/* Row-major layout: every axis longer than one steps by the product of the
+ * inner extents times the element size. */
+bool m3_view_is_contiguous(const m3_hip_view *view);
+/* Every axis of `input`, right-aligned, is 1 or equals the output axis. */
+bool m3_view_broadcasts_to(const m3_hip_view *input,
+                           const m3_hip_view *output);
+size_t m3_dtype_bytes(uint32_t dtype);
+
+/* Number of blocks for a grid-stride loop over `items` work items with
+ * `threads` threads per block, capped at `per_cu` blocks per CU. */
+uint32_t m3_grid_blocks(const m3_hip_device *device, uint64_t items,
+                        uint32_t threads, uint32_t per_cu);
+
+#endif

@@ -1,0 +1,783 @@
+/*
+ * m3_hip_runtime.hip - device, stream, arena, copies, data scans and
+ * launch timing of the m3 HIP execution provider.
+ *
+ * One device handle owns one HIP stream (default priority). Every copy,
+ * fill, scan and kernel of the handle is ordered on that stream, which is
+ * what makes a command list execute in list order and lets
+ * m3_hip_synchronize stand for the reference's commit + wait
+ * (src/m3_backend_metal.m:189-216).
+ */
+#include "m3_hip_internal.h"
+
+#include <algorithm>
+#include <cstring>
+#include <new>
+
+int m3_hip_fail(char *message, size_t capacity, int code, const char *format,
+                ...)
+{
+    if (message != nullptr && capacity != 0U) {
+        va_list arguments;
+
+        va_start(arguments, format);
+        (void)vsnprintf(message, capacity, format, arguments);
+        va_end(arguments);
+        message[capacity - 1U] = '\0';
+    }
+    return code;
+}
+
+int m3_hip_check(hipError_t status, const char *what, char *message,
+                 size_t capacity)
+{
+    if (status == hipSuccess) {
+        return M3_HIP_OK;
+    }
+    return m3_hip_fail(message, capacity,
+                       status == hipErrorOutOfMemory ? M3_HIP_OUT_OF_MEMORY
+                       : status == hipErrorNoDevice  ? M3_HIP_NO_DEVICE
+                                                     : M3_HIP_RUNTIME,
+                       "%s failed: %s", what, hipGetErrorString(status));
+}
+
+size_t m3_dtype_bytes(uint32_t dtype)
+{
+    return dtype == M3_HIP_F16 || dtype == M3_HIP_BF16 ? 2U : 4U;
+}
+
+bool m3_view_is_valid(const m3_hip_view *view)
+{
+    uint64_t count = 1U;
+
+    if (view == nullptr || view->rank > M3_HIP_MAX_RANK ||
+        view->dtype > M3_HIP_I32) {
+        return false;
+    }
+    for (uint32_t axis = 0U; axis < view->rank; ++axis) {
+        count *= view->shape[axis];
+    }
+    return count == view->element_count &&
+           (count == 0U || view->base != nullptr);
+}
+
+bool m3_view_is_contiguous(const m3_hip_view *view)
+{
+    uint64_t expected = m3_dtype_bytes(view->dtype);
+
+    if (view->element_count == 0U) {
+        return true;
+    }
+    for (int axis = (int)view->rank - 1; axis >= 0; --axis) {
+        if (view->shape[axis] > 1U && view->byte_strides[axis] != expected) {
+            return false;
+        }
+        expected *= view->shape[axis];
+    }
+    return true;
+}
+
+bool m3_view_broadcasts_to(const m3_hip_view *input,
+                           const m3_hip_view *output)
+{
+    if (input->rank > output->rank) {
+        return false;
+    }
+    for (uint32_t axis = 0U; axis < input->rank; ++axis) {
+        uint64_t dim = input->shape[axis];
+        uint64_t target = output->shape[axis + output->rank - input->rank];
+
+        if (dim != 1U && dim != target) {
+            return false;
+        }
+    }
+    return true;
+}
+
+uint32_t m3_grid_blocks(const m3_hip_device *device, uint64_t items,
+                        uint32_t threads, uint32_t per_cu)
+{
+    uint64_t wanted = (items + threads - 1U) / threads;
+    uint64_t cap = (uint64_t)device->compute_units * per_cu;
+
+    if (wanted == 0U) {
+        wanted = 1U;
+    }
+    return (uint32_t)std::min<uint64_t>(wanted, cap);
+}
+
+void m3_plan_index_space(const m3_hip_view *output,
+                         const m3_hip_view *const *operands,
+                         uint32_t operand_count, m3_index_plan *plan)
+{
+    uint32_t rank = output->rank;
+    uint64_t shape[M3_HIP_MAX_RANK];
+    int64_t strides[3][M3_HIP_MAX_RANK];
+    uint32_t kept = 0U;
+
+    for (uint32_t axis = 0U; axis < rank; ++axis) {
+        shape[axis] = output->shape[axis];
+        for (uint32_t k = 0U; k < operand_count; ++k) {
+            const m3_hip_view *view = operands[k];
+            int view_axis = (int)axis - (int)(rank - view->rank);
+            bool present = view_axis >= 0 && view->shape[view_axis] != 1U;
+
+            strides[k][axis] =
+                present ? (int64_t)view->byte_strides[view_axis] : 0;
+        }
+    }
+    /* Drop size-1 axes, then merge an axis into its outer neighbour when
+     * every operand steps across the pair as one axis. */
+    std::memset(plan, 0, sizeof(*plan));
+    for (uint32_t axis = 0U; axis < rank; ++axis) {
+        if (shape[axis] == 1U) {
+            continue;
+        }
+        if (kept != 0U) {
+            bool mergeable = true;
+
+            for (uint32_t k = 0U; k < operand_count; ++k) {
+                if (plan->strides[k][kept - 1U] !=
+                    strides[k][axis] * (int64_t)shape[axis]) {
+                    mergeable = false;
+                    break;
+                }
+            }
+            if (mergeable) {
+                plan->shape[kept - 1U] *= shape[axis];
+                for (uint32_t k = 0U; k < operand_count; ++k) {
+                    plan->strides[k][kept - 1U] = strides[k][axis];
+                }
+                continue;
+            }
+        }
+        plan->shape[kept] = shape[axis];
+        for (uint32_t k = 0U; k < operand_count; ++k) {
+            plan->strides[k][kept] = strides[k][axis];
+        }
+        ++kept;
+    }
+    if (kept == 0U) {
+        plan->shape[0] = 1U;
+        kept = 1U;
+    }
+    plan->rank = kept;
+}
+
+/* ---- device lifetime ---------------------------------------------------- */
+
+extern "C" int m3_hip_device_count(int *count, char *message,
+                                   size_t capacity)
+{
+    int found = 0;
+    hipError_t status;
+
+    if (count == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "device count output is null");
+    }
+    *count = 0;
+    status = hipGetDeviceCount(&found);
+    if (status == hipErrorNoDevice || (status == hipSuccess && found == 0)) {
+        return M3_HIP_OK;
+    }
+    if (status != hipSuccess) {
+        return m3_hip_check(status, "hipGetDeviceCount", message, capacity);
+    }
+    *count = found;
+    return M3_HIP_OK;
+}
+
+extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
+                                  char *message, size_t capacity)
+{
+    hipDeviceProp_t properties;
+    m3_hip_device *device;
+    int count = 0;
+    int code;
+
+    if (device_output == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "device output is null");
+    }
+    *device_output = nullptr;
+    code = m3_hip_device_count(&count, message, capacity);
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    if (ordinal < 0 || ordinal >= count) {
+        return m3_hip_fail(message, capacity, M3_HIP_NO_DEVICE,
+                           "HIP device %d is not present (%d found)",
+                           ordinal, count);
+    }
+    code = m3_hip_check(hipSetDevice(ordinal), "hipSetDevice", message,
+                        capacity);
+    if (code == M3_HIP_OK) {
+        code = m3_hip_check(hipGetDeviceProperties(&properties, ordinal),
+                            "hipGetDeviceProperties", message, capacity);
+    }
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    device = new (std::nothrow) m3_hip_device();
+    if (device == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_OUT_OF_MEMORY,
+                           "cannot allocate HIP device state");
+    }
+    device->ordinal = ordinal;
+    std::snprintf(device->name, sizeof(device->name), "%s (%s)",
+                  properties.name, properties.gcnArchName);
+    device->total_bytes = (uint64_t)properties.totalGlobalMem;
+    device->compute_units = (uint32_t)properties.multiProcessorCount;
+    code = m3_hip_check(hipStreamCreateWithFlags(&device->stream,
+                                                 hipStreamNonBlocking),
+                        "hipStreamCreateWithFlags", message, capacity);
+    if (code == M3_HIP_OK) {
+        code = m3_hip_check(hipHostMalloc((void **)&device->host_flags,
+                                          64U * sizeof(uint32_t),
+                                          hipHostMallocDefault),
+                            "hipHostMalloc", message, capacity);
+    }
+    if (code != M3_HIP_OK) {
+        m3_hip_device_close(device);
+        return code;
+    }
+    *device_output = device;
+    return M3_HIP_OK;
+}
+
+extern "C" void m3_hip_device_close(m3_hip_device *device)
+{
+    if (device == nullptr) {
+        return;
+    }
+    (void)hipSetDevice(device->ordinal);
+    if (device->stream != nullptr) {
+        (void)hipStreamSynchronize(device->stream);
+    }
+    for (m3_hip_pending_time &slot : device->pending) {
+        (void)hipEventDestroy(slot.start);
+        (void)hipEventDestroy(slot.stop);
+    }
+    for (hipEvent_t event : device->spare_events) {
+        (void)hipEventDestroy(event);
+    }
+    if (device->scan_flags != nullptr) {
+        (void)hipFree(device->scan_flags);
+    }
+    if (device->host_flags != nullptr) {
+        (void)hipHostFree(device->host_flags);
+    }
+    if (device->stream != nullptr) {
+        (void)hipStreamDestroy(device->stream);
+    }
+    delete device;
+}
+
+extern "C" int m3_hip_device_properties(const m3_hip_device *device,
+                                        char *name, size_t name_capacity,
+                                        uint64_t *total_bytes,
+                                        uint32_t *compute_units,
+                                        char *message, size_t capacity)
+{
+    if (device == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "device is null");
+    }
+    if (name != nullptr && name_capacity != 0U) {
+        std::snprintf(name, name_capacity, "%s", device->name);
+    }
+    if (total_bytes != nullptr) {
+        *total_bytes = device->total_bytes;
+    }
+    if (compute_units != nullptr) {
+        *compute_units = device->compute_units;
+    }
+    return M3_HIP_OK;
+}
+
+extern "C" void *m3_hip_stream(m3_hip_device *device)
+{
+    return device == nullptr ? nullptr : (void *)device->stream;
+}
+
+/* ---- memory ------------------------------------------------------------- */
+
+__global__ void m3_fill_zero_kernel(uint4 *words, uint64_t word_count,
+                                    uint8_t *tail, uint32_t tail_bytes)
+{
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+         i < word_count; i += stride) {
+        words[i] = make_uint4(0U, 0U, 0U, 0U);
+    }
+    if (blockIdx.x == 0U && threadIdx.x < tail_bytes) {
+        tail[threadIdx.x] = 0U;
+    }
+}
+
+extern "C" int m3_hip_fill_zero(m3_hip_device *device,
+                                void *device_destination, size_t byte_count,
+                                char *message, size_t capacity)
+{
+    if (device == nullptr || (byte_count != 0U &&
+                              device_destination == nullptr)) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "fill destination is null");
+    }
+    if (byte_count == 0U) {
+        return M3_HIP_OK;
+    }
+    /* Leading bytes up to 16-byte alignment are folded into the tail
+     * handling by requiring aligned starts: arenas are 256-byte aligned. */
+    if (((uintptr_t)device_destination & 15U) != 0U) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "fill destination is not 16-byte aligned");
+    }
+    uint64_t words = byte_count / 16U;
+    uint32_t tail = (uint32_t)(byte_count % 16U);
+    uint8_t *tail_pointer = (uint8_t *)device_destination + words * 16U;
+    uint32_t blocks = m3_grid_blocks(device, words == 0U ? 1U : words, 256U,
+                                     8U);
+
+    return m3_hip_launch(
+        device, "m3_fill_zero",
+        [&]() {
+            hipLaunchKernelGGL(m3_fill_zero_kernel, dim3(blocks), dim3(256),
+                               0, device->stream, (uint4 *)device_destination,
+                               words, tail_pointer, tail);
+        },
+        message, capacity);
+}
+
+extern "C" int m3_hip_arena_reserve(m3_hip_device *device, size_t byte_count,
+                                    void **base, char *message,
+                                    size_t capacity)
+{
+    void *memory = nullptr;
+    int code;
+
+    if (device == nullptr || base == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "arena device and output are required");
+    }
+    *base = nullptr;
+    if (byte_count == 0U) {
+        return M3_HIP_OK;
+    }
+    code = m3_hip_check(hipMalloc(&memory, byte_count), "hipMalloc", message,
+                        capacity);
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    /* Fresh device memory is zeroed so that nothing reads stale bytes. */
+    code = m3_hip_fill_zero(device, memory, byte_count, message, capacity);
+    if (code != M3_HIP_OK) {
+        (void)hipFree(memory);
+        return code;
+    }
+    *base = memory;
+    return M3_HIP_OK;
+}
+
+extern "C" void m3_hip_arena_release(m3_hip_device *device, void *base)
+{
+    if (base == nullptr) {
+        return;
+    }
+    if (device != nullptr) {
+        (void)hipStreamSynchronize(device->stream);
+    }
+    (void)hipFree(base);
+}
+
+extern "C" int m3_hip_copy_h2d(m3_hip_device *device,
+                               void *device_destination,
+                               const void *host_source, size_t byte_count,
+                               char *message, size_t capacity)
+{
+    int code;
+
+    if (device == nullptr ||
+        (byte_count != 0U &&
+         (device_destination == nullptr || host_source == nullptr))) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "copy endpoints are required");
+    }
+    if (byte_count == 0U) {
+        return M3_HIP_OK;
+    }
+    code = m3_hip_check(hipMemcpyAsync(device_destination, host_source,
+                                       byte_count, hipMemcpyHostToDevice,
+                                       device->stream),
+                        "hipMemcpyAsync(host to device)", message, capacity);
+    if (code == M3_HIP_OK) {
+        code = m3_hip_check(hipStreamSynchronize(device->stream),
+                            "hipStreamSynchronize", message, capacity);
+    }
+    return code;
+}
+
+extern "C" int m3_hip_copy_d2h(m3_hip_device *device, void *host_destination,
+                               const void *device_source, size_t byte_count,
+                               char *message, size_t capacity)
+{
+    int code;
+
+    if (device == nullptr ||
+        (byte_count != 0U &&
+         (device_source == nullptr || host_destination == nullptr))) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "copy endpoints are required");
+    }
+    if (byte_count == 0U) {
+        return M3_HIP_OK;
+    }
+    code = m3_hip_check(hipMemcpyAsync(host_destination, device_source,
+                                       byte_count, hipMemcpyDeviceToHost,
+                                       device->stream),
+                        "hipMemcpyAsync(device to host)", message, capacity);
+    if (code == M3_HIP_OK) {
+        code = m3_hip_check(hipStreamSynchronize(device->stream),
+                            "hipStreamSynchronize", message, capacity);
+    }
+    return code;
+}
+
+extern "C" int m3_hip_synchronize(m3_hip_device *device, char *message,
+                                  size_t capacity)
+{
+    if (device == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "device is null");
+    }
+    return m3_hip_check(hipStreamSynchronize(device->stream),
+                        "hipStreamSynchronize", message, capacity);
+}
+
+/* ---- data scans (preflight) -------------------------------------------- */
+
+/* Strided element walk shared by the scans: element `flat` of a view whose
+ * (coalesced) index space is `plan`, operand 0. */
+struct m3_scan_args {
+    const uint8_t *base;
+    uint64_t count;
+    uint32_t rank;
+    uint32_t dtype;
+    uint32_t kind;
+    uint64_t shape[M3_HIP_MAX_RANK];
+    int64_t strides[M3_HIP_MAX_RANK];
+    uint32_t *flag;
+};
+
+__device__ __forceinline__ uint32_t m3_scan_load(const uint8_t *p,
+                                                 uint32_t dtype)
+{
+    uint32_t raw = dtype == M3N_F16 || dtype == M3N_BF16
+                       ? (uint32_t)*(const uint16_t *)p
+                       : *(const uint32_t *)p;
+
+    return m3_load_as_f32_bits(raw, dtype);
+}
+
+__device__ __forceinline__ bool m3_scan_offends(uint32_t bits, uint32_t kind)
+{
+    if (kind == M3_HIP_SCAN_NAN) {
+        return m3_f32_is_nan_bits(bits);
+    }
+    /* finite and -2^31 <= v < 2^31 */
+    float v = m3_bits_f32(bits);
+
+    return !((bits & 0x7f800000U) != 0x7f800000U && v >= -2147483648.0F &&
+             v < 2147483648.0F);
+}
+
+__global__ void m3_scan_kernel(m3_scan_args args)
+{
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    bool found = false;
+
+    for (uint64_t flat = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+         flat < args.count; flat += stride) {
+        uint64_t rest = flat;
+        int64_t offset = 0;
+
+        for (int axis = (int)args.rank - 1; axis >= 0; --axis) {
+            uint64_t dim = args.shape[axis];
+            uint64_t coordinate = rest % dim;
+
+            rest /= dim;
+            offset += (int64_t)coordinate * args.strides[axis];
+        }
+        found |= m3_scan_offends(m3_scan_load(args.base + offset, args.dtype),
+                                 args.kind);
+    }
+    if (__any(found) && found) {
+        atomicOr(args.flag, 1U);
+    }
+}
+
+/* Contiguous F32 scan: 16-byte loads. */
+__global__ void m3_scan_f32_contiguous_kernel(const uint4 *data,
+                                              uint64_t quads,
+                                              const uint32_t *tail,
+                                              uint32_t tail_count,
+                                              uint32_t kind, uint32_t *flag)
+{
+    uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    bool found = false;
+
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+         i < quads; i += stride) {
+        uint4 v = data[i];
+
+        found |= m3_scan_offends(v.x, kind) | m3_scan_offends(v.y, kind) |
+                 m3_scan_offends(v.z, kind) | m3_scan_offends(v.w, kind);
+    }
+    if (blockIdx.x == 0U && threadIdx.x < tail_count) {
+        found |= m3_scan_offends(tail[threadIdx.x], kind);
+    }
+    if (__any(found) && found) {
+        atomicOr(flag, 1U);
+    }
+}
+
+__global__ void m3_clear_flags_kernel(uint32_t *flags, uint32_t count)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+
+    if (i < count) {
+        flags[i] = 0U;
+    }
+}
+
+extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
+                                 const m3_hip_view *views, size_t count,
+                                 uint32_t *flags, char *message,
+                                 size_t capacity)
+{
+    int code;
+
+    if (device == nullptr || (count != 0U && (kinds == nullptr ||
+                                              views == nullptr ||
+                                              flags == nullptr))) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "scan arguments are incomplete");
+    }
+    if (count == 0U) {
+        return M3_HIP_OK;
+    }
+    if (count > 64U) {
+        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
+                           "at most 64 views can be scanned at once");
+    }
+    if (device->scan_capacity < count) {
+        if (device->scan_flags != nullptr) {
+            (void)hipFree(device->scan_flags);
+            device->scan_flags = nullptr;
+        }
+        code = m3_hip_check(hipMalloc((void **)&device->scan_flags,
+                                      64U * sizeof(uint32_t)),
+                            "hipMalloc(scan flags)", message, capacity);
+        if (code != M3_HIP_OK) {
+            device->scan_capacity = 0U;
+            return code;
+        }
+        device->scan_capacity = 64U;
+    }
+    code = m3_hip_launch(
+        device, "m3_clear_flags",
+        [&]() {
+            hipLaunchKernelGGL(m3_clear_flags_kernel, dim3(1), dim3(64), 0,
+                               device->stream, device->scan_flags,
+                               (uint32_t)count);
+        },
+        message, capacity);
+    for (size_t i = 0U; code == M3_HIP_OK && i < count; ++i) {
+        const m3_hip_view *view = &views[i];
+        uint32_t *flag = device->scan_flags + i;
+
+        if (!m3_view_is_valid(view) || kinds[i] > M3_HIP_SCAN_I32_RANGE) {
+            return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                               "scan view %zu is malformed", i);
+        }
+        if (view->element_count == 0U) {
+            continue;
+        }
+        const m3_hip_view *operands[1] = {view};
+        m3_index_plan plan;
+        const uint8_t *base = (const uint8_t *)view->base + view->byte_offset;
+
+        m3_plan_index_space(view, operands, 1U, &plan);
+        if (view->dtype == M3_HIP_F32 && plan.rank == 1U &&
+            plan.strides[0][0] == 4 && ((uintptr_t)base & 15U) == 0U) {
+            uint64_t quads = view->element_count / 4U;
+            uint32_t tail = (uint32_t)(view->element_count % 4U);
+            uint32_t blocks = m3_grid_blocks(device, quads == 0U ? 1U : quads,
+                                             256U, 8U);
+
+            code = m3_hip_launch(
+                device, "m3_scan_f32",
+                [&]() {
+                    hipLaunchKernelGGL(
+                        m3_scan_f32_contiguous_kernel, dim3(blocks),
+                        dim3(256), 0, device->stream, (const uint4 *)base,
+                        quads, (const uint32_t *)base + quads * 4U, tail,
+                        kinds[i], flag);
+                },
+                message, capacity);
+        } else {
+            m3_scan_args args;
+
+            std::memset(&args, 0, sizeof(args));
+            args.base = base;
+            args.count = view->element_count;
+            args.rank = plan.rank;
+            args.dtype = view->dtype;
+            args.kind = kinds[i];
+            args.flag = flag;
+            for (uint32_t axis = 0U; axis < plan.rank; ++axis) {
+                args.shape[axis] = plan.shape[axis];
+                args.strides[axis] = plan.strides[0][axis];
+            }
+            uint32_t blocks = m3_grid_blocks(device, view->element_count,
+                                             256U, 8U);
+
+            code = m3_hip_launch(
+                device, "m3_scan_strided",
+                [&]() {
+                    hipLaunchKernelGGL(m3_scan_kernel, dim3(blocks),
+                                       dim3(256), 0, device->stream, args);
+                },
+                message, capacity);
+        }
+    }
+    if (code == M3_HIP_OK) {
+        code = m3_hip_check(hipMemcpyAsync(device->host_flags,
+                                           device->scan_flags,
+                                           count * sizeof(uint32_t),
+                                           hipMemcpyDeviceToHost,
+                                           device->stream),
+                            "hipMemcpyAsync(scan flags)", message, capacity);
+    }
+    if (code == M3_HIP_OK) {
+        code = m3_hip_check(hipStreamSynchronize(device->stream),
+                            "hipStreamSynchronize", message, capacity);
+    }
+    if (code == M3_HIP_OK) {
+        std::memcpy(flags, device->host_flags, count * sizeof(uint32_t));
+    }
+    return code;
+}
+
+/* ---- timing ------------------------------------------------------------- */
+
+static int m3_hip_take_event(m3_hip_device *device, hipEvent_t *event)
+{
+    if (!device->spare_events.empty()) {
+        *event = device->spare_events.back();
+        device->spare_events.pop_back();
+        return M3_HIP_OK;
+    }
+    return hipEventCreate(event) == hipSuccess ? M3_HIP_OK : M3_HIP_RUNTIME;
+}
+
+int m3_hip_time_begin(m3_hip_device *device, const char *name,
+                      m3_hip_pending_time *slot)
+{
+    slot->name = name;
+    slot->start = nullptr;
+    slot->stop = nullptr;
+    if (!device->timing) {
+        return M3_HIP_OK;
+    }
+    if (m3_hip_take_event(device, &slot->start) != M3_HIP_OK ||
+        m3_hip_take_event(device, &slot->stop) != M3_HIP_OK) {
+        return M3_HIP_RUNTIME;
+    }
+    return hipEventRecord(slot->start, device->stream) == hipSuccess
+               ? M3_HIP_OK
+               : M3_HIP_RUNTIME;
+}
+
+void m3_hip_time_end(m3_hip_device *device, m3_hip_pending_time *slot)
+{
+    if (slot->start == nullptr) {
+        return;
+    }
+    (void)hipEventRecord(slot->stop, device->stream);
+    device->pending.push_back(*slot);
+}
+
+extern "C" int m3_hip_timing_enable(m3_hip_device *device, int enabled)
+{
+    if (device == nullptr) {
+        return M3_HIP_INVALID;
+    }
+    device->timing = enabled != 0;
+    return M3_HIP_OK;
+}
+
+static void m3_hip_fold_pending(m3_hip_device *device)
+{
+    for (m3_hip_pending_time &slot : device->pending) {
+        float ms = 0.0F;
+        bool found = false;
+
+        (void)hipEventElapsedTime(&ms, slot.start, slot.stop);
+        for (m3_hip_time_total &total : device->totals) {
+            if (total.name == slot.name) {
+                total.launches += 1U;
+                total.total_ms += ms;
+                found = true;
+                break;
+            }
+        }
+        if (!found) {
+            device->totals.push_back({slot.name, 1U, (double)ms});
+        }
+        device->spare_events.push_back(slot.start);
+        device->spare_events.push_back(slot.stop);
+    }
+    device->pending.clear();
+}
+
+extern "C" int m3_hip_timing_reset(m3_hip_device *device)
+{
+    if (device == nullptr) {
+        return M3_HIP_INVALID;
+    }
+    (void)hipStreamSynchronize(device->stream);
+    m3_hip_fold_pending(device);
+    device->totals.clear();
+    return M3_HIP_OK;
+}
+
+extern "C" int m3_hip_timing_read(m3_hip_device *device,
+                                  m3_hip_kernel_time *entries,
+                                  size_t capacity, size_t *count,
+                                  char *message, size_t message_capacity)
+{
+    int code;
+
+    if (device == nullptr || count == nullptr ||
+        (capacity != 0U && entries == nullptr)) {
+        return m3_hip_fail(message, message_capacity, M3_HIP_INVALID,
+                           "timing arguments are incomplete");
+    }
+    code = m3_hip_check(hipStreamSynchronize(device->stream),
+                        "hipStreamSynchronize", message, message_capacity);
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    m3_hip_fold_pending(device);
+    *count = device->totals.size();
+    for (size_t i = 0U; i < device->totals.size() && i < capacity; ++i) {
+        std::snprintf(entries[i].name, sizeof(entries[i].name), "%s",
+                      device->totals[i].name.c_str());
+        entries[i].launches = device->totals[i].launches;
+        entries[i].total_ms = device->totals[i].total_ms;
+    }
+    return M3_HIP_OK;
+}

@@ -1,0 +1,453 @@
+/*
+ * m3_hip_softmax.hip - last-axis softmax for gfx950, bit-exact with the
+ * CPU provider of the reference.
+ *
+ * Reference semantics (src/m3_op_execute_basic.c:124-180): per row
+ *   pass 1: maximum, and the count k of +inf entries;
+ *   pass 2: sum = ((0 + e0) + e1) + ... in F32, e_j = expf(v_j - max),
+ *           skipped when max is +-inf;
+ *   pass 3: p_j = e_j / sum; an all -inf row gives zeros; a row whose
+ *           maximum is +inf gives 1/k on its +inf entries and 0 elsewhere.
+ * Rounding is reproduced, not approximated:
+ *   - the maximum and k are order-independent, so they are reduced across
+ *     the 64 lanes of a wavefront;
+ *   - e_j uses m3_expf (the libm algorithm restated bit for bit);
+ *   - the sum keeps the reference's left-to-right F32 order: one lane per
+ *     row walks the row's e_j in LDS;
+ *   - p_j = RN_f32(e_j * RN_f64(1/sum)) equals the IEEE F32 quotient
+ *     e_j / sum for all floats e_j and sum >= 1 (a quotient of two floats
+ *     lies at least 2^-49 relative from any F32 rounding midpoint unless it
+ *     is one, which needs sum = 2^k where 1/sum is exact; the double
+ *     product errs by under 2^-52).
+ *
+ * Tiled kernel (rows contiguous along the last axis, uniform row stride,
+ * width <= 8192): a 256-thread workgroup owns a tile of rows; each wave
+ * owns rows w, w+4, ... of the tile; phase 1 loads a row with 16-byte
+ * accesses (8-byte for 16-bit dtypes), reduces max and k with cross-lane
+ * shuffles, and writes e_j to LDS; phase 2 has one lane per row sum its
+ * row in order from LDS and form 1/sum in double; phase 3 reads e_j back,
+ * scales, rounds to the output dtype and stores coalesced. LDS rows are
+ * padded by 4 floats so the per-row walks of phase 2 hit distinct banks.
+ * Any other layout runs one thread per row through the three passes.
+ */
+#include "m3_hip_internal.h"
+#include "m3_libm.h"
+
+#include <cstring>
+
+namespace {
+
+constexpr uint32_t kThreads = 256U;
+constexpr uint32_t kWaves = kThreads / 64U;
+constexpr uint32_t kLdsBudget = 65536U;
+constexpr uint32_t kMaxTileRows = 16U;
+constexpr uint32_t kMaxWidth = 8192U;
+constexpr uint32_t kPad = 4U;
+
+struct m3_softmax_args {
+    const uint8_t *input;
+    uint8_t *output;
+    uint64_t rows;
+    uint64_t row_stride; /* input bytes between rows */
+    uint32_t width;
+    uint32_t in_dtype;
+    uint32_t out_dtype;
+    uint32_t tile_rows;
+};
+
+__device__ __forceinline__ float m3_wave_max(float v)
+{
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        v = fmaxf(v, __shfl_xor(v, mask, 64));
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t m3_wave_sum(uint32_t v)
+{
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        v += __shfl_xor(v, mask, 64);
+    }
+    return v;
+}
+
+/* Four consecutive row elements starting at column c, as F32. */
+template <bool F32IO>
+__device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
+                                                   uint32_t c, uint32_t dtype)
+{
+    if (F32IO) {
+        return *(const float4 *)(row + (uint64_t)c * 4U);
+    }
+    uint2 h = *(const uint2 *)(row + (uint64_t)c * 2U);
+
+    return make_float4(
+        m3_bits_f32(m3_load_as_f32_bits(h.x & 0xffffU, dtype)),
+        m3_bits_f32(m3_load_as_f32_bits(h.x >> 16U, dtype)),
+        m3_bits_f32(m3_load_as_f32_bits(h.y & 0xffffU, dtype)),
+        m3_bits_f32(m3_load_as_f32_bits(h.y >> 16U, dtype)));
+}
+
+template <bool F32IO>
+__device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint32_t c,
+                                                  uint32_t dtype, float4 p)
+{
+    if (F32IO) {
+        *(float4 *)(row + (uint64_t)c * 4U) = p;
+        return;
+    }
+    uint2 packed;
+
+    packed.x = m3_store_from_f32_bits(m3_f32_bits(p.x), dtype) |
+               (m3_store_from_f32_bits(m3_f32_bits(p.y), dtype) << 16U);
+    packed.y = m3_store_from_f32_bits(m3_f32_bits(p.z), dtype) |
+               (m3_store_from_f32_bits(m3_f32_bits(p.w), dtype) << 16U);
+    *(uint2 *)(row + (uint64_t)c * 2U) = packed;
+}
+
+__device__ __forceinline__ float m3_softmax_scale(float e, double inverse)
+{
+    return (float)((double)e * inverse);
+}
+
+/* Per-row state shared through LDS between the phases. */
+struct m3_row_state {
+    float maximum;
+    uint32_t infinities;
+    double inverse;      /* 1/sum for finite rows */
+    float one_over_count; /* 1/k for rows whose maximum is +inf */
+    uint32_t pad;
+};
+
+template <bool F32IO>
+__global__ __launch_bounds__(256) void m3_softmax_tiled_kernel(
+    m3_softmax_args a)
+{
+    extern __shared__ float lds[];
+    __shared__ m3_row_state state[kMaxTileRows];
+    __shared__ uint64_t exp_table[32];
+    const uint32_t lane = threadIdx.x & 63U;
+    const uint32_t wave = threadIdx.x >> 6U;
+    const uint32_t width = a.width;
+    const uint32_t pitch = width + kPad;
+    const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
+    const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
+    const uint32_t out_size = out_dtype == M3N_F32 ? 4U : 2U;
+
+    if (threadIdx.x < 32U) {
+        exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
+    }
+    for (uint64_t tile = blockIdx.x; tile * a.tile_rows < a.rows;
+         tile += gridDim.x) {
+        const uint64_t first_row = tile * a.tile_rows;
+        const uint32_t tile_rows =
+            (uint32_t)min((uint64_t)a.tile_rows, a.rows - first_row);
+
+        __syncthreads();
+        /* Phase 1: max, +inf count and e_j for each row of this wave. */
+        for (uint32_t r = wave; r < tile_rows; r += kWaves) {
+            const uint8_t *row = a.input + (first_row + r) * a.row_stride;
+            float *line = lds + (uint64_t)r * pitch;
+            float maximum = -INFINITY;
+            uint32_t infinities = 0U;
+
+            for (uint32_t c = lane * 4U; c < width; c += 256U) {
+                float4 v = m3_softmax_load4<F32IO>(row, c, in_dtype);
+
+                maximum = fmaxf(maximum, fmaxf(fmaxf(v.x, v.y),
+                                               fmaxf(v.z, v.w)));
+                infinities += (v.x == INFINITY) + (v.y == INFINITY) +
+                              (v.z == INFINITY) + (v.w == INFINITY);
+                *(float4 *)(line + c) = v;
+            }
+            maximum = m3_wave_max(maximum);
+            infinities = m3_wave_sum(infinities);
+            if (maximum != INFINITY && maximum != -INFINITY) {
+                for (uint32_t c = lane * 4U; c < width; c += 256U) {
+                    float4 v = *(float4 *)(line + c);
+                    float4 e;
+
+                    e.x = m3_expf_with_table(v.x - maximum, exp_table);
+                    e.y = m3_expf_with_table(v.y - maximum, exp_table);
+                    e.z = m3_expf_with_table(v.z - maximum, exp_table);
+                    e.w = m3_expf_with_table(v.w - maximum, exp_table);
+                    *(float4 *)(line + c) = e;
+                }
+            }
+            if (lane == 0U) {
+                state[r].maximum = maximum;
+                state[r].infinities = infinities;
+            }
+        }
+        __syncthreads();
+        /* Phase 2: the reference's left-to-right F32 sum, one lane per row. */
+        if (threadIdx.x < tile_rows) {
+            m3_row_state *s = &state[threadIdx.x];
+            float maximum = s->maximum;
+
+            if (maximum != INFINITY && maximum != -INFINITY) {
+                const float *line = lds + (uint64_t)threadIdx.x * pitch;
+                float sum = 0.0F;
+
+                for (uint32_t c = 0U; c < width; c += 4U) {
+                    float4 e = *(const float4 *)(line + c);
+
+                    sum = sum + e.x;
+                    sum = sum + e.y;
+                    sum = sum + e.z;
+                    sum = sum + e.w;
+                }
+                s->inverse = 1.0 / (double)sum;
+            } else if (maximum == INFINITY) {
+                s->one_over_count = 1.0F / (float)s->infinities;
+            }
+        }
+        __syncthreads();
+        /* Phase 3: scale, round to the output dtype, store. */
+        for (uint32_t r = wave; r < tile_rows; r += kWaves) {
+            const float *line = lds + (uint64_t)r * pitch;
+            uint8_t *out = a.output + (first_row + r) * (uint64_t)width *
+                                          out_size;
+            const m3_row_state s = state[r];
+
+            for (uint32_t c = lane * 4U; c < width; c += 256U) {
+                float4 v = *(const float4 *)(line + c);
+                float4 p;
+
+                if (s.maximum == -INFINITY) {
+                    p = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+                } else if (s.maximum == INFINITY) {
+                    p.x = v.x == INFINITY ? s.one_over_count : 0.0F;
+                    p.y = v.y == INFINITY ? s.one_over_count : 0.0F;
+                    p.z = v.z == INFINITY ? s.one_over_count : 0.0F;
+                    p.w = v.w == INFINITY ? s.one_over_count : 0.0F;
+                } else {
+                    p.x = m3_softmax_scale(v.x, s.inverse);
+                    p.y = m3_softmax_scale(v.y, s.inverse);
+                    p.z = m3_softmax_scale(v.z, s.inverse);
+                    p.w = m3_softmax_scale(v.w, s.inverse);
+                }
+                m3_softmax_store4<F32IO>(out, c, out_dtype, p);
+            }
+        }
+    }
+}
+
+struct m3_softmax_general_args {
+    const uint8_t *input;
+    uint8_t *output;
+    uint64_t rows;
+    uint32_t width;
+    uint32_t in_dtype;
+    uint32_t out_dtype;
+    uint32_t outer_rank;
+    int64_t column_stride;
+    uint64_t outer_shape[M3_HIP_MAX_RANK];
+    int64_t outer_strides[M3_HIP_MAX_RANK];
+};
+
+__device__ __forceinline__ float m3_general_load(const uint8_t *p,
+                                                 uint32_t dtype)
+{
+    uint32_t raw = dtype == M3N_F32 ? *(const uint32_t *)p
+                                    : (uint32_t) * (const uint16_t *)p;
+
+    return m3_bits_f32(m3_load_as_f32_bits(raw, dtype));
+}
+
+/* One thread per row: the reference's three passes over a strided row. */
+__global__ __launch_bounds__(64) void m3_softmax_general_kernel(
+    m3_softmax_general_args a)
+{
+    const uint32_t out_size = a.out_dtype == M3N_F32 ? 4U : 2U;
+    const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
+
+    for (uint64_t row = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+         row < a.rows; row += step) {
+        uint64_t rest = row;
+        int64_t base = 0;
+        float maximum = -INFINITY;
+        float sum = 0.0F;
+        uint32_t infinities = 0U;
+
+        for (int axis = (int)a.outer_rank - 1; axis >= 0; --axis) {
+            uint64_t dim = a.outer_shape[axis];
+            uint64_t q = rest / dim;
+
+            base += (int64_t)(rest - q * dim) * a.outer_strides[axis];
+            rest = q;
+        }
+        const uint8_t *in = a.input + base;
+        uint8_t *out = a.output + row * a.width * out_size;
+
+        for (uint32_t c = 0U; c < a.width; ++c) {
+            float v = m3_general_load(in + (int64_t)c * a.column_stride,
+                                      a.in_dtype);
+
+            maximum = v > maximum ? v : maximum;
+            infinities += v == INFINITY;
+        }
+        if (maximum != INFINITY && maximum != -INFINITY) {
+            for (uint32_t c = 0U; c < a.width; ++c) {
+                float v = m3_general_load(in + (int64_t)c * a.column_stride,
+                                          a.in_dtype);
+
+                sum = sum + m3_expf(v - maximum);
+            }
+        }
+        double inverse = 1.0 / (double)sum;
+        float one_over_count = 1.0F / (float)infinities;
+
+        for (uint32_t c = 0U; c < a.width; ++c) {
+            float v = m3_general_load(in + (int64_t)c * a.column_stride,
+                                      a.in_dtype);
+            float p;
+
+            if (maximum == -INFINITY) {
+                p = 0.0F;
+            } else if (maximum == INFINITY) {
+                p = v == INFINITY ? one_over_count : 0.0F;
+            } else {
+                p = m3_softmax_scale(m3_expf(v - maximum), inverse);
+            }
+            uint32_t raw = m3_store_from_f32_bits(m3_f32_bits(p),
+                                                  a.out_dtype);
+
+            if (out_size == 4U) {
+                *(uint32_t *)(out + (uint64_t)c * 4U) = raw;
+            } else {
+                *(uint16_t *)(out + (uint64_t)c * 2U) = (uint16_t)raw;
+            }
+        }
+    }
+}
+
+} // namespace
+
+extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
+                                     const m3_hip_view *input,
+                                     const m3_hip_view *output,
+                                     char *message, size_t capacity)
+{
+    if (device == nullptr || !m3_view_is_valid(input) ||
+        !m3_view_is_valid(output) || input->rank == 0U ||
+        input->rank != output->rank || input->dtype == M3_HIP_I32 ||
+        output->dtype == M3_HIP_I32 || !m3_view_is_contiguous(output)) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "softmax launch arguments are malformed");
+    }
+    for (uint32_t axis = 0U; axis < input->rank; ++axis) {
+        if (input->shape[axis] != output->shape[axis]) {
+            return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                               "softmax input and output shapes differ");
+        }
+    }
+    uint64_t width = input->shape[input->rank - 1U];
+
+    if (width == 0U) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "softmax last axis must be nonempty");
+    }
+    if (output->element_count == 0U) {
+        return M3_HIP_OK;
+    }
+    uint64_t rows = input->element_count / width;
+    const uint8_t *in = (const uint8_t *)input->base + input->byte_offset;
+    uint8_t *out = (uint8_t *)output->base + output->byte_offset;
+    uint32_t in_size = (uint32_t)m3_dtype_bytes(input->dtype);
+    uint32_t out_size = (uint32_t)m3_dtype_bytes(output->dtype);
+
+    /* Outer axes (all but the last) of the input, coalesced. */
+    m3_hip_view outer = *input;
+    m3_index_plan plan;
+    const m3_hip_view *operands[1] = {&outer};
+
+    outer.rank = input->rank - 1U;
+    m3_plan_index_space(&outer, operands, 1U, &plan);
+
+    bool uniform_rows = plan.rank == 1U;
+    uint64_t row_stride = uniform_rows ? (uint64_t)plan.strides[0][0] : 0U;
+    bool columns_contiguous =
+        width == 1U ||
+        input->byte_strides[input->rank - 1U] == (uint64_t)in_size;
+
+    if (rows == 1U) {
+        uniform_rows = true;
+        row_stride = 0U;
+    }
+    if (uniform_rows && columns_contiguous && width % 4U == 0U &&
+        width <= kMaxWidth && row_stride % (4U * in_size) == 0U &&
+        ((uintptr_t)in % (4U * in_size)) == 0U &&
+        ((uintptr_t)out % (4U * out_size)) == 0U &&
+        plan.strides[0][0] >= 0) {
+        m3_softmax_args args;
+        uint32_t pitch_bytes = ((uint32_t)width + kPad) * 4U;
+        uint32_t tile_rows = kLdsBudget / pitch_bytes;
+
+        tile_rows = tile_rows > kMaxTileRows ? kMaxTileRows : tile_rows;
+        tile_rows = tile_rows == 0U ? 1U : tile_rows;
+        std::memset(&args, 0, sizeof(args));
+        args.input = in;
+        args.output = out;
+        args.rows = rows;
+        args.row_stride = row_stride;
+        args.width = (uint32_t)width;
+        args.in_dtype = input->dtype;
+        args.out_dtype = output->dtype;
+        args.tile_rows = tile_rows;
+        uint64_t tiles = (rows + tile_rows - 1U) / tile_rows;
+        uint32_t blocks = (uint32_t)(tiles < (uint64_t)device->compute_units *
+                                                 8U
+                                         ? tiles
+                                         : (uint64_t)device->compute_units *
+                                               8U);
+        size_t lds_bytes = (size_t)tile_rows * pitch_bytes;
+        bool f32 = input->dtype == M3_HIP_F32 && output->dtype == M3_HIP_F32;
+
+        return m3_hip_launch(
+            device, "m3_softmax_rows",
+            [&]() {
+                if (f32) {
+                    hipLaunchKernelGGL((m3_softmax_tiled_kernel<true>),
+                                       dim3(blocks), dim3(kThreads),
+                                       lds_bytes, device->stream, args);
+                } else {
+                    hipLaunchKernelGGL((m3_softmax_tiled_kernel<false>),
+                                       dim3(blocks), dim3(kThreads),
+                                       lds_bytes, device->stream, args);
+                }
+            },
+            message, capacity);
+    }
+
+    m3_softmax_general_args general;
+
+    std::memset(&general, 0, sizeof(general));
+    general.input = in;
+    general.output = out;
+    general.rows = rows;
+    general.width = (uint32_t)width;
+    general.in_dtype = input->dtype;
+    general.out_dtype = output->dtype;
+    general.column_stride = (int64_t)input->byte_strides[input->rank - 1U];
+    general.outer_rank = plan.rank;
+    for (uint32_t axis = 0U; axis < plan.rank; ++axis) {
+        general.outer_shape[axis] = plan.shape[axis];
+        general.outer_strides[axis] = plan.strides[0][axis];
+    }
+    if (width > 0xffffffffULL) {
+        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
+                           "softmax rows longer than 2^32 are unsupported");
+    }
+    uint32_t blocks = m3_grid_blocks(device, rows, 64U, 16U);
+
+    return m3_hip_launch(
+        device, "m3_softmax_rows_strided",
+        [&]() {
+            hipLaunchKernelGGL(m3_softmax_general_kernel, dim3(blocks),
+                               dim3(64), 0, device->stream, general);
+        },
+        message, capacity);
+}

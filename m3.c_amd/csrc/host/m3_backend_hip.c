@@ -1,0 +1,485 @@
+/*
+ * m3_backend_hip.c - the HIP execution provider as an m3 backend.
+ *
+ * Takes the place of the Metal backend of the reference
+ * (src/m3_backend_metal.m); written in C11 against the backend vtable and
+ * the thin C ABI of m3_hip.h.
+ *
+ * Storage. The session compiler reserves one arena (one hipMalloc) sized
+ * for all of its slots and every slot is carved from it at 256-byte
+ * alignment; allocations made without a reserved arena, or beyond it, get
+ * their own hipMalloc. Device memory is zeroed when obtained. Storage is
+ * not host-visible: m3_storage_write/read become stream-ordered copies.
+ *
+ * Execution of a command list (reference: m3_metal_execute_in_pool,
+ * src/m3_backend_metal.m:178-217, and m3_metal_preflight_basic,
+ * src/m3_backend_metal_basic.m:274-302). The list is atomic with respect
+ * to data checks: before any kernel is enqueued,
+ *   1. a SOFTMAX, or a CAST from a float dtype to I32, whose input storage
+ *      is written by an earlier command of the same list is rejected with
+ *      M3_STATUS_UNSUPPORTED (the data would only exist after commit);
+ *   2. the remaining such inputs are scanned on the device (NaN for
+ *      SOFTMAX, finite and inside [-2^31, 2^31) for the cast) with one
+ *      flag readback for the whole list;
+ * and the first command in list order that fails either check decides the
+ * status (OUT_OF_RANGE for data), with no output modified. Then every
+ * command is enqueued in order on the device stream and the list waits
+ * once at the end.
+ */
+#include "m3_internal.h"
+
+#include "m3_hip.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define M3_HIP_ARENA_ALIGNMENT 256U
+#define M3_HIP_MAX_ARENAS 16U
+#define M3_HIP_MESSAGE 256U
+
+typedef struct {
+    uint8_t *base;
+    size_t size;
+    size_t used;
+} m3_hip_arena;
+
+typedef struct {
+    m3_hip_device *device;
+    m3_hip_arena arenas[M3_HIP_MAX_ARENAS];
+    size_t arena_count;
+    /* per-list preflight buffers, grown on demand */
+    m3_hip_view *scan_views;
+    uint32_t *scan_kinds;
+    uint32_t *scan_flags;
+    size_t *scan_commands;
+    size_t scan_capacity;
+} m3_hip_backend_context;
+
+static m3_status m3_hip_status(int code, const char *message,
+                               m3_error *error)
+{
+    switch (code) {
+    case M3_HIP_OK:
+        return M3_STATUS_OK;
+    case M3_HIP_NO_DEVICE:
+    case M3_HIP_UNSUPPORTED:
+        return m3_error_set(error, M3_STATUS_UNSUPPORTED, "%s", message);
+    case M3_HIP_OUT_OF_MEMORY:
+        return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY, "%s", message);
+    default:
+        return m3_error_set(error, M3_STATUS_INTERNAL, "%s", message);
+    }
+}
+
+static void m3_hip_destroy(void *opaque)
+{
+    m3_hip_backend_context *context = opaque;
+    size_t i;
+
+    for (i = 0U; i < context->arena_count; ++i) {
+        m3_hip_arena_release(context->device, context->arenas[i].base);
+    }
+    m3_hip_device_close(context->device);
+    free(context->scan_views);
+    free(context->scan_kinds);
+    free(context->scan_flags);
+    free(context->scan_commands);
+    free(context);
+}
+
+static m3_status m3_hip_reserve(void *opaque, size_t byte_count,
+                                m3_error *error)
+{
+    m3_hip_backend_context *context = opaque;
+    char message[M3_HIP_MESSAGE] = "";
+    void *base = NULL;
+    int code;
+
+    if (context->arena_count == M3_HIP_MAX_ARENAS) {
+        return m3_error_set(error, M3_STATUS_OUT_OF_RANGE,
+                            "HIP backend arena table is full");
+    }
+    code = m3_hip_arena_reserve(context->device, byte_count, &base, message,
+                                sizeof(message));
+    if (code != M3_HIP_OK) {
+        return m3_hip_status(code, message, error);
+    }
+    context->arenas[context->arena_count].base = base;
+    context->arenas[context->arena_count].size = byte_count;
+    context->arenas[context->arena_count].used = 0U;
+    context->arena_count += 1U;
+    m3_error_reset(error);
+    return M3_STATUS_OK;
+}
+
+/* handle: NULL for storage carved from an arena, else the hipMalloc base. */
+static m3_status m3_hip_allocate(void *opaque, size_t byte_count,
+                                 size_t alignment, void **handle, void **data,
+                                 m3_error *error)
+{
+    m3_hip_backend_context *context = opaque;
+    size_t granule = alignment > M3_HIP_ARENA_ALIGNMENT
+                         ? alignment
+                         : M3_HIP_ARENA_ALIGNMENT;
+    char message[M3_HIP_MESSAGE] = "";
+    void *base = NULL;
+    int code;
+
+    *handle = NULL;
+    *data = NULL;
+    if (byte_count == 0U) {
+        return M3_STATUS_OK;
+    }
+    if (context->arena_count != 0U) {
+        m3_hip_arena *arena = &context->arenas[context->arena_count - 1U];
+        size_t start = (arena->used + granule - 1U) & ~(granule - 1U);
+
+        if (start >= arena->used && start <= arena->size &&
+            byte_count <= arena->size - start) {
+            arena->used = start + byte_count;
+            *data = arena->base + start;
+            return M3_STATUS_OK;
+        }
+    }
+    code = m3_hip_arena_reserve(context->device, byte_count, &base, message,
+                                sizeof(message));
+    if (code != M3_HIP_OK) {
+        return m3_hip_status(code, message, error);
+    }
+    *handle = base;
+    *data = base;
+    return M3_STATUS_OK;
+}
+
+static void m3_hip_free_storage(void *opaque, void *handle, void *data)
+{
+    m3_hip_backend_context *context = opaque;
+
+    (void)data;
+    if (handle != NULL) {
+        m3_hip_arena_release(context->device, handle);
+    }
+}
+
+static m3_status m3_hip_write(void *opaque, void *data, size_t byte_offset,
+                              const void *source, size_t byte_count,
+                              m3_error *error)
+{
+    m3_hip_backend_context *context = opaque;
+    char message[M3_HIP_MESSAGE] = "";
+    int code = m3_hip_copy_h2d(context->device, (uint8_t *)data + byte_offset,
+                               source, byte_count, message, sizeof(message));
+
+    return code == M3_HIP_OK ? M3_STATUS_OK
+                             : m3_hip_status(code, message, error);
+}
+
+static m3_status m3_hip_read(void *opaque, const void *data,
+                             size_t byte_offset, void *destination,
+                             size_t byte_count, m3_error *error)
+{
+    m3_hip_backend_context *context = opaque;
+    char message[M3_HIP_MESSAGE] = "";
+    int code = m3_hip_copy_d2h(context->device, destination,
+                               (const uint8_t *)data + byte_offset,
+                               byte_count, message, sizeof(message));
+
+    return code == M3_HIP_OK ? M3_STATUS_OK
+                             : m3_hip_status(code, message, error);
+}
+
+static void m3_hip_view_of(const m3_tensor_view *view, m3_hip_view *out)
+{
+    uint8_t axis;
+
+    (void)memset(out, 0, sizeof(*out));
+    out->base = m3_storage_device_data(view->storage);
+    out->byte_offset = (uint64_t)view->byte_offset;
+    out->element_count = (uint64_t)view->metadata.element_count;
+    out->rank = view->metadata.rank;
+    out->dtype = (uint32_t)view->metadata.dtype;
+    for (axis = 0U; axis < view->metadata.rank; ++axis) {
+        out->shape[axis] = view->metadata.shape[axis];
+        out->byte_strides[axis] = (uint64_t)view->byte_strides[axis];
+    }
+}
+
+/* Input view that must pass a data check before the list runs, else NULL;
+ * *kind receives the scan kind. */
+static const m3_tensor_view *m3_hip_checked_input(const m3_command *command,
+                                                  uint32_t *kind)
+{
+    if (command->kind == M3_OP_SOFTMAX) {
+        *kind = M3_HIP_SCAN_NAN;
+        return command->descriptor.softmax.input;
+    }
+    if (command->kind == M3_OP_CAST &&
+        command->descriptor.cast.output->metadata.dtype == M3_DTYPE_I32 &&
+        command->descriptor.cast.input->metadata.dtype != M3_DTYPE_I32) {
+        *kind = M3_HIP_SCAN_I32_RANGE;
+        return command->descriptor.cast.input;
+    }
+    return NULL;
+}
+
+static bool m3_hip_written_before(const m3_command *commands, size_t index,
+                                  const m3_storage *storage)
+{
+    size_t i;
+
+    for (i = 0U; i < index; ++i) {
+        const m3_tensor_view *output = m3_op_output_of(&commands[i]);
+
+        if (output != NULL && output->storage == storage) {
+            return true;
+        }
+    }
+    return false;
+}
+
+static m3_status m3_hip_grow_scans(m3_hip_backend_context *context,
+                                   size_t count, m3_error *error)
+{
+    m3_hip_view *views;
+    uint32_t *kinds;
+    uint32_t *flags;
+    size_t *commands;
+
+    if (count <= context->scan_capacity) {
+        return M3_STATUS_OK;
+    }
+    views = realloc(context->scan_views, count * sizeof(*views));
+    if (views != NULL) {
+        context->scan_views = views;
+    }
+    kinds = realloc(context->scan_kinds, count * sizeof(*kinds));
+    if (kinds != NULL) {
+        context->scan_kinds = kinds;
+    }
+    flags = realloc(context->scan_flags, count * sizeof(*flags));
+    if (flags != NULL) {
+        context->scan_flags = flags;
+    }
+    commands = realloc(context->scan_commands, count * sizeof(*commands));
+    if (commands != NULL) {
+        context->scan_commands = commands;
+    }
+    if (views == NULL || kinds == NULL || flags == NULL || commands == NULL) {
+        return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY,
+                            "cannot grow HIP preflight state");
+    }
+    context->scan_capacity = count;
+    return M3_STATUS_OK;
+}
+
+static m3_status m3_hip_preflight(m3_hip_backend_context *context,
+                                  const m3_command *commands, size_t count,
+                                  m3_error *error)
+{
+    size_t rejected = SIZE_MAX; /* first producer-dependent check */
+    size_t scans = 0U;
+    size_t i;
+    m3_status status;
+
+    for (i = 0U; i < count; ++i) {
+        uint32_t kind = 0U;
+        const m3_tensor_view *input = m3_hip_checked_input(&commands[i],
+                                                           &kind);
+
+        if (input == NULL) {
+            continue;
+        }
+        if (m3_hip_written_before(commands, i, input->storage)) {
+            rejected = i;
+            break;
+        }
+        if (input->metadata.element_count == 0U) {
+            continue;
+        }
+        status = m3_hip_grow_scans(context, scans + 1U, error);
+        if (status != M3_STATUS_OK) {
+            return status;
+        }
+        m3_hip_view_of(input, &context->scan_views[scans]);
+        context->scan_kinds[scans] = kind;
+        context->scan_commands[scans] = i;
+        scans += 1U;
+    }
+    for (i = 0U; i < scans; i += 64U) {
+        char message[M3_HIP_MESSAGE] = "";
+        size_t batch = scans - i < 64U ? scans - i : 64U;
+        int code = m3_hip_scan_views(context->device, &context->scan_kinds[i],
+                                     &context->scan_views[i], batch,
+                                     &context->scan_flags[i], message,
+                                     sizeof(message));
+
+        if (code != M3_HIP_OK) {
+            return m3_hip_status(code, message, error);
+        }
+    }
+    for (i = 0U; i < scans; ++i) {
+        if (context->scan_flags[i] != 0U) {
+            if (context->scan_commands[i] > rejected) {
+                break;
+            }
+            return m3_error_set(
+                error, M3_STATUS_OUT_OF_RANGE,
+                context->scan_kinds[i] == M3_HIP_SCAN_NAN
+                    ? "softmax input contains NaN"
+                    : "float-to-I32 cast value is invalid");
+        }
+    }
+    if (rejected != SIZE_MAX) {
+        return m3_error_set(error, M3_STATUS_UNSUPPORTED,
+                            commands[rejected].kind == M3_OP_CAST
+                                ? "HIP float-to-I32 cast depends on an "
+                                  "earlier output"
+                                : "HIP softmax depends on an earlier "
+                                  "output");
+    }
+    return M3_STATUS_OK;
+}
+
+static int m3_hip_enqueue(m3_hip_backend_context *context,
+                          const m3_command *command, char *message,
+                          size_t capacity)
+{
+    const m3_op_binary *binary = m3_op_binary_of(command);
+    m3_hip_view a;
+    m3_hip_view b;
+    m3_hip_view c;
+
+    if (binary != NULL) {
+        static const uint32_t ops[] = {M3_HIP_ADD, M3_HIP_MUL, M3_HIP_SUB,
+                                       M3_HIP_DIV};
+        uint32_t op = command->kind == M3_OP_ADD   ? ops[0]
+                      : command->kind == M3_OP_MUL ? ops[1]
+                      : command->kind == M3_OP_SUB ? ops[2]
+                                                   : ops[3];
+
+        m3_hip_view_of(binary->left, &a);
+        m3_hip_view_of(binary->right, &b);
+        m3_hip_view_of(binary->output, &c);
+        return m3_hip_launch_binary(context->device, op, &a, &b, &c, message,
+                                    capacity);
+    }
+    switch (command->kind) {
+    case M3_OP_COPY:
+        m3_hip_view_of(command->descriptor.copy.input, &a);
+        m3_hip_view_of(command->descriptor.copy.output, &c);
+        return m3_hip_launch_copy(context->device, &a, &c, message,
+                                  capacity);
+    case M3_OP_CAST:
+        m3_hip_view_of(command->descriptor.cast.input, &a);
+        m3_hip_view_of(command->descriptor.cast.output, &c);
+        return m3_hip_launch_cast(context->device, &a, &c, message,
+                                  capacity);
+    case M3_OP_SOFTMAX:
+        m3_hip_view_of(command->descriptor.softmax.input, &a);
+        m3_hip_view_of(command->descriptor.softmax.output, &c);
+        return m3_hip_launch_softmax(context->device, &a, &c, message,
+                                     capacity);
+    case M3_OP_SNAKE1D:
+        m3_hip_view_of(command->descriptor.snake1d.input, &a);
+        m3_hip_view_of(command->descriptor.snake1d.alpha, &b);
+        m3_hip_view_of(command->descriptor.snake1d.output, &c);
+        return m3_hip_launch_snake1d(context->device, &a, &b, &c, message,
+                                     capacity);
+    default:
+        (void)snprintf(message, capacity,
+                       "HIP does not implement operation %d",
+                       (int)command->kind);
+        return M3_HIP_UNSUPPORTED;
+    }
+}
+
+static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
+                                size_t count, m3_scratch_arena *scratch,
+                                m3_error *error)
+{
+    m3_hip_backend_context *context = opaque;
+    char message[M3_HIP_MESSAGE] = "";
+    m3_status status;
+    size_t i;
+    int code = M3_HIP_OK;
+
+    (void)scratch;
+    status = m3_hip_preflight(context, commands, count, error);
+    if (status != M3_STATUS_OK) {
+        return status;
+    }
+    for (i = 0U; i < count && code == M3_HIP_OK; ++i) {
+        code = m3_hip_enqueue(context, &commands[i], message,
+                              sizeof(message));
+    }
+    if (code == M3_HIP_OK) {
+        code = m3_hip_synchronize(context->device, message, sizeof(message));
+    } else {
+        (void)m3_hip_synchronize(context->device, NULL, 0U);
+    }
+    return m3_hip_status(code, message, error);
+}
+
+m3_status m3_backend_create_hip(m3_backend **backend, m3_error *error)
+{
+    static const m3_backend_vtable vtable = {
+        m3_hip_destroy, m3_hip_allocate, m3_hip_free_storage, m3_hip_execute,
+        m3_hip_write,   m3_hip_read,     m3_hip_reserve};
+    m3_hip_backend_context *context;
+    m3_backend_info info;
+    char message[M3_HIP_MESSAGE] = "";
+    uint64_t total = 0U;
+    uint32_t units = 0U;
+    m3_status status;
+    int code;
+
+    if (backend == NULL) {
+        return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
+                            "HIP backend output is null");
+    }
+    *backend = NULL;
+    context = calloc(1U, sizeof(*context));
+    if (context == NULL) {
+        return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY,
+                            "cannot allocate HIP backend context");
+    }
+    code = m3_hip_device_open(0, &context->device, message, sizeof(message));
+    if (code != M3_HIP_OK) {
+        free(context);
+        return m3_hip_status(code, message, error);
+    }
+    (void)memset(&info, 0, sizeof(info));
+    code = m3_hip_device_properties(context->device, info.name,
+                                    sizeof(info.name), &total, &units,
+                                    message, sizeof(message));
+    if (code != M3_HIP_OK) {
+        m3_hip_destroy(context);
+        return m3_hip_status(code, message, error);
+    }
+    if (info.name[0] == '\0') {
+        (void)snprintf(info.name, sizeof(info.name), "HIP device 0");
+    }
+    info.kind = M3_BACKEND_HIP;
+    info.unified_memory = false;
+    info.recommended_working_set_bytes = total;
+    info.maximum_storage_bytes = total;
+    status = m3_backend_create_internal(&vtable, context, &info, backend,
+                                        error);
+    if (status != M3_STATUS_OK) {
+        m3_hip_destroy(context);
+    }
+    return status;
+}
+
+void *m3_backend_hip_device(const m3_backend *backend)
+{
+    m3_hip_backend_context *context;
+
+    if (m3_backend_vtable_of(backend) == NULL ||
+        m3_backend_vtable_of(backend)->execute != m3_hip_execute) {
+        return NULL;
+    }
+    context = m3_backend_context_internal(backend);
+    return context == NULL ? NULL : (void *)context->device;
+}
