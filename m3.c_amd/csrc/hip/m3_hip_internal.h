@@ -35,6 +35,7 @@ struct m3_hip_device {
     char name[256];
     uint64_t total_bytes;
     uint32_t compute_units;
+    uint32_t lds_per_block; /* bytes of LDS one workgroup may use */
     /* device flags for data scans and their host mirror */
     uint32_t *scan_flags;
     size_t scan_capacity;

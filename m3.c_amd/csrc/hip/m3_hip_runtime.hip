@@ -229,6 +229,7 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
                   properties.name, properties.gcnArchName);
     device->total_bytes = (uint64_t)properties.totalGlobalMem;
     device->compute_units = (uint32_t)properties.multiProcessorCount;
+    device->lds_per_block = (uint32_t)properties.sharedMemPerBlock;
     code = m3_hip_check(hipStreamCreateWithFlags(&device->stream,
                                                  hipStreamNonBlocking),
                         "hipStreamCreateWithFlags", message, capacity);

@@ -39,7 +39,8 @@ namespace {
 
 constexpr uint32_t kThreads = 256U;
 constexpr uint32_t kWaves = kThreads / 64U;
-constexpr uint32_t kLdsBudget = 65536U;
+constexpr uint32_t kLdsBudget = 65536U; /* dynamic LDS cap per workgroup */
+constexpr uint32_t kStaticLds = 1024U; /* room for the static arrays */
 constexpr uint32_t kMaxTileRows = 16U;
 constexpr uint32_t kMaxWidth = 8192U;
 constexpr uint32_t kPad = 4U;
@@ -384,7 +385,11 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
         plan.strides[0][0] >= 0) {
         m3_softmax_args args;
         uint32_t pitch_bytes = ((uint32_t)width + kPad) * 4U;
-        uint32_t tile_rows = kLdsBudget / pitch_bytes;
+        uint32_t budget = device->lds_per_block > kStaticLds
+                              ? device->lds_per_block - kStaticLds
+                              : 0U;
+        budget = budget > kLdsBudget ? kLdsBudget : budget;
+        uint32_t tile_rows = budget / pitch_bytes;
 
         tile_rows = tile_rows > kMaxTileRows ? kMaxTileRows : tile_rows;
         tile_rows = tile_rows == 0U ? 1U : tile_rows;
