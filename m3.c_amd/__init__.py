@@ -222,7 +222,7 @@ def load():
     st = ctypes.c_int
     _declare(lib, "m3_version", ctypes.c_char_p)
     _declare(lib, "m3_status_string", ctypes.c_char_p, st)
-    _declare(lib, "m3_graph_value_desc_init", None, P(ValueDesc), st,
+    _declare(lib, "m3_graph_value_desc_init", None, P(ValueDesc), st, st,
              ctypes.c_uint8, P(ctypes.c_uint64))
     _declare(lib, "m3_graph_node_desc_init", None, P(NodeDesc), st)
     _declare(lib, "m3_session_options_init", None, P(SessionOptions))

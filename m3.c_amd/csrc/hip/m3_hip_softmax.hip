@@ -113,6 +113,59 @@ __device__ __forceinline__ float m3_softmax_scale(float e, double inverse)
     return (float)((double)e * inverse);
 }
 
+/* The reference's left-to-right F32 sum of `width` values (a multiple of
+ * 4) at `line` in LDS. Loads run one 16-element block ahead of the
+ * dependent additions so LDS latency overlaps the chain. */
+__device__ __forceinline__ float m3_row_sum_in_order(const float *line,
+                                                     uint32_t width)
+{
+    float sum = 0.0F;
+    uint32_t c = 0U;
+
+    if (width >= 16U) {
+        float4 current[4];
+        float4 next[4];
+
+#pragma unroll
+        for (uint32_t k = 0U; k < 4U; ++k) {
+            current[k] = *(const float4 *)(line + 4U * k);
+        }
+        for (c = 16U; c + 16U <= width; c += 16U) {
+#pragma unroll
+            for (uint32_t k = 0U; k < 4U; ++k) {
+                next[k] = *(const float4 *)(line + c + 4U * k);
+            }
+#pragma unroll
+            for (uint32_t k = 0U; k < 4U; ++k) {
+                sum = sum + current[k].x;
+                sum = sum + current[k].y;
+                sum = sum + current[k].z;
+                sum = sum + current[k].w;
+            }
+#pragma unroll
+            for (uint32_t k = 0U; k < 4U; ++k) {
+                current[k] = next[k];
+            }
+        }
+#pragma unroll
+        for (uint32_t k = 0U; k < 4U; ++k) {
+            sum = sum + current[k].x;
+            sum = sum + current[k].y;
+            sum = sum + current[k].z;
+            sum = sum + current[k].w;
+        }
+    }
+    for (; c < width; c += 4U) {
+        float4 e = *(const float4 *)(line + c);
+
+        sum = sum + e.x;
+        sum = sum + e.y;
+        sum = sum + e.z;
+        sum = sum + e.w;
+    }
+    return sum;
+}
+
 /* Per-row state shared through LDS between the phases. */
 struct m3_row_state {
     float maximum;
@@ -189,18 +242,9 @@ __global__ __launch_bounds__(256) void m3_softmax_tiled_kernel(
             float maximum = s->maximum;
 
             if (maximum != INFINITY && maximum != -INFINITY) {
-                const float *line = lds + (uint64_t)threadIdx.x * pitch;
-                float sum = 0.0F;
-
-                for (uint32_t c = 0U; c < width; c += 4U) {
-                    float4 e = *(const float4 *)(line + c);
-
-                    sum = sum + e.x;
-                    sum = sum + e.y;
-                    sum = sum + e.z;
-                    sum = sum + e.w;
-                }
-                s->inverse = 1.0 / (double)sum;
+                s->inverse = 1.0 / (double)m3_row_sum_in_order(
+                                       lds + (uint64_t)threadIdx.x * pitch,
+                                       width);
             } else if (maximum == INFINITY) {
                 s->one_over_count = 1.0F / (float)s->infinities;
             }
@@ -235,6 +279,177 @@ __global__ __launch_bounds__(256) void m3_softmax_tiled_kernel(
         }
     }
 }
+
+/* Register-resident rows (width <= 256 * VPL, a multiple of 4): each wave
+ * owns RPW consecutive rows of a 4*RPW-row tile and keeps them in VGPRs
+ * (VPL float4 per lane per row), issuing every load of its rows before
+ * the first use. e_j goes to LDS only for the in-order sum, which lanes
+ * 0..tile-1 of wave 0 compute; p_j is then formed from the registers. */
+template <int VPL, int RPW, bool F32IO>
+__global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
+    m3_softmax_args a)
+{
+    extern __shared__ float lds[];
+    __shared__ m3_row_state state[4 * RPW];
+    __shared__ uint64_t exp_table[32];
+    constexpr uint32_t kTile = 4U * RPW;
+    const uint32_t lane = threadIdx.x & 63U;
+    const uint32_t wave = threadIdx.x >> 6U;
+    const uint32_t width = a.width;
+    const uint32_t pitch = width + kPad;
+    const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
+    const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
+    const uint32_t out_size = out_dtype == M3N_F32 ? 4U : 2U;
+
+    if (threadIdx.x < 32U) {
+        exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
+    }
+    for (uint64_t tile = blockIdx.x; tile * kTile < a.rows;
+         tile += gridDim.x) {
+        const uint64_t first_row = tile * kTile;
+        float4 v[RPW][VPL];
+        float maximum[RPW];
+
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const uint64_t row = first_row + wave * RPW + k;
+            const uint8_t *in = a.input + row * a.row_stride;
+
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                const uint32_t c = lane * 4U + 256U * j;
+
+                v[k][j] = make_float4(-INFINITY, -INFINITY, -INFINITY,
+                                      -INFINITY);
+                if (row < a.rows && c < width) {
+                    v[k][j] = m3_softmax_load4<F32IO>(in, c, in_dtype);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const uint32_t local = wave * RPW + k;
+            float m = -INFINITY;
+            uint32_t infinities = 0U;
+
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                m = fmaxf(m, fmaxf(fmaxf(v[k][j].x, v[k][j].y),
+                                   fmaxf(v[k][j].z, v[k][j].w)));
+                infinities += (v[k][j].x == INFINITY) +
+                              (v[k][j].y == INFINITY) +
+                              (v[k][j].z == INFINITY) +
+                              (v[k][j].w == INFINITY);
+            }
+            m = m3_wave_max(m);
+            infinities = m3_wave_sum(infinities);
+            maximum[k] = m;
+            if (m != INFINITY && m != -INFINITY) {
+#pragma unroll
+                for (int j = 0; j < VPL; ++j) {
+                    v[k][j].x = m3_expf_with_table(v[k][j].x - m, exp_table);
+                    v[k][j].y = m3_expf_with_table(v[k][j].y - m, exp_table);
+                    v[k][j].z = m3_expf_with_table(v[k][j].z - m, exp_table);
+                    v[k][j].w = m3_expf_with_table(v[k][j].w - m, exp_table);
+                }
+            }
+            float *line = lds + (uint64_t)local * pitch;
+
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                const uint32_t c = lane * 4U + 256U * j;
+
+                if (c < width) {
+                    *(float4 *)(line + c) = v[k][j];
+                }
+            }
+            if (lane == 0U) {
+                state[local].maximum = m;
+                state[local].infinities = infinities;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < kTile && first_row + threadIdx.x < a.rows) {
+            m3_row_state *s = &state[threadIdx.x];
+            const float m = s->maximum;
+
+            if (m != INFINITY && m != -INFINITY) {
+                s->inverse = 1.0 / (double)m3_row_sum_in_order(
+                                       lds + (uint64_t)threadIdx.x * pitch,
+                                       width);
+            } else if (m == INFINITY) {
+                s->one_over_count = 1.0F / (float)s->infinities;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const uint32_t local = wave * RPW + k;
+            const uint64_t row = first_row + local;
+            const float m = maximum[k];
+            const double inverse = state[local].inverse;
+            const float one_over_count = state[local].one_over_count;
+            uint8_t *out = a.output + row * (uint64_t)width * out_size;
+
+            if (row >= a.rows) {
+                continue;
+            }
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                const uint32_t c = lane * 4U + 256U * j;
+                float4 e = v[k][j];
+                float4 p;
+
+                if (c >= width) {
+                    continue;
+                }
+                if (m == -INFINITY) {
+                    p = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+                } else if (m == INFINITY) {
+                    p.x = e.x == INFINITY ? one_over_count : 0.0F;
+                    p.y = e.y == INFINITY ? one_over_count : 0.0F;
+                    p.z = e.z == INFINITY ? one_over_count : 0.0F;
+                    p.w = e.w == INFINITY ? one_over_count : 0.0F;
+                } else {
+                    p.x = m3_softmax_scale(e.x, inverse);
+                    p.y = m3_softmax_scale(e.y, inverse);
+                    p.z = m3_softmax_scale(e.z, inverse);
+                    p.w = m3_softmax_scale(e.w, inverse);
+                }
+                m3_softmax_store4<F32IO>(out, c, out_dtype, p);
+            }
+        }
+    }
+}
+
+typedef void (*m3_softmax_launcher)(dim3, size_t, hipStream_t,
+                                    m3_softmax_args);
+
+template <int VPL, int RPW, bool F32IO>
+void m3_launch_rows(dim3 grid, size_t lds_bytes, hipStream_t stream,
+                    m3_softmax_args args)
+{
+    hipLaunchKernelGGL((m3_softmax_rows_kernel<VPL, RPW, F32IO>), grid,
+                       dim3(kThreads), lds_bytes, stream, args);
+}
+
+struct m3_rows_variant {
+    uint32_t vectors_per_lane;
+    uint32_t rows_per_wave;
+    m3_softmax_launcher f32;
+    m3_softmax_launcher other;
+};
+
+/* Register-resident variants, preferred first for each width class. */
+const m3_rows_variant m3_rows_variants[] = {
+    {1U, 4U, &m3_launch_rows<1, 4, true>, &m3_launch_rows<1, 4, false>},
+    {2U, 4U, &m3_launch_rows<2, 4, true>, &m3_launch_rows<2, 4, false>},
+    {4U, 4U, &m3_launch_rows<4, 4, true>, &m3_launch_rows<4, 4, false>},
+    {4U, 2U, &m3_launch_rows<4, 2, true>, &m3_launch_rows<4, 2, false>},
+    {8U, 2U, &m3_launch_rows<8, 2, true>, &m3_launch_rows<8, 2, false>},
+    {8U, 1U, &m3_launch_rows<8, 1, true>, &m3_launch_rows<8, 1, false>},
+};
 
 struct m3_softmax_general_args {
     const uint8_t *input;
@@ -388,11 +603,9 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
         uint32_t budget = device->lds_per_block > kStaticLds
                               ? device->lds_per_block - kStaticLds
                               : 0U;
-        budget = budget > kLdsBudget ? kLdsBudget : budget;
-        uint32_t tile_rows = budget / pitch_bytes;
+        bool f32 = input->dtype == M3_HIP_F32 && output->dtype == M3_HIP_F32;
 
-        tile_rows = tile_rows > kMaxTileRows ? kMaxTileRows : tile_rows;
-        tile_rows = tile_rows == 0U ? 1U : tile_rows;
+        budget = budget > kLdsBudget ? kLdsBudget : budget;
         std::memset(&args, 0, sizeof(args));
         args.input = in;
         args.output = out;
@@ -401,30 +614,52 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
         args.width = (uint32_t)width;
         args.in_dtype = input->dtype;
         args.out_dtype = output->dtype;
-        args.tile_rows = tile_rows;
-        uint64_t tiles = (rows + tile_rows - 1U) / tile_rows;
-        uint32_t blocks = (uint32_t)(tiles < (uint64_t)device->compute_units *
-                                                 8U
-                                         ? tiles
-                                         : (uint64_t)device->compute_units *
-                                               8U);
-        size_t lds_bytes = (size_t)tile_rows * pitch_bytes;
-        bool f32 = input->dtype == M3_HIP_F32 && output->dtype == M3_HIP_F32;
+        for (const m3_rows_variant &variant : m3_rows_variants) {
+            uint32_t tile = 4U * variant.rows_per_wave;
+            size_t lds_bytes = (size_t)tile * pitch_bytes;
 
-        return m3_hip_launch(
-            device, "m3_softmax_rows",
-            [&]() {
-                if (f32) {
-                    hipLaunchKernelGGL((m3_softmax_tiled_kernel<true>),
-                                       dim3(blocks), dim3(kThreads),
-                                       lds_bytes, device->stream, args);
-                } else {
-                    hipLaunchKernelGGL((m3_softmax_tiled_kernel<false>),
-                                       dim3(blocks), dim3(kThreads),
-                                       lds_bytes, device->stream, args);
-                }
-            },
-            message, capacity);
+            if (width > 256U * variant.vectors_per_lane ||
+                lds_bytes > budget) {
+                continue;
+            }
+            uint64_t tiles = (rows + tile - 1U) / tile;
+            uint64_t cap = (uint64_t)device->compute_units * 8U;
+            dim3 grid((uint32_t)(tiles < cap ? tiles : cap));
+            m3_softmax_launcher launcher = f32 ? variant.f32 : variant.other;
+
+            args.tile_rows = tile;
+            return m3_hip_launch(
+                device, "m3_softmax_rows",
+                [&]() { launcher(grid, lds_bytes, device->stream, args); },
+                message, capacity);
+        }
+        uint32_t tile_rows = budget / pitch_bytes;
+
+        tile_rows = tile_rows > kMaxTileRows ? kMaxTileRows : tile_rows;
+        if (tile_rows != 0U) {
+            args.tile_rows = tile_rows;
+            uint64_t tiles = (rows + tile_rows - 1U) / tile_rows;
+            uint32_t blocks =
+                (uint32_t)(tiles < (uint64_t)device->compute_units * 8U
+                               ? tiles
+                               : (uint64_t)device->compute_units * 8U);
+            size_t lds_bytes = (size_t)tile_rows * pitch_bytes;
+
+            return m3_hip_launch(
+                device, "m3_softmax_rows_lds",
+                [&]() {
+                    if (f32) {
+                        hipLaunchKernelGGL((m3_softmax_tiled_kernel<true>),
+                                           dim3(blocks), dim3(kThreads),
+                                           lds_bytes, device->stream, args);
+                    } else {
+                        hipLaunchKernelGGL((m3_softmax_tiled_kernel<false>),
+                                           dim3(blocks), dim3(kThreads),
+                                           lds_bytes, device->stream, args);
+                    }
+                },
+                message, capacity);
+        }
     }
 
     m3_softmax_general_args general;

@@ -22,7 +22,9 @@
  *      SOFTMAX, finite and inside [-2^31, 2^31) for the cast) with one
  *      flag readback for the whole list;
  * and the first command in list order that fails either check decides the
- * status (OUT_OF_RANGE for data), with no output modified. Then every
+ * status (OUT_OF_RANGE for data), with no output modified. A view that
+ * passed its check is remembered until its storage is written (host write,
+ * kernel output) or freed, so an unchanged input is not scanned again. Then every
  * command is enqueued in order on the device stream and the list waits
  * once at the end.
  */
@@ -37,6 +39,7 @@
 #define M3_HIP_ARENA_ALIGNMENT 256U
 #define M3_HIP_MAX_ARENAS 16U
 #define M3_HIP_MESSAGE 256U
+#define M3_HIP_CLEAN_VIEWS 64U
 
 typedef struct {
     uint8_t *base;
@@ -54,7 +57,81 @@ typedef struct {
     uint32_t *scan_flags;
     size_t *scan_commands;
     size_t scan_capacity;
+    /* views whose last data check passed and whose storage has not been
+     * written since (host write, kernel output or free) */
+    m3_hip_view clean[M3_HIP_CLEAN_VIEWS];
+    uint32_t clean_kinds[M3_HIP_CLEAN_VIEWS];
+    size_t clean_count;
+    size_t clean_next;
 } m3_hip_backend_context;
+
+static bool m3_hip_same_view(const m3_hip_view *a, const m3_hip_view *b)
+{
+    uint32_t axis;
+
+    if (a->base != b->base || a->byte_offset != b->byte_offset ||
+        a->element_count != b->element_count || a->rank != b->rank ||
+        a->dtype != b->dtype) {
+        return false;
+    }
+    for (axis = 0U; axis < a->rank; ++axis) {
+        if (a->shape[axis] != b->shape[axis] ||
+            a->byte_strides[axis] != b->byte_strides[axis]) {
+            return false;
+        }
+    }
+    return true;
+}
+
+static bool m3_hip_known_clean(const m3_hip_backend_context *context,
+                               const m3_hip_view *view, uint32_t kind)
+{
+    size_t i;
+
+    for (i = 0U; i < context->clean_count; ++i) {
+        if (context->clean_kinds[i] == kind &&
+            m3_hip_same_view(&context->clean[i], view)) {
+            return true;
+        }
+    }
+    return false;
+}
+
+static void m3_hip_remember_clean(m3_hip_backend_context *context,
+                                  const m3_hip_view *view, uint32_t kind)
+{
+    size_t slot;
+
+    if (m3_hip_known_clean(context, view, kind)) {
+        return;
+    }
+    if (context->clean_count < M3_HIP_CLEAN_VIEWS) {
+        slot = context->clean_count++;
+    } else {
+        slot = context->clean_next;
+        context->clean_next = (context->clean_next + 1U) % M3_HIP_CLEAN_VIEWS;
+    }
+    context->clean[slot] = *view;
+    context->clean_kinds[slot] = kind;
+}
+
+/* Forgets every clean view over the storage that starts at `base`. */
+static void m3_hip_forget_storage(m3_hip_backend_context *context,
+                                  const void *base)
+{
+    size_t i = 0U;
+
+    while (i < context->clean_count) {
+        if (context->clean[i].base == base) {
+            context->clean_count -= 1U;
+            context->clean[i] = context->clean[context->clean_count];
+            context->clean_kinds[i] = context->clean_kinds[context->clean_count];
+        } else {
+            ++i;
+        }
+    }
+    context->clean_next = 0U;
+}
 
 static m3_status m3_hip_status(int code, const char *message,
                                m3_error *error)
@@ -156,7 +233,7 @@ static void m3_hip_free_storage(void *opaque, void *handle, void *data)
 {
     m3_hip_backend_context *context = opaque;
 
-    (void)data;
+    m3_hip_forget_storage(context, data);
     if (handle != NULL) {
         m3_hip_arena_release(context->device, handle);
     }
@@ -168,7 +245,10 @@ static m3_status m3_hip_write(void *opaque, void *data, size_t byte_offset,
 {
     m3_hip_backend_context *context = opaque;
     char message[M3_HIP_MESSAGE] = "";
-    int code = m3_hip_copy_h2d(context->device, (uint8_t *)data + byte_offset,
+    int code;
+
+    m3_hip_forget_storage(context, data);
+    code = m3_hip_copy_h2d(context->device, (uint8_t *)data + byte_offset,
                                source, byte_count, message, sizeof(message));
 
     return code == M3_HIP_OK ? M3_STATUS_OK
@@ -302,6 +382,9 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
             return status;
         }
         m3_hip_view_of(input, &context->scan_views[scans]);
+        if (m3_hip_known_clean(context, &context->scan_views[scans], kind)) {
+            continue;
+        }
         context->scan_kinds[scans] = kind;
         context->scan_commands[scans] = i;
         scans += 1U;
@@ -316,6 +399,12 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
 
         if (code != M3_HIP_OK) {
             return m3_hip_status(code, message, error);
+        }
+    }
+    for (i = 0U; i < scans; ++i) {
+        if (context->scan_flags[i] == 0U) {
+            m3_hip_remember_clean(context, &context->scan_views[i],
+                                  context->scan_kinds[i]);
         }
     }
     for (i = 0U; i < scans; ++i) {
@@ -410,6 +499,12 @@ static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
         return status;
     }
     for (i = 0U; i < count && code == M3_HIP_OK; ++i) {
+        const m3_tensor_view *output = m3_op_output_of(&commands[i]);
+
+        if (output != NULL) {
+            m3_hip_forget_storage(context,
+                                  m3_storage_device_data(output->storage));
+        }
         code = m3_hip_enqueue(context, &commands[i], message,
                               sizeof(message));
     }

@@ -57,7 +57,7 @@ def hip_available():
     return m3.hip_device_count() > 0
 
 
-@pytest.fixture()
+@pytest.fixture(scope="session")
 def gpu(hip_available):
     if not hip_available:
         pytest.fail("test is marked gpu but no HIP device is visible; the "

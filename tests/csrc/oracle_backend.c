@@ -1,0 +1,227 @@
+/*
+ * oracle_backend.c - TEST INFRASTRUCTURE: an m3 backend over host memory
+ * whose execute hook evaluates commands with the oracle.
+ *
+ * Registered through m3_provider_set_gpu_factory, it stands in for the HIP
+ * device on machines without a GPU so that the graph compiler, liveness
+ * planner, scheduler and session I/O of libm3.so can be tested on the CPU.
+ * It reports itself as M3_BACKEND_HIP so the scheduler treats it as the GPU
+ * provider, records every executed list, and is never part of the product.
+ */
+#include "m3_backend.h"
+#include "m3_oracle.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+#define ORACLE_BACKEND_LOG 4096
+
+typedef struct {
+    int marker;
+} oracle_backend_context;
+
+static int g_log_kinds[ORACLE_BACKEND_LOG];
+static int g_log_lists[ORACLE_BACKEND_LOG];
+static size_t g_log_count;
+static size_t g_list_count;
+static size_t g_allocations;
+static size_t g_fail_allocation_at; /* 0: never */
+static size_t g_reserved;
+
+void oracle_backend_reset(void);
+size_t oracle_backend_log(int *kinds, int *lists, size_t capacity);
+size_t oracle_backend_lists(void);
+size_t oracle_backend_reserved(void);
+void oracle_backend_fail_allocation_at(size_t index);
+m3_status oracle_backend_create(m3_backend **backend, m3_error *error);
+
+void oracle_backend_reset(void)
+{
+    g_log_count = 0U;
+    g_list_count = 0U;
+    g_allocations = 0U;
+    g_fail_allocation_at = 0U;
+    g_reserved = 0U;
+}
+
+size_t oracle_backend_log(int *kinds, int *lists, size_t capacity)
+{
+    size_t i;
+
+    for (i = 0U; i < g_log_count && i < capacity; ++i) {
+        kinds[i] = g_log_kinds[i];
+        lists[i] = g_log_lists[i];
+    }
+    return g_log_count;
+}
+
+size_t oracle_backend_lists(void)
+{
+    return g_list_count;
+}
+
+size_t oracle_backend_reserved(void)
+{
+    return g_reserved;
+}
+
+void oracle_backend_fail_allocation_at(size_t index)
+{
+    g_fail_allocation_at = index;
+}
+
+static void destroy(void *context)
+{
+    free(context);
+}
+
+static m3_status allocate(void *context, size_t byte_count, size_t alignment,
+                          void **handle, void **data, m3_error *error)
+{
+    size_t size = (byte_count + alignment - 1U) / alignment * alignment;
+    void *memory;
+
+    (void)context;
+    *handle = NULL;
+    *data = NULL;
+    g_allocations += 1U;
+    if (g_fail_allocation_at != 0U && g_allocations == g_fail_allocation_at) {
+        return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY,
+                            "injected allocation failure");
+    }
+    if (byte_count == 0U) {
+        return M3_STATUS_OK;
+    }
+    memory = aligned_alloc(alignment, size);
+    if (memory == NULL) {
+        return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY, "no memory");
+    }
+    memset(memory, 0, size);
+    *handle = memory;
+    *data = memory;
+    return M3_STATUS_OK;
+}
+
+static void free_storage(void *context, void *handle, void *data)
+{
+    (void)context;
+    (void)data;
+    free(handle);
+}
+
+static m3_status reserve(void *context, size_t byte_count, m3_error *error)
+{
+    (void)context;
+    (void)error;
+    g_reserved += byte_count;
+    return M3_STATUS_OK;
+}
+
+static void to_oracle(const m3_tensor_view *view, oracle_view *out)
+{
+    uint8_t axis;
+
+    memset(out, 0, sizeof(*out));
+    out->data = m3_storage_data(view->storage);
+    out->byte_offset = view->byte_offset;
+    out->dtype = (uint32_t)view->metadata.dtype;
+    out->rank = view->metadata.rank;
+    for (axis = 0U; axis < view->metadata.rank; ++axis) {
+        out->shape[axis] = view->metadata.shape[axis];
+        out->byte_strides[axis] = view->byte_strides[axis];
+    }
+}
+
+static m3_status execute(void *context, const m3_command *commands,
+                         size_t count, m3_scratch_arena *scratch,
+                         m3_error *error)
+{
+    size_t i;
+
+    (void)context;
+    (void)scratch;
+    for (i = 0U; i < count; ++i) {
+        const m3_command *c = &commands[i];
+        oracle_view a;
+        oracle_view b;
+        oracle_view o;
+        int status = 0;
+
+        if (g_log_count < ORACLE_BACKEND_LOG) {
+            g_log_kinds[g_log_count] = (int)c->kind;
+            g_log_lists[g_log_count] = (int)g_list_count;
+            g_log_count += 1U;
+        }
+        switch (c->kind) {
+        case M3_OP_ADD:
+        case M3_OP_MUL:
+        case M3_OP_SUB:
+        case M3_OP_DIV: {
+            const m3_op_binary *op = &c->descriptor.add;
+            uint32_t code = c->kind == M3_OP_ADD   ? ORACLE_ADD
+                            : c->kind == M3_OP_MUL ? ORACLE_MUL
+                            : c->kind == M3_OP_SUB ? ORACLE_SUB
+                                                   : ORACLE_DIV;
+
+            to_oracle(op->left, &a);
+            to_oracle(op->right, &b);
+            to_oracle(op->output, &o);
+            status = oracle_binary(code, &a, &b, &o);
+            break;
+        }
+        case M3_OP_COPY:
+        case M3_OP_CAST:
+            to_oracle(c->descriptor.cast.input, &a);
+            to_oracle(c->descriptor.cast.output, &o);
+            status = oracle_cast(&a, &o);
+            break;
+        case M3_OP_SOFTMAX:
+            to_oracle(c->descriptor.softmax.input, &a);
+            to_oracle(c->descriptor.softmax.output, &o);
+            status = oracle_preflight_nan(&a);
+            if (status == 0) {
+                status = oracle_softmax(&a, &o);
+            }
+            break;
+        case M3_OP_SNAKE1D:
+            to_oracle(c->descriptor.snake1d.input, &a);
+            to_oracle(c->descriptor.snake1d.alpha, &b);
+            to_oracle(c->descriptor.snake1d.output, &o);
+            status = oracle_snake1d(&a, &b, &o);
+            break;
+        default:
+            return m3_error_set(error, M3_STATUS_UNSUPPORTED,
+                                "oracle backend: kind %d", (int)c->kind);
+        }
+        if (status != 0) {
+            return m3_error_set(error, (m3_status)status,
+                                "oracle backend preflight failed");
+        }
+    }
+    g_list_count += 1U;
+    return M3_STATUS_OK;
+}
+
+m3_status oracle_backend_create(m3_backend **backend, m3_error *error)
+{
+    static const m3_backend_vtable vtable = {destroy, allocate, free_storage,
+                                             execute, NULL, NULL, reserve};
+    m3_backend_info info;
+    oracle_backend_context *context = calloc(1U, sizeof(*context));
+    m3_status status;
+
+    if (context == NULL) {
+        return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY, "no memory");
+    }
+    memset(&info, 0, sizeof(info));
+    strcpy(info.name, "oracle test backend");
+    info.kind = M3_BACKEND_HIP;
+    info.unified_memory = true;
+    info.maximum_storage_bytes = (uint64_t)SIZE_MAX;
+    status = m3_backend_create_internal(&vtable, context, &info, backend,
+                                        error);
+    if (status != M3_STATUS_OK) {
+        free(context);
+    }
+    return status;
+}

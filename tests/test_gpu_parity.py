@@ -1,0 +1,331 @@
+"""Randomised parity of the HIP provider with the oracle (GPU).
+
+Seeded inputs at sizes the oracle finishes in well under a second; every
+launch path of every kernel family is hit (vector fast paths, tails,
+broadcast classes, strided general paths, 16-bit dtypes, aliasing). The
+bar is bit-exact output and equal status for every case, including NaN
+payloads, infinities, signed zeros and subnormals in the inputs.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import m3
+from harness import HipFixture, ViewSpec, as_bytes, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+SPECIALS32 = np.array([0x00000000, 0x80000000, 0x7f800000, 0xff800000,
+                       0x7fc00000, 0xffc12345, 0x7f800001, 0x00000001,
+                       0x807fffff, 0x3f800000, 0x477ff000, 0x477fefff,
+                       0x38800000, 0x387fffff, 0x33000000, 0x33000001,
+                       0x7f7fffff, 0x3f801000, 0x3f803000], np.uint32)
+
+
+@pytest.fixture(scope="module")
+def hip(gpu):
+    fixture = HipFixture()
+    yield fixture
+    fixture.close()
+
+
+def random_f32(rng, count, scale=4.0, specials=0.05):
+    values = (rng.standard_normal(count) * scale).astype(np.float32)
+    bits = values.view(np.uint32)
+    pick = rng.random(count) < specials
+    bits[pick] = rng.choice(SPECIALS32, size=int(pick.sum()))
+    return bits.view(np.float32)
+
+
+def random_bits16(rng, count):
+    return rng.integers(0, 1 << 16, size=count, dtype=np.uint32).astype(
+        np.uint16)
+
+
+def storage_for(rng, dtype, count, specials=0.05):
+    if dtype == m3.F32:
+        return as_bytes(random_f32(rng, count, specials=specials))
+    if dtype == m3.I32:
+        return as_bytes(rng.integers(-2**31, 2**31, size=count,
+                                     dtype=np.int64).astype(np.int32))
+    if dtype == m3.F16:
+        values = (rng.standard_normal(count) * 4).astype(np.float16)
+        bits = values.view(np.uint16)
+        pick = rng.random(count) < specials
+        bits[pick] = random_bits16(rng, int(pick.sum()))
+        return as_bytes(bits)
+    values = (rng.standard_normal(count) * 4).astype(np.float32)
+    bits = (values.view(np.uint32) >> 16).astype(np.uint16)
+    pick = rng.random(count) < specials
+    bits[pick] = random_bits16(rng, int(pick.sum()))
+    return as_bytes(bits)
+
+
+def compare(hip, kind, storages, views, name):
+    print("gpu case", name, flush=True, file=sys.stderr)
+    status, got, message = hip.run(kind, storages, views)
+    ostatus, expected = run_oracle(kind, storages, views)
+    assert status == ostatus, (name, m3.status_name(status), message)
+    for index, (a, b) in enumerate(zip(got, expected)):
+        if bytes(a) != bytes(b):
+            diff = np.flatnonzero(a != b)
+            raise AssertionError("%s: storage %d differs at %d bytes, first "
+                                 "at byte %d" % (name, index, diff.size,
+                                                 diff[0]))
+
+
+def nbytes(spec):
+    if spec.count() == 0:
+        return 0
+    last = spec.offset + sum((d - 1) * s for d, s in
+                             zip(spec.shape, spec.byte_strides()))
+    return last + m3.DTYPE_SIZES[spec.dtype]
+
+
+# ---- binary -----------------------------------------------------------------
+
+BINARY_LAYOUTS = [
+    # (left shape, right shape, output shape)
+    ((8, 64, 96), (96,), (8, 64, 96)),          # trailing broadcast
+    ((8, 64, 96), (8, 64, 96), (8, 64, 96)),    # full x full
+    ((8, 64, 96), (1,), (8, 64, 96)),           # scalar
+    ((3, 40, 100), (40, 1), (3, 40, 100)),      # row broadcast, inner 100
+    ((3, 40, 6), (40, 1), (3, 40, 6)),          # periodic, inner 6
+    ((5, 7, 9), (7, 1), (5, 7, 9)),             # periodic, odd sizes
+    ((4, 1, 33), (1, 5, 33), (4, 5, 33)),       # two-sided broadcast
+    ((1000003,), (1000003,), (1000003,)),       # odd length, tail
+    ((2, 3, 4, 5, 6), (1, 3, 1, 5, 1), (2, 3, 4, 5, 6)),  # general
+    ((), (), ()),                               # rank zero
+    ((7,), (), (7,)),                           # rank-zero right
+    ((4, 262), (262,), (4, 262)),               # period not a multiple of 4
+]
+
+
+@pytest.mark.parametrize("op", [m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV])
+@pytest.mark.parametrize("layout", range(len(BINARY_LAYOUTS)))
+def test_binary_f32_layouts(hip, op, layout):
+    rng = np.random.default_rng(1000 + 10 * op + layout)
+    ls, rs, os_ = BINARY_LAYOUTS[layout]
+    views = [ViewSpec(0, m3.F32, ls), ViewSpec(1, m3.F32, rs),
+             ViewSpec(2, m3.F32, os_)]
+    storages = [storage_for(rng, m3.F32, views[0].count()),
+                storage_for(rng, m3.F32, views[1].count()),
+                np.zeros(nbytes(views[2]), np.uint8)]
+    compare(hip, op, storages, views, "binary op%d layout%d" % (op, layout))
+
+
+@pytest.mark.parametrize("dtypes", [(m3.F16, m3.F16, m3.F16),
+                                    (m3.BF16, m3.BF16, m3.BF16),
+                                    (m3.F32, m3.BF16, m3.F16),
+                                    (m3.F16, m3.F32, m3.BF16),
+                                    (m3.BF16, m3.F16, m3.F32)])
+@pytest.mark.parametrize("layout", [0, 1, 3, 4, 7, 8])
+def test_binary_mixed_dtypes(hip, dtypes, layout):
+    rng = np.random.default_rng(2000 + layout + 7 * sum(dtypes))
+    ls, rs, os_ = BINARY_LAYOUTS[layout]
+    views = [ViewSpec(0, dtypes[0], ls), ViewSpec(1, dtypes[1], rs),
+             ViewSpec(2, dtypes[2], os_)]
+    storages = [storage_for(rng, dtypes[0], views[0].count()),
+                storage_for(rng, dtypes[1], views[1].count()),
+                np.zeros(nbytes(views[2]), np.uint8)]
+    for op in (m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV):
+        compare(hip, op, storages, views,
+                "binary %s layout%d op%d" % (dtypes, layout, op))
+
+
+def test_binary_strided_and_offset_views(hip):
+    rng = np.random.default_rng(3)
+    # left: transposed [64, 48] view of a [48, 64] buffer at a 4-byte
+    # offset; right: every other element of a [96] buffer.
+    left = ViewSpec(0, m3.F32, (64, 48), (4, 256), 4)
+    right = ViewSpec(1, m3.F32, (48,), (8,), 0)
+    out = ViewSpec(2, m3.F32, (64, 48))
+    storages = [storage_for(rng, m3.F32, 48 * 64 + 1),
+                storage_for(rng, m3.F32, 96),
+                np.zeros(nbytes(out), np.uint8)]
+    for op in (m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV):
+        compare(hip, op, storages, [left, right, out], "strided op%d" % op)
+
+
+def test_binary_exact_alias_in_place(hip):
+    rng = np.random.default_rng(4)
+    shape = (16, 1000)
+    storages = [storage_for(rng, m3.F32, 16000),
+                storage_for(rng, m3.F32, 1000)]
+    views = [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, (1000,)),
+             ViewSpec(0, m3.F32, shape)]
+    compare(hip, m3.OP_MUL, storages, views, "in-place mul")
+
+
+# ---- cast / copy -------------------------------------------------------------
+
+DTYPES = [m3.F32, m3.F16, m3.BF16, m3.I32]
+
+
+@pytest.mark.parametrize("src", DTYPES)
+@pytest.mark.parametrize("dst", DTYPES)
+@pytest.mark.parametrize("count", [1, 3, 4, 1021, 65536 + 7])
+def test_cast_all_pairs(hip, src, dst, count):
+    rng = np.random.default_rng(5000 + 97 * src + 13 * dst + count)
+    storages = [storage_for(rng, src, count, specials=0.2),
+                np.zeros(count * m3.DTYPE_SIZES[dst], np.uint8)]
+    views = [ViewSpec(0, src, (count,)), ViewSpec(1, dst, (count,))]
+    if src != m3.I32 and dst == m3.I32:
+        # valid in-range values (the invalid case is a preflight test)
+        values = rng.uniform(-2e9, 2e9, count).astype(np.float32)
+        if src == m3.F32:
+            storages[0] = as_bytes(values)
+        elif src == m3.F16:
+            storages[0] = as_bytes(rng.uniform(-6e4, 6e4, count).astype(
+                np.float16).view(np.uint16))
+        else:
+            storages[0] = as_bytes((values.view(np.uint32) >> 16).astype(
+                np.uint16))
+    kind = m3.OP_COPY if src == dst else m3.OP_CAST
+    compare(hip, kind, storages, views, "cast %d->%d n=%d" % (src, dst, count))
+
+
+def test_cast_exhaustive_16bit_sources(hip):
+    """All 65536 half and bfloat16 bit patterns to every other dtype."""
+    bits = as_bytes(np.arange(1 << 16, dtype=np.uint32).astype(np.uint16))
+    for src in (m3.F16, m3.BF16):
+        for dst in (m3.F32, m3.F16, m3.BF16):
+            if dst == src:
+                continue
+            views = [ViewSpec(0, src, (1 << 16,)),
+                     ViewSpec(1, dst, (1 << 16,))]
+            storages = [bits, np.zeros((1 << 16) * m3.DTYPE_SIZES[dst],
+                                       np.uint8)]
+            compare(hip, m3.OP_CAST, storages, views,
+                    "exhaustive %d->%d" % (src, dst))
+
+
+def test_cast_f32_dense_bit_sweep(hip):
+    """Every 4099th F32 bit pattern (about a million, all classes) to F16
+    and BF16."""
+    bits = np.arange(0, 1 << 32, 4099, dtype=np.uint64).astype(np.uint32)
+    for dst in (m3.F16, m3.BF16):
+        views = [ViewSpec(0, m3.F32, (bits.size,)),
+                 ViewSpec(1, dst, (bits.size,))]
+        storages = [as_bytes(bits), np.zeros(bits.size * 2, np.uint8)]
+        compare(hip, m3.OP_CAST, storages, views, "sweep ->%d" % dst)
+
+
+def test_cast_strided_input(hip):
+    rng = np.random.default_rng(6)
+    for src, dst in ((m3.F32, m3.F16), (m3.BF16, m3.F32), (m3.I32, m3.BF16),
+                     (m3.F16, m3.F16)):
+        src_view = ViewSpec(0, src, (33, 17), (m3.DTYPE_SIZES[src],
+                                               33 * m3.DTYPE_SIZES[src]))
+        storages = [storage_for(rng, src, 33 * 17),
+                    np.zeros(33 * 17 * m3.DTYPE_SIZES[dst], np.uint8)]
+        kind = m3.OP_COPY if src == dst else m3.OP_CAST
+        compare(hip, kind, storages, [src_view, ViewSpec(1, dst, (33, 17))],
+                "strided cast %d->%d" % (src, dst))
+
+
+# ---- softmax ------------------------------------------------------------------
+
+def softmax_logits(rng, rows, width, causal=True, specials=True):
+    values = (rng.standard_normal((rows, width)) * 3).astype(np.float32)
+    if causal:
+        mask = np.arange(width)[None, :] > (np.arange(rows)[:, None] %
+                                            max(width, 1))
+        values[mask] = -np.inf
+    if specials and rows >= 4:
+        values[0, :] = -np.inf
+        values[1, ::3] = np.inf
+        values[2, :] = 0.0
+        values[3, :] = np.float32(1e-40)
+    return values
+
+
+@pytest.mark.parametrize("width", [1, 3, 4, 12, 64, 256, 260, 512, 1000,
+                                   1024, 2048, 3000, 4096, 8192, 10000])
+def test_softmax_widths(hip, width):
+    rng = np.random.default_rng(7000 + width)
+    rows = max(4, min(300, 300000 // width))
+    logits = softmax_logits(rng, rows, width)
+    views = [ViewSpec(0, m3.F32, (rows, width)),
+             ViewSpec(1, m3.F32, (rows, width))]
+    storages = [as_bytes(logits), np.zeros(logits.nbytes, np.uint8)]
+    compare(hip, m3.OP_SOFTMAX, storages, views, "softmax w=%d" % width)
+
+
+@pytest.mark.parametrize("dtypes", [(m3.F16, m3.F16), (m3.BF16, m3.BF16),
+                                    (m3.F32, m3.F16), (m3.BF16, m3.F32)])
+@pytest.mark.parametrize("width", [5, 256, 1024, 1500])
+def test_softmax_dtypes(hip, dtypes, width):
+    rng = np.random.default_rng(8000 + width + 17 * dtypes[0] + dtypes[1])
+    rows = 64
+    logits = softmax_logits(rng, rows, width)
+    if dtypes[0] == m3.F16:
+        source = as_bytes(logits.astype(np.float16).view(np.uint16))
+    elif dtypes[0] == m3.BF16:
+        source = as_bytes((logits.view(np.uint32) >> 16).astype(np.uint16))
+    else:
+        source = as_bytes(logits)
+    views = [ViewSpec(0, dtypes[0], (rows, width)),
+             ViewSpec(1, dtypes[1], (rows, width))]
+    storages = [source, np.zeros(rows * width * m3.DTYPE_SIZES[dtypes[1]],
+                                 np.uint8)]
+    compare(hip, m3.OP_SOFTMAX, storages, views,
+            "softmax %s w=%d" % (dtypes, width))
+
+
+def test_softmax_strided_and_in_place(hip):
+    rng = np.random.default_rng(9)
+    logits = softmax_logits(rng, 64, 1024)
+    # rows with a padded stride, and a transposed view (column stride)
+    padded = np.full((64, 1040), 7.0, np.float32)
+    padded[:, :1024] = logits
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(padded),
+                                 np.zeros(logits.nbytes, np.uint8)],
+            [ViewSpec(0, m3.F32, (64, 1024), (4160, 4)),
+             ViewSpec(1, m3.F32, (64, 1024))], "softmax padded rows")
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(logits.T.copy()),
+                                 np.zeros(logits.nbytes, np.uint8)],
+            [ViewSpec(0, m3.F32, (64, 1024), (4, 256)),
+             ViewSpec(1, m3.F32, (64, 1024))], "softmax transposed")
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(logits)],
+            [ViewSpec(0, m3.F32, (64, 1024)),
+             ViewSpec(0, m3.F32, (64, 1024))], "softmax in place")
+    batched = softmax_logits(rng, 4 * 32, 1024).reshape(4, 32, 1024)
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(batched),
+                                 np.zeros(batched.nbytes, np.uint8)],
+            [ViewSpec(0, m3.F32, (4, 32, 1024)),
+             ViewSpec(1, m3.F32, (4, 32, 1024))], "softmax rank 3")
+
+
+# ---- snake1d -------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(2, 16, 1024), (1, 3, 5), (3, 7, 12),
+                                   (2, 96, 4096)])
+def test_snake1d_layouts(hip, shape):
+    rng = np.random.default_rng(10000 + sum(shape))
+    count = int(np.prod(shape))
+    x = random_f32(rng, count, scale=3.0, specials=0.01)
+    x[:8] = np.array([200.0, -1e5, 3e38, 0.0, -0.0, 1e-30, 1e30, 125.0],
+                     np.float32)[:min(8, count)]
+    alpha = rng.uniform(0.1, 2.0, shape[1]).astype(np.float32)
+    alpha[0] = np.uint32(0xb089705f).view(np.float32)  # -epsilon
+    views = [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, (1, shape[1], 1)),
+             ViewSpec(2, m3.F32, shape)]
+    storages = [as_bytes(x), as_bytes(alpha), np.zeros(x.nbytes, np.uint8)]
+    compare(hip, m3.OP_SNAKE1D, storages, views, "snake %s" % (shape,))
+
+
+def test_snake1d_strided_input_and_alias(hip):
+    rng = np.random.default_rng(11)
+    x = random_f32(rng, 2 * 8 * 64, scale=2.0, specials=0.0)
+    alpha = rng.uniform(0.1, 2.0, 16).astype(np.float32)
+    # input: channels-last buffer [2, 64, 8] viewed as [2, 8, 64]
+    views = [ViewSpec(0, m3.F32, (2, 8, 64), (2048, 4, 32)),
+             ViewSpec(1, m3.F32, (1, 8, 1), (32, 8, 4)),
+             ViewSpec(2, m3.F32, (2, 8, 64))]
+    storages = [as_bytes(x), as_bytes(alpha), np.zeros(x.nbytes, np.uint8)]
+    compare(hip, m3.OP_SNAKE1D, storages, views, "snake strided")
+    compare(hip, m3.OP_SNAKE1D, [as_bytes(x), as_bytes(alpha[:8])],
+            [ViewSpec(0, m3.F32, (2, 8, 64)), ViewSpec(1, m3.F32, (1, 8, 1)),
+             ViewSpec(0, m3.F32, (2, 8, 64))], "snake in place")

@@ -1,0 +1,360 @@
+"""Graph builder, session compiler, liveness planner and scheduler (CPU).
+
+libm3.so runs unchanged; the scheduler's GPU backend constructor is
+replaced (m3_provider_set_gpu_factory) by a test backend over host memory
+that evaluates commands with the oracle (tests/csrc/oracle_backend.c).
+Restates the reference's graph tests (tests/test_graph_runtime.c:87-248)
+and adds brute-force checks of the liveness plan on random graphs.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, m3
+
+BUILD = os.path.join(ROOT, "tests", "_build")
+LIB = os.path.join(BUILD, "liboracle_backend.so")
+
+
+def _build_backend():
+    os.makedirs(BUILD, exist_ok=True)
+    sources = [os.path.join(ROOT, "tests", "csrc", "oracle_backend.c"),
+               os.path.join(ROOT, "oracle", "m3_oracle.c")]
+    subprocess.run(["gcc", "-std=c11", "-O2", "-fPIC", "-shared",
+                    "-ffp-contract=off", "-mfma", "-D_POSIX_C_SOURCE=200809L",
+                    "-I", os.path.join(ROOT, "include"),
+                    "-I", os.path.join(ROOT, "oracle")] + sources +
+                   ["-L", os.path.join(ROOT, "m3.c_amd"), "-lm3",
+                    "-Wl,-rpath," + os.path.join(ROOT, "m3.c_amd"), "-lm",
+                    "-o", LIB], check=True)
+
+
+@pytest.fixture(scope="module")
+def backend_lib():
+    lib, _ = m3.load()
+    _build_backend()
+    fake = ctypes.CDLL(LIB)
+    fake.oracle_backend_log.restype = ctypes.c_size_t
+    fake.oracle_backend_log.argtypes = [ctypes.POINTER(ctypes.c_int),
+                                        ctypes.POINTER(ctypes.c_int),
+                                        ctypes.c_size_t]
+    fake.oracle_backend_lists.restype = ctypes.c_size_t
+    fake.oracle_backend_reserved.restype = ctypes.c_size_t
+    fake.oracle_backend_fail_allocation_at.argtypes = [ctypes.c_size_t]
+    factory = ctypes.cast(fake.oracle_backend_create, ctypes.c_void_p)
+    lib.m3_provider_set_gpu_factory.argtypes = [ctypes.c_void_p]
+    lib.m3_provider_set_gpu_factory(factory)
+    yield fake
+    lib.m3_provider_set_gpu_factory(None)
+
+
+@pytest.fixture()
+def fake(backend_lib):
+    backend_lib.oracle_backend_reset()
+    return backend_lib
+
+
+def log_of(fake):
+    kinds = (ctypes.c_int * 4096)()
+    lists = (ctypes.c_int * 4096)()
+    count = fake.oracle_backend_log(kinds, lists, 4096)
+    return list(kinds[:count]), list(lists[:count])
+
+
+def reference_graph():
+    """tests/test_graph_runtime.c:30-85 with TANH replaced by COPY: the
+    liveness plan depends only on the topology and the sizes."""
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, (4,))
+    c = g.add_value(m3.CONSTANT, m3.F32, (4,))
+    t0 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+    t1 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+    t2 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+    y = g.add_value(m3.OUTPUT, m3.F32, (4,))
+    constant = np.array([0.5, -1.0, 2.0, 3.0], np.float32)
+    g.set_constant(c, constant)
+    g.add_node(m3.OP_ADD, [x, c], [t0])
+    g.add_node(m3.OP_COPY, [t0], [t1])
+    g.add_node(m3.OP_MUL, [t1, c], [t2])
+    g.add_node(m3.OP_ADD, [t2, x], [y])
+    return g, x, y, constant
+
+
+def test_liveness_plan_kat_and_execution(fake):
+    g, x, y, constant = reference_graph()
+    session = m3.Session(g, allow_neural_engine=False)
+    g.free()
+    plan = session.plan()
+    assert (plan.value_count, plan.node_count, plan.storage_slot_count,
+            plan.allocated_bytes) == (6, 4, 5, 80)
+    assert fake.oracle_backend_reserved() == 5 * 256
+    assert [session.provider(i) for i in range(4)] == [m3.PROVIDER_HIP] * 4
+    data = np.array([1.0, 2.0, -3.0, 0.25], np.float32)
+    session.write(x, data)
+    session.run()
+    out = session.read(y, np.zeros(4, np.float32))
+    expected = ((data + constant) * constant + data).astype(np.float32)
+    assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
+    kinds, lists = log_of(fake)
+    assert kinds == [m3.OP_ADD, m3.OP_COPY, m3.OP_MUL, m3.OP_ADD]
+    assert lists == [0, 0, 0, 0]  # one partition, one list per run
+    session.free()
+
+
+def test_session_io_contracts(fake):
+    g, x, y, _ = reference_graph()
+    session = m3.Session(g)
+    data = np.zeros(4, np.float32)
+    lib, _ = m3.load()
+    ptr = data.ctypes.data_as(ctypes.c_void_p)
+    assert lib.m3_session_write_input(session.handle, y, ptr, 16,
+                                      None) == m3.INVALID_ARGUMENT
+    assert lib.m3_session_read_output(session.handle, x, ptr, 16,
+                                      None) == m3.INVALID_ARGUMENT
+    assert lib.m3_session_write_input(session.handle, x, ptr, 15,
+                                      None) == m3.INVALID_ARGUMENT
+    assert lib.m3_session_write_input(session.handle, 99, ptr, 16,
+                                      None) == m3.OUT_OF_RANGE
+    error = m3.Error()
+    node = ctypes.c_int()
+    assert lib.m3_session_get_node_provider(session.handle, 4,
+                                            ctypes.byref(node),
+                                            ctypes.byref(error)) == \
+        m3.OUT_OF_RANGE
+    session.free()
+
+
+def _session_status(graph, options=None):
+    lib, _ = m3.load()
+    handle = ctypes.c_void_p()
+    error = m3.Error()
+    opts = None
+    if options is not None:
+        opts = ctypes.byref(m3.SessionOptions(*options))
+    status = lib.m3_session_create(ctypes.byref(handle), graph.handle, opts,
+                                   ctypes.byref(error))
+    if handle:
+        lib.m3_session_free(handle)
+    return status, bool(handle.value), error.text()
+
+
+def test_graph_validation_rejects_atomically(fake):
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, (2,))
+    t = g.add_value(m3.TEMPORARY, m3.F32, (2,))
+    y = g.add_value(m3.OUTPUT, m3.F32, (2,))
+    g.add_node(m3.OP_ADD, [t, x], [y])
+    status, made, _ = _session_status(g)
+    assert status == m3.INVALID_ARGUMENT and not made
+    lib, _ = m3.load()
+    node = m3.NodeDesc()
+    lib.m3_graph_node_desc_init(ctypes.byref(node), m3.OP_ADD)
+    node.inputs[1] = x
+    inferred = ctypes.c_uint32(m3.VALUE_NONE)
+    assert lib.m3_graph_add_inferred_value(
+        g.handle, ctypes.byref(node), 0, m3.TEMPORARY, m3.F32,
+        ctypes.byref(inferred), None) == m3.OUT_OF_RANGE
+    assert inferred.value == m3.VALUE_NONE
+    node.kind = 999
+    node.inputs[0] = x
+    assert lib.m3_graph_add_inferred_value(
+        g.handle, ctypes.byref(node), 0, m3.TEMPORARY, m3.F32,
+        ctypes.byref(inferred), None) == m3.UNSUPPORTED
+    g.free()
+
+    g = m3.Graph()
+    c = g.add_value(m3.CONSTANT, m3.F32, (2,))
+    y = g.add_value(m3.OUTPUT, m3.F32, (2,))
+    g.add_node(m3.OP_COPY, [c], [y])
+    status, made, _ = _session_status(g)
+    assert status == m3.INVALID_ARGUMENT and not made  # unset constant
+    g.free()
+
+
+def test_topology_errors(fake):
+    def graph_with(nodes, roles):
+        g = m3.Graph()
+        ids = [g.add_value(role, m3.F32, (3,)) for role in roles]
+        for kind, ins, outs in nodes:
+            g.add_node(kind, [ids[i] for i in ins], [ids[o] for o in outs])
+        return g
+
+    cases = [
+        # writes an input
+        ([(m3.OP_COPY, [0], [0])], [m3.INPUT]),
+        # two producers
+        ([(m3.OP_COPY, [0], [1]), (m3.OP_COPY, [0], [1])],
+         [m3.INPUT, m3.OUTPUT]),
+        # no producer for an output
+        ([(m3.OP_COPY, [0], [1])], [m3.INPUT, m3.OUTPUT, m3.OUTPUT]),
+    ]
+    for nodes, roles in cases:
+        g = graph_with(nodes, roles)
+        status, made, _ = _session_status(g)
+        assert status == m3.INVALID_ARGUMENT and not made
+        g.free()
+
+
+def test_extra_and_out_of_range_node_operands(fake):
+    lib, _ = m3.load()
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, (3,))
+    y = g.add_value(m3.OUTPUT, m3.F32, (3,))
+    node = m3.NodeDesc()
+    lib.m3_graph_node_desc_init(ctypes.byref(node), m3.OP_COPY)
+    node.inputs[0] = x
+    node.inputs[1] = x  # COPY takes one input
+    node.outputs[0] = y
+    assert lib.m3_graph_add_node(g.handle, ctypes.byref(node), None) == m3.OK
+    assert _session_status(g)[0] == m3.INVALID_ARGUMENT
+    g.free()
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, (3,))
+    y = g.add_value(m3.OUTPUT, m3.F32, (3,))
+    g.add_node(m3.OP_COPY, [x + 7], [y])
+    assert _session_status(g)[0] == m3.OUT_OF_RANGE
+    g.free()
+
+
+def test_provider_options(fake):
+    g, _, _, _ = reference_graph()
+    assert _session_status(g, (False, False, False))[0] == \
+        m3.INVALID_ARGUMENT
+    status, made, text = _session_status(g, (False, False, True))
+    assert status == m3.UNSUPPORTED and not made
+    assert "no CPU provider" in text
+    assert _session_status(g, (False, True, False))[0] == m3.OK
+    # Neural Engine alone gives GPU storage but no provider for regular
+    # nodes, as in the reference (src/m3_provider.c:62-99).
+    assert _session_status(g, (True, False, False))[0] == m3.UNSUPPORTED
+    g.free()
+
+
+def test_out_of_scope_operation_is_unsupported(fake):
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, (3,))
+    y = g.add_value(m3.OUTPUT, m3.F32, (3,))
+    g.add_node(m3.OP_TANH, [x], [y])
+    status, made, _ = _session_status(g)
+    assert status == m3.UNSUPPORTED and not made
+    g.free()
+    lib, _ = m3.load()
+    g = m3.Graph()
+    assert lib.m3_graph_add_coreml_partition(g.handle, None,
+                                             None) == m3.UNSUPPORTED
+    g.free()
+
+
+def test_allocation_failure_leaves_no_session(fake):
+    g, _, _, _ = reference_graph()
+    for index in range(1, 6):
+        fake.oracle_backend_fail_allocation_at(index)
+        status, made, _ = _session_status(g)
+        assert status == m3.OUT_OF_MEMORY and not made
+    fake.oracle_backend_fail_allocation_at(0)
+    assert _session_status(g)[0] == m3.OK
+    g.free()
+
+
+def _random_graph(rng, nodes):
+    """A random DAG of elementwise nodes over [5, 7] F32 values with mixed
+    sizes (broadcast [7] and [1] operands)."""
+    g = m3.Graph()
+    shape = (5, 7)
+    values = []  # (id, shape, numpy value)
+    inputs = []
+    for i in range(3):
+        vid = g.add_value(m3.INPUT, m3.F32, shape)
+        data = rng.standard_normal(shape).astype(np.float32)
+        inputs.append((vid, data))
+        values.append((vid, shape, data))
+    c = g.add_value(m3.CONSTANT, m3.F32, (7,))
+    cdata = rng.standard_normal(7).astype(np.float32)
+    g.set_constant(c, cdata)
+    values.append((c, (7,), cdata))
+    produced = []
+    ops = [(m3.OP_ADD, np.add), (m3.OP_MUL, np.multiply),
+           (m3.OP_SUB, np.subtract)]
+    for n in range(nodes):
+        kind, fn = ops[rng.integers(len(ops))]
+        a = values[rng.integers(len(values))]
+        b = values[rng.integers(len(values))]
+        out_shape = np.broadcast_shapes(a[1], b[1])
+        role = m3.OUTPUT if n == nodes - 1 or rng.random() < 0.15 \
+            else m3.TEMPORARY
+        vid = g.add_value(role, m3.F32, out_shape)
+        result = fn(np.broadcast_to(a[2], out_shape),
+                    np.broadcast_to(b[2], out_shape)).astype(np.float32)
+        g.add_node(kind, [a[0], b[0]], [vid])
+        values.append((vid, out_shape, result))
+        if role == m3.OUTPUT:
+            produced.append((vid, result))
+    return g, inputs, produced
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_graphs_reuse_slots_without_clobbering(fake, seed):
+    rng = np.random.default_rng(seed)
+    g, inputs, outputs = _random_graph(rng, 40)
+    session = m3.Session(g)
+    g.free()
+    plan = session.plan()
+    assert plan.storage_slot_count < plan.value_count  # reuse happened
+    for vid, data in inputs:
+        session.write(vid, data)
+    session.run()
+    for vid, expected in outputs:
+        got = session.read(vid, np.zeros(expected.shape, np.float32))
+        assert np.array_equal(got.view(np.uint32),
+                              expected.view(np.uint32)), vid
+    session.free()
+
+
+def test_command_executor_runs_flow_math(fake, backend_lib):
+    """The non-graph caller (src/m3_command_executor.c:55-92) used by the
+    flow CFG/Euler math: one list per op through the scheduler."""
+    lib, _ = m3.load()
+    backend = ctypes.c_void_p()
+    error = m3.Error()
+    assert backend_lib.oracle_backend_create(ctypes.byref(backend),
+                                             ctypes.byref(error)) == m3.OK
+    executor = (ctypes.c_uint8 * 64)()
+    lib.m3_command_executor_init(executor, backend)
+    storages = []
+    views = []
+    arrays = [np.arange(6, dtype=np.float32), np.full(1, 2.0, np.float32),
+              np.zeros(6, np.float32)]
+    for array in arrays:
+        storage = ctypes.c_void_p()
+        lib.m3_storage_allocate(backend, array.nbytes, 64,
+                                ctypes.byref(storage), None)
+        lib.m3_storage_write(storage, 0, array.ctypes.data_as(
+            ctypes.c_void_p), array.nbytes, None)
+        view = m3.TensorView()
+        shape = (ctypes.c_uint64 * 8)(*array.shape)
+        assert lib.m3_tensor_view_contiguous(ctypes.byref(view), storage,
+                                             m3.F32, 1, shape, 0,
+                                             None) == m3.OK
+        storages.append(storage)
+        views.append(view)
+    command = m3.Command()
+    command.kind = m3.OP_MUL
+    for i in range(3):
+        command.descriptor.views[i] = ctypes.pointer(views[i])
+    lib.m3_command_executor_execute.argtypes = [ctypes.c_void_p,
+                                                ctypes.POINTER(m3.Command),
+                                                ctypes.c_size_t,
+                                                ctypes.POINTER(m3.Error)]
+    assert lib.m3_command_executor_execute(executor, ctypes.byref(command), 1,
+                                           ctypes.byref(error)) == m3.OK
+    out = np.zeros(6, np.float32)
+    lib.m3_storage_read(storages[2], 0, out.ctypes.data_as(ctypes.c_void_p),
+                        24, None)
+    assert list(out) == [0, 2, 4, 6, 8, 10]
+    lib.m3_command_executor_dispose(executor)
+    for storage in storages:
+        lib.m3_storage_free(storage)
+    lib.m3_backend_free(backend)
