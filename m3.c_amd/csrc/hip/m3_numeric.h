@@ -13,10 +13,9 @@
  *     the F16 subnormal step 2^-24 at the F32 unit in the last place;
  *   - F32 -> BF16 adds 0x7fff plus the kept low bit; NaN keeps its top 16
  *     bits and sets 0x0040.
- * m3_binary_nan_fix makes a NaN result carry the bits an x86-64 SSE
- * operation produces (first NaN operand quieted, else the default NaN
- * 0xffc00000), so that arithmetic on NaN inputs matches a CPU run of the
- * reference bit for bit.
+ * m3_binary_nan_fix makes a NaN result carry the bits the x86-64 build of
+ * the reference's CPU provider produces, so that arithmetic on NaN inputs
+ * matches it bit for bit.
  *
  * The file is valid C11 and HIP C++; under HIP every function is
  * __host__ __device__.
@@ -109,14 +108,22 @@ M3_HD int m3_f32_is_nan_bits(uint32_t bits)
     return (bits & 0x7fffffffU) > 0x7f800000U;
 }
 
-/* Bits of the NaN an x86-64 scalar SSE operation returns for operands a and
- * b when the IEEE result is NaN; `result` is returned unchanged when it is
- * not NaN. */
-M3_HD uint32_t m3_binary_nan_fix(uint32_t result, uint32_t a, uint32_t b)
+/* Bits of the NaN the x86-64 CPU provider returns for operands a and b
+ * when the IEEE result is NaN; `result` is returned unchanged when it is
+ * not NaN. A single NaN operand propagates quieted; an invalid operation
+ * on non-NaN operands gives the default NaN 0xffc00000. When both operands
+ * are NaN, IEEE 754 leaves the payload open: the reference's host loop
+ * compiled by gcc for x86-64 evaluates a commutative operation (ADD, MUL)
+ * as b (op) a and so returns b's NaN, and SUB/DIV return a's. */
+M3_HD uint32_t m3_binary_nan_fix(uint32_t result, uint32_t a, uint32_t b,
+                                 int commutative)
 {
-    uint32_t propagated = m3_f32_is_nan_bits(a)   ? (a | 0x00400000U)
-                          : m3_f32_is_nan_bits(b) ? (b | 0x00400000U)
-                                                  : 0xffc00000U;
+    int a_nan = m3_f32_is_nan_bits(a);
+    int b_nan = m3_f32_is_nan_bits(b);
+    uint32_t propagated = (a_nan && !(commutative && b_nan))
+                              ? (a | 0x00400000U)
+                          : b_nan ? (b | 0x00400000U)
+                                  : 0xffc00000U;
 
     return m3_f32_is_nan_bits(result) ? propagated : result;
 }
@@ -160,7 +167,8 @@ M3_HD uint32_t m3_binary_f32_bits(uint32_t op, uint32_t a, uint32_t b)
     } else {
         r = x / y;
     }
-    return m3_binary_nan_fix(m3_f32_bits(r), a, b);
+    return m3_binary_nan_fix(m3_f32_bits(r), a, b,
+                             op == M3N_ADD || op == M3N_MUL);
 }
 
 #endif
