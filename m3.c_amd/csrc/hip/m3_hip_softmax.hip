@@ -79,7 +79,7 @@ template <bool F32IO>
 __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
                                                    uint32_t c, uint32_t dtype)
 {
-    if (F32IO) {
+    if (F32IO || dtype == M3N_F32) {
         return *(const float4 *)(row + (uint64_t)c * 4U);
     }
     uint2 h = *(const uint2 *)(row + (uint64_t)c * 2U);
@@ -95,7 +95,7 @@ template <bool F32IO>
 __device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint32_t c,
                                                   uint32_t dtype, float4 p)
 {
-    if (F32IO) {
+    if (F32IO || dtype == M3N_F32) {
         *(float4 *)(row + (uint64_t)c * 4U) = p;
         return;
     }
