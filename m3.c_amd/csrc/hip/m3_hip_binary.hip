@@ -142,7 +142,7 @@ __device__ __forceinline__ void m3_store4(uint8_t *out, uint32_t dtype,
                                           uint32_t f, uint4 v)
 {
     if (F32ONLY || dtype == M3N_F32) {
-        *(uint4 *)(out + (uint64_t)f * 4U) = v;
+        m3_stream_store((uint4 *)(out + (uint64_t)f * 4U), v);
         return;
     }
     uint2 packed;
@@ -151,7 +151,7 @@ __device__ __forceinline__ void m3_store4(uint8_t *out, uint32_t dtype,
                (m3_store_from_f32_bits(v.y, dtype) << 16U);
     packed.y = m3_store_from_f32_bits(v.z, dtype) |
                (m3_store_from_f32_bits(v.w, dtype) << 16U);
-    *(uint2 *)(out + (uint64_t)f * 2U) = packed;
+    m3_stream_store((uint2 *)(out + (uint64_t)f * 2U), packed);
 }
 
 template <int OP, bool F32ONLY>
@@ -356,15 +356,17 @@ int m3_launch_binary_op(m3_hip_device *device, const m3_hip_view *left,
 
         return m3_hip_launch(
             device, names[OP],
-            [&]() {
+            [&](hipEvent_t start, hipEvent_t stop) {
                 if (f32) {
-                    hipLaunchKernelGGL((m3_binary_vec_kernel<OP, true>),
-                                       dim3(blocks), dim3(kThreads), 0,
-                                       device->stream, vec);
+                    hipExtLaunchKernelGGL((m3_binary_vec_kernel<OP, true>),
+                                          dim3(blocks), dim3(kThreads), 0,
+                                          device->stream, start, stop, 0U,
+                                          vec);
                 } else {
-                    hipLaunchKernelGGL((m3_binary_vec_kernel<OP, false>),
-                                       dim3(blocks), dim3(kThreads), 0,
-                                       device->stream, vec);
+                    hipExtLaunchKernelGGL((m3_binary_vec_kernel<OP, false>),
+                                          dim3(blocks), dim3(kThreads), 0,
+                                          device->stream, start, stop, 0U,
+                                          vec);
                 }
             },
             message, capacity);
@@ -390,9 +392,10 @@ int m3_launch_binary_op(m3_hip_device *device, const m3_hip_view *left,
 
     return m3_hip_launch(
         device, names[OP],
-        [&]() {
-            hipLaunchKernelGGL((m3_binary_general_kernel<OP>), dim3(blocks),
-                               dim3(256), 0, device->stream, general);
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL((m3_binary_general_kernel<OP>), dim3(blocks),
+                                  dim3(256), 0, device->stream, start, stop,
+                                  0U, general);
         },
         message, capacity);
 }

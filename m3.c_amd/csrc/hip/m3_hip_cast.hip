@@ -94,7 +94,7 @@ __global__ __launch_bounds__(256) void m3_cast_vec_kernel(
                                      m3_convert<IN, OUT>(v[u].z),
                                      m3_convert<IN, OUT>(v[u].w));
 
-                out[g] = out_io::pack(r);
+                m3_stream_store(&out[g], out_io::pack(r));
             }
         }
     }
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void m3_copy_bytes_kernel(
             uint64_t g = first + u * kThreads;
 
             if (g < words) {
-                output[g] = v[u];
+                m3_stream_store(&output[g], v[u]);
             }
         }
     }
@@ -196,15 +196,16 @@ __global__ __launch_bounds__(256) void m3_copy_bytes_kernel(
 
 template <uint32_t IN, uint32_t OUT>
 void m3_launch_cast_vec(m3_hip_device *device, const uint8_t *input,
-                        uint8_t *output, uint64_t count, uint32_t blocks)
+                        uint8_t *output, uint64_t count, uint32_t blocks,
+                        hipEvent_t start, hipEvent_t stop)
 {
-    hipLaunchKernelGGL((m3_cast_vec_kernel<IN, OUT>), dim3(blocks),
-                       dim3(kThreads), 0, device->stream, input, output,
-                       count, count / 4U);
+    hipExtLaunchKernelGGL((m3_cast_vec_kernel<IN, OUT>), dim3(blocks),
+                          dim3(kThreads), 0, device->stream, start, stop, 0U,
+                          input, output, count, count / 4U);
 }
 
 typedef void (*m3_cast_launcher)(m3_hip_device *, const uint8_t *, uint8_t *,
-                                 uint64_t, uint32_t);
+                                 uint64_t, uint32_t, hipEvent_t, hipEvent_t);
 
 m3_cast_launcher m3_cast_vec_launcher(uint32_t in, uint32_t out)
 {
@@ -268,11 +269,12 @@ int m3_launch_unary(m3_hip_device *device, const m3_hip_view *input,
 
         return m3_hip_launch(
             device, name,
-            [&]() {
-                hipLaunchKernelGGL(m3_copy_bytes_kernel, dim3(blocks),
-                                   dim3(kThreads), 0, device->stream,
-                                   (const uint4 *)in, (uint4 *)out, words,
-                                   in + words * 16U, out + words * 16U, tail);
+            [&](hipEvent_t start, hipEvent_t stop) {
+                hipExtLaunchKernelGGL(m3_copy_bytes_kernel, dim3(blocks),
+                                      dim3(kThreads), 0, device->stream, start,
+                                      stop, 0U, (const uint4 *)in,
+                                      (uint4 *)out, words, in + words * 16U,
+                                      out + words * 16U, tail);
             },
             message, capacity);
     }
@@ -291,8 +293,10 @@ int m3_launch_unary(m3_hip_device *device, const m3_hip_view *input,
 
             return m3_hip_launch(
                 device, name,
-                [&]() { launcher(device, in, out, count, blocks); }, message,
-                capacity);
+                [&](hipEvent_t start, hipEvent_t stop) {
+                    launcher(device, in, out, count, blocks, start, stop);
+                },
+                message, capacity);
         }
     }
     m3_strided_args args;
@@ -312,9 +316,10 @@ int m3_launch_unary(m3_hip_device *device, const m3_hip_view *input,
 
     return m3_hip_launch(
         device, name,
-        [&]() {
-            hipLaunchKernelGGL(m3_cast_strided_kernel, dim3(blocks),
-                               dim3(256), 0, device->stream, args, !same);
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL(m3_cast_strided_kernel, dim3(blocks),
+                                  dim3(256), 0, device->stream, start, stop,
+                                  0U, args, !same);
         },
         message, capacity);
 }

@@ -344,10 +344,11 @@ extern "C" int m3_hip_fill_zero(m3_hip_device *device,
 
     return m3_hip_launch(
         device, "m3_fill_zero",
-        [&]() {
-            hipLaunchKernelGGL(m3_fill_zero_kernel, dim3(blocks), dim3(256),
-                               0, device->stream, (uint4 *)device_destination,
-                               words, tail_pointer, tail);
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL(m3_fill_zero_kernel, dim3(blocks), dim3(256),
+                                  0, device->stream, start, stop, 0U,
+                                  (uint4 *)device_destination, words,
+                                  tail_pointer, tail);
         },
         message, capacity);
 }
@@ -482,22 +483,26 @@ __device__ __forceinline__ uint32_t m3_scan_load(const uint8_t *p,
     return m3_load_as_f32_bits(raw, dtype);
 }
 
-__device__ __forceinline__ bool m3_scan_offends(uint32_t bits, uint32_t kind)
+/* 1 when the element offends the scan's condition, else 0. */
+__device__ __forceinline__ uint32_t m3_scan_offends(uint32_t bits,
+                                                    uint32_t kind)
 {
     if (kind == M3_HIP_SCAN_NAN) {
-        return m3_f32_is_nan_bits(bits);
+        return m3_f32_is_nan_bits(bits) ? 1U : 0U;
     }
     /* finite and -2^31 <= v < 2^31 */
     float v = m3_bits_f32(bits);
 
-    return !((bits & 0x7f800000U) != 0x7f800000U && v >= -2147483648.0F &&
-             v < 2147483648.0F);
+    return ((bits & 0x7f800000U) != 0x7f800000U && v >= -2147483648.0F &&
+            v < 2147483648.0F)
+               ? 0U
+               : 1U;
 }
 
 __global__ void m3_scan_kernel(m3_scan_args args)
 {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    bool found = false;
+    uint32_t found = 0U;
 
     for (uint64_t flat = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
          flat < args.count; flat += stride) {
@@ -514,7 +519,7 @@ __global__ void m3_scan_kernel(m3_scan_args args)
         found |= m3_scan_offends(m3_scan_load(args.base + offset, args.dtype),
                                  args.kind);
     }
-    if (__any(found) && found) {
+    if (__any(found != 0U) && found != 0U) {
         atomicOr(args.flag, 1U);
     }
 }
@@ -527,7 +532,7 @@ __global__ void m3_scan_f32_contiguous_kernel(const uint4 *data,
                                               uint32_t kind, uint32_t *flag)
 {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    bool found = false;
+    uint32_t found = 0U;
 
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
          i < quads; i += stride) {
@@ -539,7 +544,7 @@ __global__ void m3_scan_f32_contiguous_kernel(const uint4 *data,
     if (blockIdx.x == 0U && threadIdx.x < tail_count) {
         found |= m3_scan_offends(tail[threadIdx.x], kind);
     }
-    if (__any(found) && found) {
+    if (__any(found != 0U) && found != 0U) {
         atomicOr(flag, 1U);
     }
 }
@@ -589,10 +594,10 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
     }
     code = m3_hip_launch(
         device, "m3_clear_flags",
-        [&]() {
-            hipLaunchKernelGGL(m3_clear_flags_kernel, dim3(1), dim3(64), 0,
-                               device->stream, device->scan_flags,
-                               (uint32_t)count);
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL(m3_clear_flags_kernel, dim3(1), dim3(64), 0,
+                                  device->stream, start, stop, 0U,
+                                  device->scan_flags, (uint32_t)count);
         },
         message, capacity);
     for (size_t i = 0U; code == M3_HIP_OK && i < count; ++i) {
@@ -620,12 +625,13 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
 
             code = m3_hip_launch(
                 device, "m3_scan_f32",
-                [&]() {
-                    hipLaunchKernelGGL(
-                        m3_scan_f32_contiguous_kernel, dim3(blocks),
-                        dim3(256), 0, device->stream, (const uint4 *)base,
-                        quads, (const uint32_t *)base + quads * 4U, tail,
-                        kinds[i], flag);
+                [&](hipEvent_t start, hipEvent_t stop) {
+                    hipExtLaunchKernelGGL(m3_scan_f32_contiguous_kernel,
+                                          dim3(blocks), dim3(256), 0,
+                                          device->stream, start, stop, 0U,
+                                          (const uint4 *)base, quads,
+                                          (const uint32_t *)base + quads * 4U,
+                                          tail, kinds[i], flag);
                 },
                 message, capacity);
         } else {
@@ -647,9 +653,10 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
 
             code = m3_hip_launch(
                 device, "m3_scan_strided",
-                [&]() {
-                    hipLaunchKernelGGL(m3_scan_kernel, dim3(blocks),
-                                       dim3(256), 0, device->stream, args);
+                [&](hipEvent_t start, hipEvent_t stop) {
+                    hipExtLaunchKernelGGL(m3_scan_kernel, dim3(blocks),
+                                          dim3(256), 0, device->stream, start,
+                                          stop, 0U, args);
                 },
                 message, capacity);
         }
@@ -693,13 +700,17 @@ int m3_hip_time_begin(m3_hip_device *device, const char *name,
     if (!device->timing) {
         return M3_HIP_OK;
     }
-    if (m3_hip_take_event(device, &slot->start) != M3_HIP_OK ||
-        m3_hip_take_event(device, &slot->stop) != M3_HIP_OK) {
+    if (m3_hip_take_event(device, &slot->start) != M3_HIP_OK) {
+        slot->start = nullptr;
         return M3_HIP_RUNTIME;
     }
-    return hipEventRecord(slot->start, device->stream) == hipSuccess
-               ? M3_HIP_OK
-               : M3_HIP_RUNTIME;
+    if (m3_hip_take_event(device, &slot->stop) != M3_HIP_OK) {
+        device->spare_events.push_back(slot->start);
+        slot->start = nullptr;
+        slot->stop = nullptr;
+        return M3_HIP_RUNTIME;
+    }
+    return M3_HIP_OK;
 }
 
 void m3_hip_time_end(m3_hip_device *device, m3_hip_pending_time *slot)
@@ -707,7 +718,6 @@ void m3_hip_time_end(m3_hip_device *device, m3_hip_pending_time *slot)
     if (slot->start == nullptr) {
         return;
     }
-    (void)hipEventRecord(slot->stop, device->stream);
     device->pending.push_back(*slot);
 }
 
@@ -726,7 +736,13 @@ static void m3_hip_fold_pending(m3_hip_device *device)
         float ms = 0.0F;
         bool found = false;
 
-        (void)hipEventElapsedTime(&ms, slot.start, slot.stop);
+        device->spare_events.push_back(slot.start);
+        device->spare_events.push_back(slot.stop);
+        /* a launch that failed never recorded its events: not counted */
+        if (hipEventElapsedTime(&ms, slot.start, slot.stop) != hipSuccess) {
+            (void)hipGetLastError();
+            continue;
+        }
         for (m3_hip_time_total &total : device->totals) {
             if (total.name == slot.name) {
                 total.launches += 1U;
@@ -738,8 +754,6 @@ static void m3_hip_fold_pending(m3_hip_device *device)
         if (!found) {
             device->totals.push_back({slot.name, 1U, (double)ms});
         }
-        device->spare_events.push_back(slot.start);
-        device->spare_events.push_back(slot.stop);
     }
     device->pending.clear();
 }

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void m3_snake1d_vec_kernel(
                 y.y = m3_snake(x[u].y, alpha[u], inverse);
                 y.z = m3_snake(x[u].z, alpha[u], inverse);
                 y.w = m3_snake(x[u].w, alpha[u], inverse);
-                a.output[g] = y;
+                m3_stream_store(&a.output[g], y);
             }
         }
     }
@@ -179,9 +179,10 @@ extern "C" int m3_hip_launch_snake1d(m3_hip_device *device,
 
         return m3_hip_launch(
             device, "m3_snake1d",
-            [&]() {
-                hipLaunchKernelGGL(m3_snake1d_vec_kernel, dim3(blocks),
-                                   dim3(kThreads), 0, device->stream, args);
+            [&](hipEvent_t start, hipEvent_t stop) {
+                hipExtLaunchKernelGGL(m3_snake1d_vec_kernel, dim3(blocks),
+                                      dim3(kThreads), 0, device->stream, start,
+                                      stop, 0U, args);
             },
             message, capacity);
     }
@@ -202,9 +203,10 @@ extern "C" int m3_hip_launch_snake1d(m3_hip_device *device,
 
     return m3_hip_launch(
         device, "m3_snake1d_strided",
-        [&]() {
-            hipLaunchKernelGGL(m3_snake1d_general_kernel, dim3(blocks),
-                               dim3(256), 0, device->stream, general);
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL(m3_snake1d_general_kernel, dim3(blocks),
+                                  dim3(256), 0, device->stream, start, stop,
+                                  0U, general);
         },
         message, capacity);
 }

@@ -20,15 +20,21 @@
  *     is one, which needs sum = 2^k where 1/sum is exact; the double
  *     product errs by under 2^-52).
  *
- * Tiled kernel (rows contiguous along the last axis, uniform row stride,
- * width <= 8192): a 256-thread workgroup owns a tile of rows; each wave
- * owns rows w, w+4, ... of the tile; phase 1 loads a row with 16-byte
- * accesses (8-byte for 16-bit dtypes), reduces max and k with cross-lane
- * shuffles, and writes e_j to LDS; phase 2 has one lane per row sum its
- * row in order from LDS and form 1/sum in double; phase 3 reads e_j back,
- * scales, rounds to the output dtype and stores coalesced. LDS rows are
- * padded by 4 floats so the per-row walks of phase 2 hit distinct banks.
- * Any other layout runs one thread per row through the three passes.
+ * Kernels, chosen by layout and width (rows contiguous along the last axis
+ * with a uniform row stride and width a multiple of 4 use the first two):
+ *   - width <= 2048: wave-independent rows (m3_softmax_rows_kernel). A wave
+ *     holds R rows in VGPRs, reduces max and k with shuffles, forms e_j in
+ *     place and streams 256-column chunks through a wave-private LDS tile
+ *     where one lane per row continues the in-order sum; no workgroup
+ *     barrier separates the phases, so waves overlap memory and arithmetic.
+ *   - width <= 8192: a 256-thread workgroup owns a tile of rows; each wave
+ *     owns rows w, w+4, ... of the tile; phase 1 loads a row with 16-byte
+ *     accesses (8-byte for 16-bit dtypes), reduces max and k, and writes
+ *     e_j to LDS; phase 2 has one lane per row sum its row in order from
+ *     LDS and form 1/sum in double; phase 3 reads e_j back, scales, rounds
+ *     to the output dtype and stores coalesced. LDS rows are padded by 4
+ *     floats so the per-row walks of phase 2 hit distinct banks.
+ *   - any other layout: one thread per row through the three passes.
  */
 #include "m3_hip_internal.h"
 #include "m3_libm.h"
@@ -39,11 +45,14 @@ namespace {
 
 constexpr uint32_t kThreads = 256U;
 constexpr uint32_t kWaves = kThreads / 64U;
-constexpr uint32_t kLdsBudget = 65536U; /* dynamic LDS cap per workgroup */
 constexpr uint32_t kStaticLds = 1024U; /* room for the static arrays */
+constexpr uint32_t kTiledLdsCap = 65536U; /* dynamic LDS of the tiled kernel */
 constexpr uint32_t kMaxTileRows = 16U;
 constexpr uint32_t kMaxWidth = 8192U;
 constexpr uint32_t kPad = 4U;
+constexpr uint32_t kChunk = 256U;         /* columns per LDS chunk */
+constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
+constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
 
 struct m3_softmax_args {
     const uint8_t *input;
@@ -74,6 +83,15 @@ __device__ __forceinline__ uint32_t m3_wave_sum(uint32_t v)
     return v;
 }
 
+__device__ __forceinline__ uint32_t m3_wave_max_u32(uint32_t v)
+{
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        v = max(v, (uint32_t)__shfl_xor((int)v, mask, 64));
+    }
+    return v;
+}
+
 /* Four consecutive row elements starting at column c, as F32. */
 template <bool F32IO>
 __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
@@ -91,12 +109,14 @@ __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
         m3_bits_f32(m3_load_as_f32_bits(h.y >> 16U, dtype)));
 }
 
+/* Four results at column c, rounded to the output dtype (streaming
+ * stores). */
 template <bool F32IO>
 __device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint32_t c,
                                                   uint32_t dtype, float4 p)
 {
     if (F32IO || dtype == M3N_F32) {
-        *(float4 *)(row + (uint64_t)c * 4U) = p;
+        m3_stream_store((float4 *)(row + (uint64_t)c * 4U), p);
         return;
     }
     uint2 packed;
@@ -105,7 +125,7 @@ __device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint32_t c,
                (m3_store_from_f32_bits(m3_f32_bits(p.y), dtype) << 16U);
     packed.y = m3_store_from_f32_bits(m3_f32_bits(p.z), dtype) |
                (m3_store_from_f32_bits(m3_f32_bits(p.w), dtype) << 16U);
-    *(uint2 *)(row + (uint64_t)c * 2U) = packed;
+    m3_stream_store((uint2 *)(row + (uint64_t)c * 2U), packed);
 }
 
 __device__ __forceinline__ float m3_softmax_scale(float e, double inverse)
@@ -280,70 +300,119 @@ __global__ __launch_bounds__(256) void m3_softmax_tiled_kernel(
     }
 }
 
-/* Register-resident rows (width <= 256 * VPL, a multiple of 4): each wave
- * owns RPW consecutive rows of a 4*RPW-row tile and keeps them in VGPRs
- * (VPL float4 per lane per row), issuing every load of its rows before
- * the first use. e_j goes to LDS only for the in-order sum, which lanes
- * 0..tile-1 of wave 0 compute; p_j is then formed from the registers. */
-template <int VPL, int RPW, bool F32IO>
+/* Sum of the first n (a multiple of 4, at most 256) floats of an LDS line,
+ * continuing the left-to-right F32 sum s. Full 256-element chunks keep
+ * eight 16-byte loads in flight ahead of the dependent additions. */
+__device__ __forceinline__ float m3_chunk_sum(float s, const float *line,
+                                              uint32_t n)
+{
+    if (n == kChunk) {
+        float4 ahead[8];
+
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ahead[i] = *(const float4 *)(line + 4 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < (int)kChunk / 4; ++i) {
+            float4 e = ahead[i & 7];
+
+            if (i + 8 < (int)kChunk / 4) {
+                ahead[i & 7] = *(const float4 *)(line + 4 * (i + 8));
+            }
+            s = s + e.x;
+            s = s + e.y;
+            s = s + e.z;
+            s = s + e.w;
+        }
+        return s;
+    }
+    for (uint32_t c = 0U; c < n; c += 4U) {
+        float4 e = *(const float4 *)(line + c);
+
+        s = s + e.x;
+        s = s + e.y;
+        s = s + e.z;
+        s = s + e.w;
+    }
+    return s;
+}
+
+/* Orders this wave's LDS writes before its later LDS reads of other lanes'
+ * data (the LDS executes one wave's operations in issue order). */
+__device__ __forceinline__ void m3_wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/* Wave-independent rows (width <= 256 * VPL, a multiple of 4). Each wave
+ * takes R consecutive rows at a time and keeps them in VGPRs (VPL float4
+ * per lane per row): it reduces max with shuffles, forms e_j in place,
+ * then walks the row in 256-column chunks, writing each chunk of its R
+ * rows to a wave-private LDS tile where lanes 0..R-1 continue their row's
+ * left-to-right sum. The sum stops after the row's last nonzero e_j: the
+ * trailing terms are +0 and leave a nonnegative F32 sum unchanged, so the
+ * result is identical while masked (causal) rows cost half. p_j is formed
+ * from the registers and streamed out with nontemporal stores. No
+ * workgroup barrier is needed after the table copy, so waves of one CU
+ * overlap their loads, arithmetic and sums freely. */
+template <int VPL, int R, bool F32IO>
 __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     m3_softmax_args a)
 {
-    extern __shared__ float lds[];
-    __shared__ m3_row_state state[4 * RPW];
+    __shared__ float tiles[kWaves][R][kLine];
     __shared__ uint64_t exp_table[32];
-    constexpr uint32_t kTile = 4U * RPW;
     const uint32_t lane = threadIdx.x & 63U;
     const uint32_t wave = threadIdx.x >> 6U;
     const uint32_t width = a.width;
-    const uint32_t pitch = width + kPad;
     const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
     const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
-    const uint32_t out_size = out_dtype == M3N_F32 ? 4U : 2U;
+    const uint64_t out_pitch =
+        (uint64_t)width * (out_dtype == M3N_F32 ? 4U : 2U);
+    const uint64_t tasks = (a.rows + R - 1U) / R;
+    float *tile = &tiles[wave][0][0];
 
     if (threadIdx.x < 32U) {
         exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
     }
-    for (uint64_t tile = blockIdx.x; tile * kTile < a.rows;
-         tile += gridDim.x) {
-        const uint64_t first_row = tile * kTile;
-        float4 v[RPW][VPL];
-        float maximum[RPW];
+    __syncthreads();
+    for (uint64_t task = (uint64_t)blockIdx.x * kWaves + wave; task < tasks;
+         task += (uint64_t)gridDim.x * kWaves) {
+        const uint64_t first_row = task * R;
+        /* rows of this task that exist (the last task may be partial) */
+        const uint32_t present = (uint32_t)min((uint64_t)R, a.rows - first_row);
+        const uint8_t *in = a.input + first_row * a.row_stride;
+        float4 v[R][VPL];
+        float maximum[R];
+        uint32_t length[R]; /* elements up to the last nonzero e_j */
 
-        __syncthreads();
 #pragma unroll
-        for (int k = 0; k < RPW; ++k) {
-            const uint64_t row = first_row + wave * RPW + k;
-            const uint8_t *in = a.input + row * a.row_stride;
-
+        for (int k = 0; k < R; ++k) {
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
-                const uint32_t c = lane * 4U + 256U * j;
+                const uint32_t c = lane * 4U + kChunk * j;
 
                 v[k][j] = make_float4(-INFINITY, -INFINITY, -INFINITY,
                                       -INFINITY);
-                if (row < a.rows && c < width) {
+                if ((uint32_t)k < present && c < width) {
                     v[k][j] = m3_softmax_load4<F32IO>(in, c, in_dtype);
                 }
             }
+            in += a.row_stride;
         }
 #pragma unroll
-        for (int k = 0; k < RPW; ++k) {
-            const uint32_t local = wave * RPW + k;
+        for (int k = 0; k < R; ++k) {
             float m = -INFINITY;
-            uint32_t infinities = 0U;
+            uint32_t last = 0U; /* 1 + index of the last nonzero float4 */
 
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
                 m = fmaxf(m, fmaxf(fmaxf(v[k][j].x, v[k][j].y),
                                    fmaxf(v[k][j].z, v[k][j].w)));
-                infinities += (v[k][j].x == INFINITY) +
-                              (v[k][j].y == INFINITY) +
-                              (v[k][j].z == INFINITY) +
-                              (v[k][j].w == INFINITY);
             }
             m = m3_wave_max(m);
-            infinities = m3_wave_sum(infinities);
             maximum[k] = m;
             if (m != INFINITY && m != -INFINITY) {
 #pragma unroll
@@ -352,53 +421,74 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
                     v[k][j].y = m3_expf_with_table(v[k][j].y - m, exp_table);
                     v[k][j].z = m3_expf_with_table(v[k][j].z - m, exp_table);
                     v[k][j].w = m3_expf_with_table(v[k][j].w - m, exp_table);
+
+                    uint32_t nonzero =
+                        m3_f32_bits(v[k][j].x) | m3_f32_bits(v[k][j].y) |
+                        m3_f32_bits(v[k][j].z) | m3_f32_bits(v[k][j].w);
+
+                    last = nonzero != 0U ? lane + 64U * j + 1U : last;
                 }
             }
-            float *line = lds + (uint64_t)local * pitch;
+            length[k] = m3_wave_max_u32(last) * 4U;
+        }
+        uint32_t my_length = 0U;
+        uint32_t wave_length = 0U;
 
 #pragma unroll
-            for (int j = 0; j < VPL; ++j) {
-                const uint32_t c = lane * 4U + 256U * j;
-
-                if (c < width) {
-                    *(float4 *)(line + c) = v[k][j];
-                }
-            }
-            if (lane == 0U) {
-                state[local].maximum = m;
-                state[local].infinities = infinities;
-            }
+        for (int k = 0; k < R; ++k) {
+            my_length = lane == (uint32_t)k ? length[k] : my_length;
+            wave_length = max(wave_length, length[k]);
         }
-        __syncthreads();
-        if (threadIdx.x < kTile && first_row + threadIdx.x < a.rows) {
-            m3_row_state *s = &state[threadIdx.x];
-            const float m = s->maximum;
+        float sum = 0.0F;
 
-            if (m != INFINITY && m != -INFINITY) {
-                s->inverse = 1.0 / (double)m3_row_sum_in_order(
-                                       lds + (uint64_t)threadIdx.x * pitch,
-                                       width);
-            } else if (m == INFINITY) {
-                s->one_over_count = 1.0F / (float)s->infinities;
-            }
-        }
-        __syncthreads();
 #pragma unroll
-        for (int k = 0; k < RPW; ++k) {
-            const uint32_t local = wave * RPW + k;
-            const uint64_t row = first_row + local;
+        for (int j = 0; j < VPL; ++j) {
+            const uint32_t base = kChunk * j;
+
+            if (base >= wave_length) {
+                break;
+            }
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                *(float4 *)(tile + k * kLine + lane * 4U) = v[k][j];
+            }
+            m3_wave_sync();
+            if (lane < (uint32_t)R && base < my_length) {
+                const uint32_t n = min(my_length - base, kChunk);
+
+                sum = m3_chunk_sum(sum, tile + lane * kLine, n);
+            }
+            m3_wave_sync();
+        }
+        const double inverse_of_lane = 1.0 / (double)sum;
+
+        uint8_t *out = a.output + first_row * out_pitch;
+
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const double inverse = __shfl(inverse_of_lane, k, 64);
             const float m = maximum[k];
-            const double inverse = state[local].inverse;
-            const float one_over_count = state[local].one_over_count;
-            uint8_t *out = a.output + row * (uint64_t)width * out_size;
+            float one_over_count = 0.0F;
 
-            if (row >= a.rows) {
+            if (m == INFINITY) {
+                uint32_t count = 0U;
+
+#pragma unroll
+                for (int j = 0; j < VPL; ++j) {
+                    count += (v[k][j].x == INFINITY) +
+                             (v[k][j].y == INFINITY) +
+                             (v[k][j].z == INFINITY) +
+                             (v[k][j].w == INFINITY);
+                }
+                one_over_count = 1.0F / (float)m3_wave_sum(count);
+            }
+            if ((uint32_t)k >= present) {
                 continue;
             }
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
-                const uint32_t c = lane * 4U + 256U * j;
-                float4 e = v[k][j];
+                const uint32_t c = lane * 4U + kChunk * j;
+                const float4 e = v[k][j];
                 float4 p;
 
                 if (c >= width) {
@@ -419,19 +509,20 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
                 }
                 m3_softmax_store4<F32IO>(out, c, out_dtype, p);
             }
+            out += out_pitch;
         }
     }
 }
 
-typedef void (*m3_softmax_launcher)(dim3, size_t, hipStream_t,
-                                    m3_softmax_args);
+typedef void (*m3_softmax_launcher)(dim3, hipStream_t, hipEvent_t,
+                                    hipEvent_t, m3_softmax_args);
 
-template <int VPL, int RPW, bool F32IO>
-void m3_launch_rows(dim3 grid, size_t lds_bytes, hipStream_t stream,
-                    m3_softmax_args args)
+template <int VPL, int R, bool F32IO>
+void m3_launch_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
+                    hipEvent_t stop, m3_softmax_args args)
 {
-    hipLaunchKernelGGL((m3_softmax_rows_kernel<VPL, RPW, F32IO>), grid,
-                       dim3(kThreads), lds_bytes, stream, args);
+    hipExtLaunchKernelGGL((m3_softmax_rows_kernel<VPL, R, F32IO>), grid,
+                          dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
 struct m3_rows_variant {
@@ -441,13 +532,11 @@ struct m3_rows_variant {
     m3_softmax_launcher other;
 };
 
-/* Register-resident variants, preferred first for each width class. */
+/* Wave-independent variants; the first whose width class fits is used. */
 const m3_rows_variant m3_rows_variants[] = {
-    {1U, 4U, &m3_launch_rows<1, 4, true>, &m3_launch_rows<1, 4, false>},
+    {1U, 8U, &m3_launch_rows<1, 8, true>, &m3_launch_rows<1, 8, false>},
     {2U, 4U, &m3_launch_rows<2, 4, true>, &m3_launch_rows<2, 4, false>},
-    {4U, 4U, &m3_launch_rows<4, 4, true>, &m3_launch_rows<4, 4, false>},
     {4U, 2U, &m3_launch_rows<4, 2, true>, &m3_launch_rows<4, 2, false>},
-    {8U, 2U, &m3_launch_rows<8, 2, true>, &m3_launch_rows<8, 2, false>},
     {8U, 1U, &m3_launch_rows<8, 1, true>, &m3_launch_rows<8, 1, false>},
 };
 
@@ -605,7 +694,6 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
                               : 0U;
         bool f32 = input->dtype == M3_HIP_F32 && output->dtype == M3_HIP_F32;
 
-        budget = budget > kLdsBudget ? kLdsBudget : budget;
         std::memset(&args, 0, sizeof(args));
         args.input = in;
         args.output = out;
@@ -615,24 +703,25 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
         args.in_dtype = input->dtype;
         args.out_dtype = output->dtype;
         for (const m3_rows_variant &variant : m3_rows_variants) {
-            uint32_t tile = 4U * variant.rows_per_wave;
-            size_t lds_bytes = (size_t)tile * pitch_bytes;
-
-            if (width > 256U * variant.vectors_per_lane ||
-                lds_bytes > budget) {
+            if (width > kChunk * variant.vectors_per_lane) {
                 continue;
             }
-            uint64_t tiles = (rows + tile - 1U) / tile;
-            uint64_t cap = (uint64_t)device->compute_units * 8U;
-            dim3 grid((uint32_t)(tiles < cap ? tiles : cap));
+            uint64_t tasks =
+                (rows + variant.rows_per_wave - 1U) / variant.rows_per_wave;
+            uint64_t blocks = (tasks + kWaves - 1U) / kWaves;
+            dim3 grid((uint32_t)(blocks < kMaxGrid ? blocks : kMaxGrid));
             m3_softmax_launcher launcher = f32 ? variant.f32 : variant.other;
 
-            args.tile_rows = tile;
             return m3_hip_launch(
                 device, "m3_softmax_rows",
-                [&]() { launcher(grid, lds_bytes, device->stream, args); },
+                [&](hipEvent_t start, hipEvent_t stop) {
+                    launcher(grid, device->stream, start, stop, args);
+                },
                 message, capacity);
         }
+        /* Rows wider than the register variants: whole rows in LDS,
+         * within the dynamic LDS a launch gets without opting in. */
+        budget = budget > kTiledLdsCap ? kTiledLdsCap : budget;
         uint32_t tile_rows = budget / pitch_bytes;
 
         tile_rows = tile_rows > kMaxTileRows ? kMaxTileRows : tile_rows;
@@ -647,15 +736,17 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
 
             return m3_hip_launch(
                 device, "m3_softmax_rows_lds",
-                [&]() {
+                [&](hipEvent_t start, hipEvent_t stop) {
                     if (f32) {
-                        hipLaunchKernelGGL((m3_softmax_tiled_kernel<true>),
-                                           dim3(blocks), dim3(kThreads),
-                                           lds_bytes, device->stream, args);
+                        hipExtLaunchKernelGGL((m3_softmax_tiled_kernel<true>),
+                                              dim3(blocks), dim3(kThreads),
+                                              lds_bytes, device->stream, start,
+                                              stop, 0U, args);
                     } else {
-                        hipLaunchKernelGGL((m3_softmax_tiled_kernel<false>),
-                                           dim3(blocks), dim3(kThreads),
-                                           lds_bytes, device->stream, args);
+                        hipExtLaunchKernelGGL((m3_softmax_tiled_kernel<false>),
+                                              dim3(blocks), dim3(kThreads),
+                                              lds_bytes, device->stream, start,
+                                              stop, 0U, args);
                     }
                 },
                 message, capacity);
@@ -685,9 +776,10 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
 
     return m3_hip_launch(
         device, "m3_softmax_rows_strided",
-        [&]() {
-            hipLaunchKernelGGL(m3_softmax_general_kernel, dim3(blocks),
-                               dim3(64), 0, device->stream, general);
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL(m3_softmax_general_kernel, dim3(blocks),
+                                  dim3(64), 0, device->stream, start, stop, 0U,
+                                  general);
         },
         message, capacity);
 }

@@ -18,10 +18,9 @@
  *         cosine polynomial selected by the quadrant.
  *
  * These restatements were checked bit for bit against that libm: expf on
- * all 2,239,836,979 floats in (-103.9, 88.7) and sinf on all 2^32 floats,
- * with zero mismatches. The test suite re-checks a dense sample on every
- * run. Inputs outside expf's regular range use the same special cases as
- * the library (-inf and x < log(2^-150) give +0).
+ * every non-NaN float up to log(2^128) (all 3,196,059,650 floats <= 0.5
+ * and all floats in (-103.9, 88.7)) and sinf on all 2^32 floats, with zero
+ * mismatches. The test suite re-checks a dense sample on every run.
  *
  * Valid C11 and HIP C++; under HIP every function is __host__ __device__.
  * All double operations must stay unfused except where fma() is written.
@@ -92,24 +91,38 @@ M3_HD float m3_expf_with_table(float x, const uint64_t *table)
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-    double xd = (double)x;
+    /* The library returns +0 below log(2^-150) (and for -inf). Clamping the
+     * argument at -128 gives the same result without a branch: the
+     * arithmetic below then yields a double near 2^-184.7, which rounds to
+     * +0 in the final conversion, and every x in (-128, log(2^-150)) also
+     * rounds to +0 (checked on all floats). */
+    double xd = (double)fmaxf(x, -128.0F);
     double kd;
     double r;
     double s;
     double z;
     double y;
     uint64_t ki;
-    uint64_t t;
 
-    if (x < -0x1.9fe368p6F) {
-        return 0.0F; /* includes -inf */
-    }
     kd = fma(inv_ln2_n, xd, shift);
     ki = m3_f64_bits(kd);
     kd -= shift;
     r = fma(inv_ln2_n, xd, -kd);
-    t = table[ki % 32U] + (ki << 47U);
-    s = m3_bits_f64(t);
+    /* s = bits(T[ki % 32] + (ki << 47) mod 2^64). The addend's low word is
+     * zero, so only the high word changes: high(T) + (low(ki) << 15). The
+     * device form keeps the two words apart so that this stays a single
+     * 32-bit shift-add. */
+#if defined(__HIP_DEVICE_COMPILE__)
+    {
+        typedef uint32_t m3_words __attribute__((ext_vector_type(2)));
+        m3_words entry = ((const m3_words *)table)[ki % 32U];
+
+        entry.y += (uint32_t)ki << 15U;
+        s = __builtin_bit_cast(double, entry);
+    }
+#else
+    s = m3_bits_f64(table[ki % 32U] + (ki << 47U));
+#endif
     z = fma(c0, r, c1);
     y = fma(c2, r, 1.0);
     y = fma(z, r * r, y);
@@ -131,12 +144,8 @@ M3_LIBM_CONST uint32_t m3_sinf_two_over_pi[24] = {
     0x6295993cU, 0x95993c43U, 0x993c4390U, 0x3c439041U
 };
 
-/* Polynomial coefficients: cosine c0..c4, sine s1..s3. The second set
- * negates the cosine polynomial for quadrants 2 and 3. */
-typedef struct {
-    double c0, c1, c2, c3, c4, s1, s2, s3;
-} m3_sinf_poly;
-
+/* Sine polynomial (even quadrant, odd = 0) or cosine polynomial (odd
+ * quadrant), the cosine negated for quadrants 2 and 3. */
 M3_HD double m3_sinf_eval(double x, double x2, int odd, int negate_cos)
 {
     const double s1 = -0x1.555545995a603p-3;

@@ -274,6 +274,34 @@ def test_softmax_dtypes(hip, dtypes, width):
             "softmax %s w=%d" % (dtypes, width))
 
 
+@pytest.mark.parametrize("width", [4, 200, 260, 1024, 2000, 4096, 6000])
+def test_softmax_zero_tails(hip, width):
+    """Rows whose e_j end in a run of zeros: -inf tails, finite tails that
+    underflow expf to +0, masked blocks inside the row, and cut points at
+    every offset inside a 256-column chunk."""
+    rng = np.random.default_rng(11000 + width)
+    rows = 96
+    logits = (rng.standard_normal((rows, width)) * 3).astype(np.float32)
+    for r in range(rows):
+        cut = 1 + (r * 37 + int(rng.integers(0, width))) % width
+        kind = r % 4
+        if kind == 0:
+            logits[r, cut:] = -np.inf
+        elif kind == 1:
+            logits[r, cut:] = np.float32(-200.0)
+        elif kind == 2:
+            logits[r, cut:] = -np.inf
+            start = int(rng.integers(0, cut))
+            logits[r, start:start + max(1, cut // 3)] = -np.inf
+            logits[r, 0] = 1.0
+        else:
+            logits[r, : cut - 1] = -np.inf
+    views = [ViewSpec(0, m3.F32, (rows, width)),
+             ViewSpec(1, m3.F32, (rows, width))]
+    storages = [as_bytes(logits), np.zeros(logits.nbytes, np.uint8)]
+    compare(hip, m3.OP_SOFTMAX, storages, views, "softmax tails w=%d" % width)
+
+
 def test_softmax_strided_and_in_place(hip):
     rng = np.random.default_rng(9)
     logits = softmax_logits(rng, 64, 1024)
