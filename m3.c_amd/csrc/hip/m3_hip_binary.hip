@@ -116,8 +116,13 @@ __device__ __forceinline__ uint4 m3_operand_load4(const m3_bin_operand &o,
                              : f - m3_fast_div_q(o.period, f) *
                                        o.period.divisor;
 
+        /* a full F32 operand is read once per launch with 16-byte
+         * accesses: streamed; a trailing broadcast operand is reread by
+         * every row: cached (8-byte streaming loads measured slower) */
         if (dtype == M3N_F32) {
-            return *(const uint4 *)(o.base + (uint64_t)index * 4U);
+            const uint4 *p = (const uint4 *)(o.base + (uint64_t)index * 4U);
+
+            return o.mode == M3_BIN_FULL ? m3_stream_load(p) : *p;
         }
         uint2 half = *(const uint2 *)(o.base + (uint64_t)index * 2U);
 

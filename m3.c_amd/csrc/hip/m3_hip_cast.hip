@@ -11,7 +11,8 @@
  *   - float -> float: exact widening to F32, then the bit-exact RNE
  *     narrowing of m3_numeric.h. NaN payloads follow the reference rules.
  * The output is contiguous. A contiguous, aligned input runs the vector
- * kernel (four elements per lane per group, four groups in flight);
+ * kernel (four elements per lane per group, four groups in flight, output
+ * written with streaming stores);
  * strided inputs run a per-element kernel over the coalesced index space.
  */
 #include "m3_hip_internal.h"
@@ -26,18 +27,22 @@ constexpr uint32_t kUnroll = 4U;
 template <uint32_t DT>
 struct m3_vec_io;
 
-/* Four 4-byte elements: one 16-byte access. */
+/* Four 4-byte elements: one 16-byte access, read with a streaming load
+ * (each input byte is read once). */
 template <>
 struct m3_vec_io<4U> {
     using type = uint4;
+    __device__ static type load(const type *p) { return m3_stream_load(p); }
     __device__ static uint4 unpack(type v) { return v; }
     __device__ static type pack(uint4 v) { return v; }
 };
 
-/* Four 2-byte elements: one 8-byte access. */
+/* Four 2-byte elements: one 8-byte access, read with an ordinary load
+ * (8-byte streaming loads measured slower on gfx950). */
 template <>
 struct m3_vec_io<2U> {
     using type = uint2;
+    __device__ static type load(const type *p) { return *p; }
     __device__ static uint4 unpack(type v)
     {
         return make_uint4(v.x & 0xffffU, v.x >> 16U, v.y & 0xffffU,
@@ -81,7 +86,7 @@ __global__ __launch_bounds__(256) void m3_cast_vec_kernel(
             uint64_t g = first + u * kThreads;
 
             if (g < groups) {
-                v[u] = in_io::unpack(in[g]);
+                v[u] = in_io::unpack(in_io::load(&in[g]));
             }
         }
 #pragma unroll
@@ -177,7 +182,7 @@ __global__ __launch_bounds__(256) void m3_copy_bytes_kernel(
             uint64_t g = first + u * kThreads;
 
             if (g < words) {
-                v[u] = input[g];
+                v[u] = m3_stream_load(&input[g]);
             }
         }
 #pragma unroll

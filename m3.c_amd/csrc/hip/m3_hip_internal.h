@@ -111,6 +111,22 @@ __device__ __forceinline__ void m3_stream_store(float4 *p, float4 v)
     __builtin_nontemporal_store(w, (m3_f32x4 *)p);
 }
 
+/* Streaming loads for inputs that one kernel reads exactly once (not for
+ * broadcast operands, which stay cached across the grid). */
+__device__ __forceinline__ uint4 m3_stream_load(const uint4 *p)
+{
+    m3_u32x4 w = __builtin_nontemporal_load((const m3_u32x4 *)p);
+
+    return make_uint4(w.x, w.y, w.z, w.w);
+}
+
+__device__ __forceinline__ uint2 m3_stream_load(const uint2 *p)
+{
+    m3_u32x2 w = __builtin_nontemporal_load((const m3_u32x2 *)p);
+
+    return make_uint2(w.x, w.y);
+}
+
 /* Unsigned 32-bit division by an invariant divisor d >= 1:
  * q = (umulhi(n, mul) + n) >> shift with shift = ceil(log2 d) and
  * mul = floor(2^32 (2^shift - d) / d) + 1; the sum is formed in 64 bits,

@@ -95,12 +95,12 @@ __device__ __forceinline__ uint32_t m3_wave_max_u32(uint32_t v)
 /* Four consecutive row elements starting at column c, as F32. */
 template <bool F32IO>
 __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
-                                                   uint32_t c, uint32_t dtype)
+                                                   uint64_t c, uint32_t dtype)
 {
     if (F32IO || dtype == M3N_F32) {
-        return *(const float4 *)(row + (uint64_t)c * 4U);
+        return *(const float4 *)(row + c * 4U);
     }
-    uint2 h = *(const uint2 *)(row + (uint64_t)c * 2U);
+    uint2 h = *(const uint2 *)(row + c * 2U);
 
     return make_float4(
         m3_bits_f32(m3_load_as_f32_bits(h.x & 0xffffU, dtype)),
@@ -112,11 +112,11 @@ __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
 /* Four results at column c, rounded to the output dtype (streaming
  * stores). */
 template <bool F32IO>
-__device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint32_t c,
+__device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint64_t c,
                                                   uint32_t dtype, float4 p)
 {
     if (F32IO || dtype == M3N_F32) {
-        m3_stream_store((float4 *)(row + (uint64_t)c * 4U), p);
+        m3_stream_store((float4 *)(row + c * 4U), p);
         return;
     }
     uint2 packed;
@@ -125,7 +125,7 @@ __device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint32_t c,
                (m3_store_from_f32_bits(m3_f32_bits(p.y), dtype) << 16U);
     packed.y = m3_store_from_f32_bits(m3_f32_bits(p.z), dtype) |
                (m3_store_from_f32_bits(m3_f32_bits(p.w), dtype) << 16U);
-    m3_stream_store((uint2 *)(row + (uint64_t)c * 2U), packed);
+    m3_stream_store((uint2 *)(row + c * 2U), packed);
 }
 
 __device__ __forceinline__ float m3_softmax_scale(float e, double inverse)
@@ -300,40 +300,57 @@ __global__ __launch_bounds__(256) void m3_softmax_tiled_kernel(
     }
 }
 
+/* Adds four floats to s in order. */
+__device__ __forceinline__ float m3_add4(float s, float4 e)
+{
+    s = s + e.x;
+    s = s + e.y;
+    s = s + e.z;
+    return s + e.w;
+}
+
 /* Sum of the first n (a multiple of 4, at most 256) floats of an LDS line,
- * continuing the left-to-right F32 sum s. Full 256-element chunks keep
- * eight 16-byte loads in flight ahead of the dependent additions. */
+ * continuing the left-to-right F32 sum s. A full chunk keeps DEPTH 16-byte
+ * loads in flight ahead of the dependent additions; a partial chunk (the
+ * end of a trimmed row) issues four loads per 16 elements before adding
+ * them, so LDS latency is paid once per 16 additions, not per 4. */
+template <int DEPTH>
 __device__ __forceinline__ float m3_chunk_sum(float s, const float *line,
                                               uint32_t n)
 {
     if (n == kChunk) {
-        float4 ahead[8];
+        float4 ahead[DEPTH];
 
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < DEPTH; ++i) {
             ahead[i] = *(const float4 *)(line + 4 * i);
         }
 #pragma unroll
         for (int i = 0; i < (int)kChunk / 4; ++i) {
-            float4 e = ahead[i & 7];
+            float4 e = ahead[i % DEPTH];
 
-            if (i + 8 < (int)kChunk / 4) {
-                ahead[i & 7] = *(const float4 *)(line + 4 * (i + 8));
+            if (i + DEPTH < (int)kChunk / 4) {
+                ahead[i % DEPTH] = *(const float4 *)(line + 4 * (i + DEPTH));
             }
-            s = s + e.x;
-            s = s + e.y;
-            s = s + e.z;
-            s = s + e.w;
+            s = m3_add4(s, e);
         }
         return s;
     }
-    for (uint32_t c = 0U; c < n; c += 4U) {
-        float4 e = *(const float4 *)(line + c);
+    uint32_t c = 0U;
 
-        s = s + e.x;
-        s = s + e.y;
-        s = s + e.z;
-        s = s + e.w;
+    for (; c + 16U <= n; c += 16U) {
+        float4 a = *(const float4 *)(line + c);
+        float4 b = *(const float4 *)(line + c + 4U);
+        float4 d = *(const float4 *)(line + c + 8U);
+        float4 f = *(const float4 *)(line + c + 12U);
+
+        s = m3_add4(s, a);
+        s = m3_add4(s, b);
+        s = m3_add4(s, d);
+        s = m3_add4(s, f);
+    }
+    for (; c < n; c += 4U) {
+        s = m3_add4(s, *(const float4 *)(line + c));
     }
     return s;
 }
@@ -358,7 +375,7 @@ __device__ __forceinline__ void m3_wave_sync()
  * from the registers and streamed out with nontemporal stores. No
  * workgroup barrier is needed after the table copy, so waves of one CU
  * overlap their loads, arithmetic and sums freely. */
-template <int VPL, int R, bool F32IO>
+template <int VPL, int R, int DEPTH, bool F32IO>
 __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     m3_softmax_args a)
 {
@@ -369,8 +386,9 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     const uint32_t width = a.width;
     const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
     const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
-    const uint64_t out_pitch =
-        (uint64_t)width * (out_dtype == M3N_F32 ? 4U : 2U);
+    const uint32_t in_size = in_dtype == M3N_F32 ? 4U : 2U;
+    const uint32_t out_size = out_dtype == M3N_F32 ? 4U : 2U;
+    const uint64_t out_pitch = (uint64_t)width * out_size;
     const uint64_t tasks = (a.rows + R - 1U) / R;
     float *tile = &tiles[wave][0][0];
 
@@ -382,8 +400,12 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
          task += (uint64_t)gridDim.x * kWaves) {
         const uint64_t first_row = task * R;
         /* rows of this task that exist (the last task may be partial) */
-        const uint32_t present = (uint32_t)min((uint64_t)R, a.rows - first_row);
-        const uint8_t *in = a.input + first_row * a.row_stride;
+        const uint32_t present =
+            (uint32_t)min((uint64_t)R, a.rows - first_row);
+        /* this lane's first column of the task's first row; chunk j of a
+         * row is a constant offset from it */
+        const uint8_t *in = a.input + first_row * a.row_stride +
+                            (uint64_t)lane * 4U * in_size;
         float4 v[R][VPL];
         float maximum[R];
         uint32_t length[R]; /* elements up to the last nonzero e_j */
@@ -397,7 +419,8 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
                 v[k][j] = make_float4(-INFINITY, -INFINITY, -INFINITY,
                                       -INFINITY);
                 if ((uint32_t)k < present && c < width) {
-                    v[k][j] = m3_softmax_load4<F32IO>(in, c, in_dtype);
+                    v[k][j] = m3_softmax_load4<F32IO>(
+                        in, (uint64_t)kChunk * j, in_dtype);
                 }
             }
             in += a.row_stride;
@@ -456,13 +479,14 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
             if (lane < (uint32_t)R && base < my_length) {
                 const uint32_t n = min(my_length - base, kChunk);
 
-                sum = m3_chunk_sum(sum, tile + lane * kLine, n);
+                sum = m3_chunk_sum<DEPTH>(sum, tile + lane * kLine, n);
             }
             m3_wave_sync();
         }
         const double inverse_of_lane = 1.0 / (double)sum;
 
-        uint8_t *out = a.output + first_row * out_pitch;
+        uint8_t *out = a.output + first_row * out_pitch +
+                       (uint64_t)lane * 4U * out_size;
 
 #pragma unroll
         for (int k = 0; k < R; ++k) {
@@ -507,7 +531,8 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
                     p.z = m3_softmax_scale(e.z, inverse);
                     p.w = m3_softmax_scale(e.w, inverse);
                 }
-                m3_softmax_store4<F32IO>(out, c, out_dtype, p);
+                m3_softmax_store4<F32IO>(out, (uint64_t)kChunk * j,
+                                         out_dtype, p);
             }
             out += out_pitch;
         }
@@ -517,12 +542,13 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
 typedef void (*m3_softmax_launcher)(dim3, hipStream_t, hipEvent_t,
                                     hipEvent_t, m3_softmax_args);
 
-template <int VPL, int R, bool F32IO>
+template <int VPL, int R, int DEPTH, bool F32IO>
 void m3_launch_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                     hipEvent_t stop, m3_softmax_args args)
 {
-    hipExtLaunchKernelGGL((m3_softmax_rows_kernel<VPL, R, F32IO>), grid,
-                          dim3(kThreads), 0, stream, start, stop, 0U, args);
+    hipExtLaunchKernelGGL((m3_softmax_rows_kernel<VPL, R, DEPTH, F32IO>),
+                          grid, dim3(kThreads), 0, stream, start, stop, 0U,
+                          args);
 }
 
 struct m3_rows_variant {
@@ -532,12 +558,18 @@ struct m3_rows_variant {
     m3_softmax_launcher other;
 };
 
-/* Wave-independent variants; the first whose width class fits is used. */
+/* Wave-independent variants; the first whose width class fits is used.
+ * Rows per wave and sum prefetch depth keep each variant within 128 VGPRs
+ * (four waves per SIMD). */
 const m3_rows_variant m3_rows_variants[] = {
-    {1U, 8U, &m3_launch_rows<1, 8, true>, &m3_launch_rows<1, 8, false>},
-    {2U, 4U, &m3_launch_rows<2, 4, true>, &m3_launch_rows<2, 4, false>},
-    {4U, 2U, &m3_launch_rows<4, 2, true>, &m3_launch_rows<4, 2, false>},
-    {8U, 1U, &m3_launch_rows<8, 1, true>, &m3_launch_rows<8, 1, false>},
+    {1U, 8U, &m3_launch_rows<1, 8, 8, true>,
+     &m3_launch_rows<1, 8, 8, false>},
+    {2U, 4U, &m3_launch_rows<2, 4, 8, true>,
+     &m3_launch_rows<2, 4, 8, false>},
+    {4U, 4U, &m3_launch_rows<4, 4, 4, true>,
+     &m3_launch_rows<4, 4, 4, false>},
+    {8U, 2U, &m3_launch_rows<8, 2, 4, true>,
+     &m3_launch_rows<8, 2, 4, false>},
 };
 
 struct m3_softmax_general_args {
