@@ -61,6 +61,20 @@ def log(*parts):
     print(*parts, file=sys.stderr, flush=True)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter passes
+    (profiles/hbm_traffic.json: FETCH_SIZE and WRITE_SIZE, each scaled by
+    the same counter's reading for a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as handle:
+            table = json.load(handle)
+    except (OSError, ValueError):
+        return None
+    entry = table.get("kernels", {}).get(kernel)
+    return None if entry is None else entry.get("traffic_bytes")
+
+
 # ---- CPU baseline (checker side: oracle/_ref or oracle) -------------------
 
 class CpuBaseline:
@@ -579,7 +593,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1),
                      "peak": PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("m3_softmax_rows")},
         "cpu_baseline": cpu_line,
         "op_classes": results,
     }
