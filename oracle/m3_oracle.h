@@ -12,9 +12,11 @@
  *
  * Pinning (what checks each function, besides the reference's golden
  * vectors):
- *   conversions      exhaustive vs the compiled reference (oracle/_ref)
- *                    over all 2^16 half/bfloat inputs and a dense F32
- *                    sweep; closed-form IEEE RNE vs numpy for finite values
+ *   conversions      exhaustive vs the compiled reference (oracle/_ref):
+ *                    the full F32->F16/BF16 tables (all 2^32 inputs) and
+ *                    F16/BF16->F32 tables (all 2^16) hash to the values the
+ *                    reference's CAST produces (tests/test_numeric_cpu.py);
+ *                    closed-form IEEE RNE vs numpy for finite values
  *   binary           closed form (one IEEE op, RNE) vs numpy; strided and
  *                    broadcast layouts vs the compiled reference
  *   cast             conversions above + truncation closed form
