@@ -92,6 +92,30 @@ __device__ __forceinline__ uint32_t m3_wave_max_u32(uint32_t v)
     return v;
 }
 
+/* A value that is equal in every lane of the wave, moved to a scalar
+ * register so that branches on it are uniform (the compiler cannot prove
+ * that a cross-lane reduction is uniform). */
+__device__ __forceinline__ uint32_t m3_uniform_u32(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+__device__ __forceinline__ float m3_uniform_f32(float v)
+{
+    return __builtin_bit_cast(float, m3_uniform_u32(m3_f32_bits(v)));
+}
+
+/* Lane `k`'s double, as a wave-uniform value. */
+__device__ __forceinline__ double m3_lane_f64(double v, int k)
+{
+    uint64_t bits = __builtin_bit_cast(uint64_t, v);
+    uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bits, k);
+    uint32_t hi =
+        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(bits >> 32U), k);
+
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32U) | lo);
+}
+
 /* Four consecutive row elements starting at column c, as F32. */
 template <bool F32IO>
 __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
@@ -382,7 +406,7 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     __shared__ float tiles[kWaves][R][kLine];
     __shared__ uint64_t exp_table[32];
     const uint32_t lane = threadIdx.x & 63U;
-    const uint32_t wave = threadIdx.x >> 6U;
+    const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
     const uint32_t width = a.width;
     const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
     const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
@@ -435,7 +459,7 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
                 m = fmaxf(m, fmaxf(fmaxf(v[k][j].x, v[k][j].y),
                                    fmaxf(v[k][j].z, v[k][j].w)));
             }
-            m = m3_wave_max(m);
+            m = m3_uniform_f32(m3_wave_max(m));
             maximum[k] = m;
             if (m != INFINITY && m != -INFINITY) {
 #pragma unroll
@@ -452,7 +476,7 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
                     last = nonzero != 0U ? lane + 64U * j + 1U : last;
                 }
             }
-            length[k] = m3_wave_max_u32(last) * 4U;
+            length[k] = m3_uniform_u32(m3_wave_max_u32(last)) * 4U;
         }
         uint32_t my_length = 0U;
         uint32_t wave_length = 0U;
@@ -490,11 +514,41 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
 
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            const double inverse = __shfl(inverse_of_lane, k, 64);
             const float m = maximum[k];
-            float one_over_count = 0.0F;
 
-            if (m == INFINITY) {
+            if ((uint32_t)k >= present) {
+                continue;
+            }
+            if (m != INFINITY && m != -INFINITY) {
+                const double inverse = m3_lane_f64(inverse_of_lane, k);
+
+#pragma unroll
+                for (int j = 0; j < VPL; ++j) {
+                    const float4 e = v[k][j];
+                    float4 p;
+
+                    if (lane * 4U + kChunk * j >= width) {
+                        continue;
+                    }
+                    p.x = m3_softmax_scale(e.x, inverse);
+                    p.y = m3_softmax_scale(e.y, inverse);
+                    p.z = m3_softmax_scale(e.z, inverse);
+                    p.w = m3_softmax_scale(e.w, inverse);
+                    m3_softmax_store4<F32IO>(out, (uint64_t)kChunk * j,
+                                             out_dtype, p);
+                }
+            } else if (m == -INFINITY) {
+                /* every entry is -inf: zeros */
+#pragma unroll
+                for (int j = 0; j < VPL; ++j) {
+                    if (lane * 4U + kChunk * j < width) {
+                        m3_softmax_store4<F32IO>(
+                            out, (uint64_t)kChunk * j, out_dtype,
+                            make_float4(0.0F, 0.0F, 0.0F, 0.0F));
+                    }
+                }
+            } else {
+                /* maximum +inf: 1/k on the k +inf entries, 0 elsewhere */
                 uint32_t count = 0U;
 
 #pragma unroll
@@ -504,35 +558,24 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
                              (v[k][j].z == INFINITY) +
                              (v[k][j].w == INFINITY);
                 }
-                one_over_count = 1.0F / (float)m3_wave_sum(count);
-            }
-            if ((uint32_t)k >= present) {
-                continue;
-            }
-#pragma unroll
-            for (int j = 0; j < VPL; ++j) {
-                const uint32_t c = lane * 4U + kChunk * j;
-                const float4 e = v[k][j];
-                float4 p;
+                const float one_over_count =
+                    1.0F / (float)m3_wave_sum(count);
 
-                if (c >= width) {
-                    continue;
-                }
-                if (m == -INFINITY) {
-                    p = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
-                } else if (m == INFINITY) {
+#pragma unroll
+                for (int j = 0; j < VPL; ++j) {
+                    const float4 e = v[k][j];
+                    float4 p;
+
+                    if (lane * 4U + kChunk * j >= width) {
+                        continue;
+                    }
                     p.x = e.x == INFINITY ? one_over_count : 0.0F;
                     p.y = e.y == INFINITY ? one_over_count : 0.0F;
                     p.z = e.z == INFINITY ? one_over_count : 0.0F;
                     p.w = e.w == INFINITY ? one_over_count : 0.0F;
-                } else {
-                    p.x = m3_softmax_scale(e.x, inverse);
-                    p.y = m3_softmax_scale(e.y, inverse);
-                    p.z = m3_softmax_scale(e.z, inverse);
-                    p.w = m3_softmax_scale(e.w, inverse);
+                    m3_softmax_store4<F32IO>(out, (uint64_t)kChunk * j,
+                                             out_dtype, p);
                 }
-                m3_softmax_store4<F32IO>(out, (uint64_t)kChunk * j,
-                                         out_dtype, p);
             }
             out += out_pitch;
         }

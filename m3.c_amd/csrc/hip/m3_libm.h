@@ -181,56 +181,107 @@ M3_HD uint32_t m3_sinf_top12(float value)
     return (m3_f32_bits(value) >> 20U) & 0x7ffU;
 }
 
-/* sinf of the libm, for every float input (NaN and infinities give NaN). */
-M3_HD float m3_sinf(float y)
+/* sinf for |y| >= 120 and for infinities and NaN (which give NaN): the
+ * 96-bit fixed-point reduction with 192 bits of 2/pi. */
+M3_HD float m3_sinf_large(float y)
 {
-    const double half_pi = 0x1.921FB54442D18p0;
     const double pi63 = 0x1.921FB54442D18p-62;
-    const float pio4f = (float)0x1.921FB54442D18p-1;
-    uint32_t top = m3_sinf_top12(y);
-    double x = (double)y;
+    uint32_t xi = m3_f32_bits(y);
+    const uint32_t *window;
+    uint32_t shift;
+    uint64_t lo;
+    uint64_t mid;
+    uint64_t hi;
+    uint64_t q;
+    double x;
     int n;
     int quadrant;
     double sign;
 
-    if (top < m3_sinf_top12(pio4f)) {
-        if (top < m3_sinf_top12(0x1p-12F)) {
-            return y;
-        }
-        return (float)m3_sinf_eval(x, x * x, 0, 0);
-    }
-    if (top < m3_sinf_top12(120.0F)) {
-        double r = x * 0x1.45F306DC9C883p+23;
-
-        n = ((int32_t)r + 0x800000) >> 24;
-        x = fma(-(double)n, half_pi, x);
-        quadrant = n;
-    } else if (top < m3_sinf_top12(INFINITY)) {
-        uint32_t xi = m3_f32_bits(y);
-        const uint32_t *window = &m3_sinf_two_over_pi[(xi >> 26U) & 15U];
-        uint32_t shift = (xi >> 23U) & 7U;
-        uint64_t lo;
-        uint64_t mid;
-        uint64_t hi;
-        uint64_t q;
-
-        xi = (xi & 0xffffffU) | 0x800000U;
-        xi <<= shift;
-        hi = (uint64_t)(xi * window[0]);
-        mid = (uint64_t)xi * window[4];
-        lo = (uint64_t)xi * window[8];
-        hi = (lo >> 32U) | (hi << 32U);
-        hi += mid;
-        q = (hi + (1ULL << 61U)) >> 62U;
-        hi -= q << 62U;
-        x = (double)(int64_t)hi * pi63;
-        n = (int)q;
-        quadrant = n + (int)(m3_f32_bits(y) >> 31U);
-    } else {
+    if (m3_sinf_top12(y) >= m3_sinf_top12(INFINITY)) {
         return (y - y) / (y - y);
     }
+    window = &m3_sinf_two_over_pi[(xi >> 26U) & 15U];
+    shift = (xi >> 23U) & 7U;
+    xi = (xi & 0xffffffU) | 0x800000U;
+    xi <<= shift;
+    hi = (uint64_t)(xi * window[0]);
+    mid = (uint64_t)xi * window[4];
+    lo = (uint64_t)xi * window[8];
+    hi = (lo >> 32U) | (hi << 32U);
+    hi += mid;
+    q = (hi + (1ULL << 61U)) >> 62U;
+    hi -= q << 62U;
+    x = (double)(int64_t)hi * pi63;
+    n = (int)q;
+    quadrant = n + (int)(m3_f32_bits(y) >> 31U);
     sign = ((quadrant & 3) == 1 || (quadrant & 3) == 2) ? -1.0 : 1.0;
     return (float)m3_sinf_eval(x * sign, x * x, n & 1, (quadrant & 2) != 0);
+}
+
+/* sinf of the libm, for every float input (NaN and infinities give NaN).
+ *
+ * For |y| < 120 every input runs one branch-free sequence, which gives
+ * the library's result bit for bit (checked on all floats):
+ *   - the library's separate path for |y| < 0.75 evaluates the sine
+ *     polynomial on y itself; the reduction below gives n = 0 there and
+ *     fma(-0, pi/2, y) = y exactly, so it is the same evaluation;
+ *   - its |y| < 2^-12 path returns y, kept here as a final select (it also
+ *     keeps the sign of -0);
+ *   - the library negates the cosine coefficients for quadrants 2 and 3
+ *     and evaluates the sine polynomial on -x for quadrants 1 and 2; with
+ *     round-to-nearest both equal negating the polynomial's result, so
+ *     quadrant n gives (n odd ? cosine : sine), negated when n & 2.
+ * Both polynomials are evaluated and one is selected, so SIMD lanes in
+ * different quadrants do not diverge. */
+M3_HD float m3_sinf(float y)
+{
+    const double half_pi = 0x1.921FB54442D18p0;
+    const double s1 = -0x1.555545995a603p-3;
+    const double s2 = 0x1.1107605230bc4p-7;
+    const double s3 = -0x1.994eb3774cf24p-13;
+    const double c0 = 0x1p0;
+    const double c1 = -0x1.ffffffd0c621cp-2;
+    const double c2 = 0x1.55553e1068f19p-5;
+    const double c3 = -0x1.6c087e89a359dp-10;
+    const double c4 = 0x1.99343027bf8c3p-16;
+    uint32_t top = m3_sinf_top12(y);
+    double x;
+    double r;
+    int32_t n;
+    double x2;
+    double sine;
+    double cosine;
+    double value;
+
+    if (top >= m3_sinf_top12(120.0F)) {
+        return m3_sinf_large(y);
+    }
+    x = (double)y;
+    r = x * 0x1.45F306DC9C883p+23;
+    n = ((int32_t)r + 0x800000) >> 24;
+    x = fma(-(double)n, half_pi, x);
+    x2 = x * x;
+    {
+        double x3 = x * x2;
+        double t = fma(x2, s3, s2);
+        double x7 = x3 * x2;
+        double s = fma(x3, s1, x);
+
+        sine = fma(x7, t, s);
+    }
+    {
+        double x4 = x2 * x2;
+        double t2 = fma(x2, c4, c3);
+        double t1 = fma(x2, c1, c0);
+        double x6 = x4 * x2;
+        double c = fma(x4, c2, t1);
+
+        cosine = fma(x6, t2, c);
+    }
+    value = (n & 1) != 0 ? cosine : sine;
+    value = (n & 2) != 0 ? -value : value;
+    return top < m3_sinf_top12(0x1p-12F) ? y : (float)value;
 }
 
 #endif
