@@ -23,7 +23,7 @@
  *   3. when both inputs classify and the output is contiguous and aligned,
  *      the vector kernel runs: each lane handles groups of 4 consecutive
  *      outputs with 16-byte (F32) or 8-byte (F16/BF16) loads and stores,
- *      four groups in flight per lane, grid-stride over the tensor;
+ *      two groups in flight per lane, grid-stride over the tensor;
  *      divisions by I and P use precomputed multiply-shift divisors;
  *   4. anything else runs the general kernel: per-element offsets from the
  *      coalesced stride table.
@@ -62,7 +62,7 @@ struct m3_bin_vec_args {
 };
 
 constexpr uint32_t kThreads = 256U;
-constexpr uint32_t kUnroll = 4U;
+constexpr uint32_t kUnroll = 2U; /* groups in flight per lane (measured best) */
 
 __device__ __forceinline__ uint32_t m3_load_raw(const uint8_t *p,
                                                 uint32_t dtype)
@@ -159,19 +159,19 @@ __device__ __forceinline__ void m3_store4(uint8_t *out, uint32_t dtype,
     m3_stream_store((uint2 *)(out + (uint64_t)f * 2U), packed);
 }
 
-template <int OP, bool F32ONLY>
+template <int OP, bool F32ONLY, int UNROLL = (int)kUnroll>
 __global__ __launch_bounds__(256) void m3_binary_vec_kernel(m3_bin_vec_args a)
 {
     const uint32_t out_dtype = F32ONLY ? (uint32_t)M3N_F32 : a.out_dtype;
-    const uint32_t step = gridDim.x * kThreads * kUnroll;
+    const uint32_t step = gridDim.x * kThreads * UNROLL;
 
-    for (uint32_t first = blockIdx.x * kThreads * kUnroll + threadIdx.x;
+    for (uint32_t first = blockIdx.x * kThreads * UNROLL + threadIdx.x;
          first < a.groups; first += step) {
-        uint4 left[kUnroll];
-        uint4 right[kUnroll];
+        uint4 left[UNROLL];
+        uint4 right[UNROLL];
 
 #pragma unroll
-        for (uint32_t u = 0U; u < kUnroll; ++u) {
+        for (uint32_t u = 0U; u < UNROLL; ++u) {
             uint32_t g = first + u * kThreads;
 
             if (g < a.groups) {
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void m3_binary_vec_kernel(m3_bin_vec_args a)
             }
         }
 #pragma unroll
-        for (uint32_t u = 0U; u < kUnroll; ++u) {
+        for (uint32_t u = 0U; u < UNROLL; ++u) {
             uint32_t g = first + u * kThreads;
 
             if (g < a.groups) {

@@ -11,7 +11,7 @@
  *   - float -> float: exact widening to F32, then the bit-exact RNE
  *     narrowing of m3_numeric.h. NaN payloads follow the reference rules.
  * The output is contiguous. A contiguous, aligned input runs the vector
- * kernel (four elements per lane per group, four groups in flight, output
+ * kernel (four elements per lane per group, two groups in flight, output
  * written with streaming stores);
  * strided inputs run a per-element kernel over the coalesced index space.
  */
@@ -22,7 +22,7 @@
 namespace {
 
 constexpr uint32_t kThreads = 256U;
-constexpr uint32_t kUnroll = 4U;
+constexpr uint32_t kUnroll = 2U; /* groups in flight per lane (measured best) */
 
 template <uint32_t DT>
 struct m3_vec_io;
