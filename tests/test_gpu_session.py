@@ -1,0 +1,359 @@
+"""The public m3_graph / m3_session API on the HIP provider (GPU).
+
+Graph -> compiler (liveness slots carved from one device arena) ->
+write_input (host to device) -> m3_session_run (every node on the session
+stream) -> read_output (device to host), checked bit for bit against the
+oracle or against numpy where a float32 IEEE operation is the definition.
+Each benchmark configuration runs here at a reduced size.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import m3
+from harness import ViewSpec, as_bytes, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32 if a.dtype.itemsize == 4
+                                        else np.uint16)
+
+
+def run_graph(graph, feeds, outputs, **options):
+    session = m3.Session(graph, **options)
+    graph.free()
+    for node in range(session.plan().node_count):
+        assert session.provider(node) == m3.PROVIDER_HIP
+    for value, array in feeds:
+        session.write(value, array)
+    session.run()
+    results = [session.read(value, np.zeros(shape, dtype))
+               for value, shape, dtype in outputs]
+    session.free()
+    return results
+
+
+def test_reference_graph_plan_and_result(gpu):
+    """tests/test_graph_runtime.c:87-160 on the GPU, TANH replaced by COPY
+    (the plan depends only on topology and sizes): 6 values, 4 nodes,
+    5 slots, 80 bytes; every node on the HIP provider."""
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, (4,))
+    c = g.add_value(m3.CONSTANT, m3.F32, (4,))
+    t0 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+    t1 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+    t2 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+    y = g.add_value(m3.OUTPUT, m3.F32, (4,))
+    constant = np.array([0.5, -1.0, 2.0, 3.0], np.float32)
+    g.set_constant(c, constant)
+    g.add_node(m3.OP_ADD, [x, c], [t0])
+    g.add_node(m3.OP_COPY, [t0], [t1])
+    g.add_node(m3.OP_MUL, [t1, c], [t2])
+    g.add_node(m3.OP_ADD, [t2, x], [y])
+    session = m3.Session(g)
+    g.free()
+    plan = session.plan()
+    assert (plan.value_count, plan.node_count, plan.storage_slot_count,
+            plan.allocated_bytes) == (6, 4, 5, 80)
+    assert [session.provider(i) for i in range(4)] == [m3.PROVIDER_HIP] * 4
+    data = np.array([1.0, 2.0, -3.0, 0.25], np.float32)
+    session.write(x, data)
+    session.run()
+    out = session.read(y, np.zeros(4, np.float32))
+    expected = ((data + constant) * constant + data).astype(np.float32)
+    assert np.array_equal(bits(out), bits(expected))
+    # repeated runs on unchanged inputs give the same bits
+    session.run()
+    again = session.read(y, np.zeros(4, np.float32))
+    assert np.array_equal(bits(again), bits(expected))
+    session.free()
+
+
+def _random_graph(rng, nodes, shape):
+    """A random DAG of ADD/MUL/SUB/DIV over F32 values of `shape` with
+    broadcast operands of the trailing size and of size 1."""
+    g = m3.Graph()
+    values = []
+    feeds = []
+    for _ in range(3):
+        vid = g.add_value(m3.INPUT, m3.F32, shape)
+        data = rng.standard_normal(shape).astype(np.float32)
+        feeds.append((vid, data))
+        values.append((vid, shape, data))
+    for cshape in ((shape[-1],), (1,)):
+        vid = g.add_value(m3.CONSTANT, m3.F32, cshape)
+        data = (rng.standard_normal(cshape) + 3.0).astype(np.float32)
+        g.set_constant(vid, data)
+        values.append((vid, cshape, data))
+    ops = [(m3.OP_ADD, np.add), (m3.OP_MUL, np.multiply),
+           (m3.OP_SUB, np.subtract), (m3.OP_DIV, np.divide)]
+    outputs = []
+    for n in range(nodes):
+        kind, fn = ops[rng.integers(len(ops))]
+        a = values[rng.integers(len(values))]
+        b = values[rng.integers(len(values))]
+        out_shape = np.broadcast_shapes(a[1], b[1])
+        role = m3.OUTPUT if n == nodes - 1 or rng.random() < 0.15 \
+            else m3.TEMPORARY
+        vid = g.add_value(role, m3.F32, out_shape)
+        with np.errstate(all="ignore"):
+            result = fn(np.broadcast_to(a[2], out_shape),
+                        np.broadcast_to(b[2], out_shape)).astype(np.float32)
+        g.add_node(kind, [a[0], b[0]], [vid])
+        values.append((vid, out_shape, result))
+        if role == m3.OUTPUT:
+            outputs.append((vid, out_shape, result))
+    return g, feeds, outputs
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_graphs_reuse_slots_on_device(gpu, seed):
+    """Temporaries share arena slots by liveness; no live value is
+    overwritten (every output matches numpy's float32 IEEE result)."""
+    rng = np.random.default_rng(100 + seed)
+    g, feeds, outputs = _random_graph(rng, 40, (6, 37, 40))
+    session = m3.Session(g)
+    g.free()
+    plan = session.plan()
+    assert plan.storage_slot_count < plan.value_count
+    for vid, data in feeds:
+        session.write(vid, data)
+    session.run()
+    for vid, shape, expected in outputs:
+        got = session.read(vid, np.zeros(shape, np.float32))
+        finite = np.isfinite(expected)
+        assert np.array_equal(bits(got)[finite], bits(expected)[finite]), vid
+        assert np.array_equal(np.isnan(got), np.isnan(expected)), vid
+    session.free()
+
+
+def test_mul_broadcast_config(gpu):
+    """C1 at reduced size: x ~ U(-1,1) times a constant c ~ N(0,1)
+    broadcast over the last axis."""
+    shape = (2, 64, 1536)
+    x = m3.rng_fill("uniform", int(np.prod(shape)), seed=0, a=-1.0,
+                    b=1.0).reshape(shape)
+    c = m3.rng_fill("normal", shape[-1], seed=0, sequence=1, a=1.0)
+    g = m3.Graph()
+    vx = g.add_value(m3.INPUT, m3.F32, shape)
+    vc = g.add_value(m3.CONSTANT, m3.F32, shape[-1:])
+    vy = g.add_value(m3.OUTPUT, m3.F32, shape)
+    g.set_constant(vc, c)
+    g.add_node(m3.OP_MUL, [vx, vc], [vy])
+    (y,) = run_graph(g, [(vx, x)], [(vy, shape, np.float32)])
+    assert np.array_equal(bits(y), bits((x * c).astype(np.float32)))
+
+
+def _oracle_unary(kind, src, src_dtype, dst_shape, dst_dtype, np_out):
+    out = np.zeros(int(np.prod(dst_shape)) * m3.DTYPE_SIZES[dst_dtype],
+                   np.uint8)
+    status, storages = run_oracle(kind, [as_bytes(src), out],
+                                  [ViewSpec(0, src_dtype, src.shape),
+                                   ViewSpec(1, dst_dtype, dst_shape)])
+    assert status == m3.OK
+    return storages[1].view(np_out).reshape(dst_shape)
+
+
+def test_softmax_causal_config(gpu):
+    """C2 at reduced size: causal logits ~ N(0,3), strict upper triangle
+    -inf, bit-exact with the oracle (the C library's expf)."""
+    n = 256
+    s = m3.rng_fill("normal", 3 * n * n, seed=0, a=3.0).reshape(3, n, n)
+    s[:, np.triu(np.ones((n, n), bool), k=1)] = -np.inf
+    g = m3.Graph()
+    vi = g.add_value(m3.INPUT, m3.F32, s.shape)
+    vo = g.add_value(m3.OUTPUT, m3.F32, s.shape)
+    g.add_node(m3.OP_SOFTMAX, [vi], [vo])
+    (p,) = run_graph(g, [(vi, s)], [(vo, s.shape, np.float32)])
+    expected = _oracle_unary(m3.OP_SOFTMAX, s, m3.F32, s.shape, m3.F32,
+                             np.float32)
+    assert np.array_equal(bits(p), bits(expected))
+
+
+def test_softmax_nan_input_is_rejected_until_rewritten(gpu):
+    """A NaN in the input makes the run OUT_OF_RANGE and leaves the output
+    untouched; a clean rewrite is accepted, and a NaN written later is
+    seen again (the device scan result does not outlive a host write)."""
+    shape = (8, 64)
+    clean = m3.rng_fill("normal", 8 * 64, seed=3, a=2.0).reshape(shape)
+    dirty = clean.copy()
+    dirty[5, 17] = np.nan
+    g = m3.Graph()
+    vi = g.add_value(m3.INPUT, m3.F32, shape)
+    vo = g.add_value(m3.OUTPUT, m3.F32, shape)
+    g.add_node(m3.OP_SOFTMAX, [vi], [vo])
+    session = m3.Session(g)
+    g.free()
+    lib, _ = m3.load()
+    session.write(vi, dirty)
+    assert lib.m3_session_run(session.handle, None) == m3.OUT_OF_RANGE
+    assert not session.read(vo, np.ones(shape, np.float32)).any()
+    session.write(vi, clean)
+    session.run()
+    good = session.read(vo, np.zeros(shape, np.float32))
+    expected = _oracle_unary(m3.OP_SOFTMAX, clean, m3.F32, shape, m3.F32,
+                             np.float32)
+    assert np.array_equal(bits(good), bits(expected))
+    session.write(vi, dirty)
+    assert lib.m3_session_run(session.handle, None) == m3.OUT_OF_RANGE
+    assert np.array_equal(bits(session.read(vo, np.zeros(shape, np.float32))),
+                          bits(expected))
+    session.free()
+
+
+@pytest.mark.parametrize("pair", [(m3.F32, m3.F16), (m3.F16, m3.F32),
+                                  (m3.F32, m3.BF16), (m3.BF16, m3.F32)])
+def test_cast_config(gpu, pair):
+    """C3 at reduced size: normals ~ N(0, 1e3) with 5% specials (subnormal,
+    signed zeros, infinities, NaN payloads), bit-exact."""
+    src_dtype, dst_dtype = pair
+    n = 256 * 256
+    rng = np.random.default_rng(7)
+    values = (rng.standard_normal(n) * 1000).astype(np.float32)
+    raw = values.view(np.uint32).copy()
+    pick = rng.random(n) < 0.05
+    specials = np.array([0x00000001, 0x007fffff, 0x80000000, 0x00000000,
+                         0x7f800000, 0xff800000, 0x7fc00001, 0x7f800123,
+                         0xffa00000], np.uint32)
+    raw[pick] = specials[rng.integers(len(specials), size=int(pick.sum()))]
+    f32 = raw.view(np.float32).reshape(256, 256)
+    if src_dtype == m3.F16:
+        src = f32.astype(np.float16).view(np.uint16)
+    elif src_dtype == m3.BF16:
+        src = (f32.view(np.uint32) >> 16).astype(np.uint16)
+    else:
+        src = f32
+    out_np = np.float32 if dst_dtype == m3.F32 else np.uint16
+    g = m3.Graph()
+    vi = g.add_value(m3.INPUT, src_dtype, src.shape)
+    vo = g.add_value(m3.OUTPUT, dst_dtype, src.shape)
+    g.add_node(m3.OP_CAST, [vi], [vo])
+    (got,) = run_graph(g, [(vi, src)], [(vo, src.shape, out_np)])
+    expected = _oracle_unary(m3.OP_CAST, src, src_dtype, src.shape,
+                             dst_dtype, out_np)
+    assert np.array_equal(bits(got), bits(expected))
+
+
+def test_snake_config(gpu):
+    """C4 at reduced size: x ~ N(0,1), alpha ~ U(0.1, 2) per channel."""
+    shape = (2, 48, 4096)
+    x = m3.rng_fill("normal", int(np.prod(shape)), seed=0,
+                    a=1.0).reshape(shape)
+    alpha = m3.rng_fill("uniform", shape[1], seed=0, sequence=1, a=0.1,
+                        b=2.0).reshape(1, shape[1], 1)
+    g = m3.Graph()
+    vx = g.add_value(m3.INPUT, m3.F32, shape)
+    va = g.add_value(m3.CONSTANT, m3.F32, alpha.shape)
+    vy = g.add_value(m3.OUTPUT, m3.F32, shape)
+    g.set_constant(va, alpha)
+    g.add_node(m3.OP_SNAKE1D, [vx, va], [vy])
+    (y,) = run_graph(g, [(vx, x)], [(vy, shape, np.float32)])
+    out = np.zeros(x.nbytes, np.uint8)
+    status, storages = run_oracle(
+        m3.OP_SNAKE1D, [as_bytes(x), as_bytes(alpha), out],
+        [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, alpha.shape),
+         ViewSpec(2, m3.F32, shape)])
+    assert status == m3.OK
+    assert np.array_equal(bits(y), storages[2].view(np.uint32)
+                          .reshape(shape))
+
+
+def test_euler_cfg_graph(gpu):
+    """C5 at reduced size: 4 Euler CFG steps in the reference's op order
+    (src/m3_flow_solver_math.c:36-135), constants per step, temporaries
+    reusing slots; checked against the same float32 operations in numpy."""
+    shape = (2, 64, 96)
+    count = int(np.prod(shape))
+    steps = 4
+    rng = m3.rng_new(0, 0)
+    x0 = m3.rng_fill("normal", count, seed=0, a=1.0, rng=rng).reshape(shape)
+    vus = [m3.rng_fill("normal", count, seed=0, a=1.0, rng=rng)
+           .reshape(shape) for _ in range(steps)]
+    vcs = [m3.rng_fill("normal", count, seed=0, a=1.0, rng=rng)
+           .reshape(shape) for _ in range(steps)]
+    scale = np.float32(3.0)
+    dt = np.float32(1.0 / 30.0)
+    g = m3.Graph()
+    vx = g.add_value(m3.INPUT, m3.F32, shape)
+    consts = {}
+    for name, value in (("minus_one", -1.0), ("scale", scale), ("dt", dt)):
+        vid = g.add_value(m3.CONSTANT, m3.F32, (1,))
+        g.set_constant(vid, np.array([value], np.float32))
+        consts[name] = vid
+    current = vx
+    expected = x0.copy()
+    for k in range(steps):
+        vu = g.add_value(m3.CONSTANT, m3.F32, shape)
+        vc = g.add_value(m3.CONSTANT, m3.F32, shape)
+        g.set_constant(vu, vus[k])
+        g.set_constant(vc, vcs[k])
+        t = [g.add_value(m3.TEMPORARY, m3.F32, shape) for _ in range(5)]
+        nxt = g.add_value(m3.OUTPUT if k == steps - 1 else m3.TEMPORARY,
+                          m3.F32, shape)
+        g.add_node(m3.OP_MUL, [vu, consts["minus_one"]], [t[0]])
+        g.add_node(m3.OP_ADD, [vc, t[0]], [t[1]])
+        g.add_node(m3.OP_MUL, [t[1], consts["scale"]], [t[2]])
+        g.add_node(m3.OP_ADD, [vu, t[2]], [t[3]])
+        g.add_node(m3.OP_MUL, [t[3], consts["dt"]], [t[4]])
+        g.add_node(m3.OP_ADD, [current, t[4]], [nxt])
+        current = nxt
+        a = (vus[k] * np.float32(-1.0)).astype(np.float32)
+        a = (vcs[k] + a).astype(np.float32)
+        a = (a * scale).astype(np.float32)
+        v = (vus[k] + a).astype(np.float32)
+        b = (v * dt).astype(np.float32)
+        expected = (expected + b).astype(np.float32)
+    session = m3.Session(g)
+    g.free()
+    plan = session.plan()
+    assert plan.storage_slot_count < plan.value_count
+    session.write(vx, x0)
+    session.run()
+    y = session.read(current, np.zeros(shape, np.float32))
+    assert np.array_equal(bits(y), bits(expected))
+    session.free()
+
+
+def test_gpu_provider_disabled_is_unsupported(gpu):
+    """With the GPU provider disallowed there is no CPU fallback."""
+    g = m3.Graph()
+    vi = g.add_value(m3.INPUT, m3.F32, (4,))
+    vo = g.add_value(m3.OUTPUT, m3.F32, (4,))
+    g.add_node(m3.OP_SOFTMAX, [vi], [vo])
+    lib, _ = m3.load()
+    handle = ctypes.c_void_p()
+    error = m3.Error()
+    options = m3.SessionOptions(False, False, True)
+    status = lib.m3_session_create(ctypes.byref(handle), g.handle,
+                                   ctypes.byref(options), ctypes.byref(error))
+    assert status == m3.UNSUPPORTED and not handle
+    g.free()
+
+
+def test_two_sessions_interleave(gpu):
+    """Two sessions (two backends, two streams) alternate runs; each keeps
+    its own arena and results."""
+    shape = (16, 96)
+    graphs = []
+    for seed in (11, 12):
+        x = m3.rng_fill("normal", 16 * 96, seed=seed, a=2.0).reshape(shape)
+        g = m3.Graph()
+        vi = g.add_value(m3.INPUT, m3.F32, shape)
+        vo = g.add_value(m3.OUTPUT, m3.F32, shape)
+        g.add_node(m3.OP_SOFTMAX, [vi], [vo])
+        session = m3.Session(g)
+        g.free()
+        session.write(vi, x)
+        graphs.append((session, vi, vo, x))
+    for _ in range(3):
+        for session, _, _, _ in graphs:
+            session.run()
+    for session, vi, vo, x in graphs:
+        got = session.read(vo, np.zeros(shape, np.float32))
+        expected = _oracle_unary(m3.OP_SOFTMAX, x, m3.F32, shape, m3.F32,
+                                 np.float32)
+        assert np.array_equal(bits(got), bits(expected))
+        session.free()
