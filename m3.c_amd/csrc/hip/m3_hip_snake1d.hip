@@ -10,7 +10,8 @@
  * sinf is m3_sinf, the C library algorithm restated bit for bit; the
  * division is the IEEE F32 quotient; this file is compiled with
  * -ffp-contract=off so no statement fuses. inv depends only on the channel
- * and is formed once per group of four outputs.
+ * and is formed once per lane and loop iteration when the lane's groups lie
+ * in one channel, else once per group of four outputs.
  *
  * The vector kernel handles contiguous, 16-byte aligned x and output with
  * L a multiple of 4: a lane takes four consecutive elements of one
@@ -27,14 +28,51 @@ namespace {
 constexpr uint32_t kThreads = 256U;
 constexpr uint32_t kUnroll = 4U;
 
-__device__ __forceinline__ float m3_snake(float x, float a, float inverse)
+/* y = x + inverse * sin(a*x)^2 given sine = sin(a*x). */
+__device__ __forceinline__ float m3_snake_finish(float x, float sine,
+                                                 float inverse)
 {
-    float angle = a * x;
-    float sine = m3_sinf(angle);
     float square = sine * sine;
     float scaled = inverse * square;
 
     return x + scaled;
+}
+
+__device__ __forceinline__ float m3_snake(float x, float a, float inverse)
+{
+    return m3_snake_finish(x, m3_sinf(a * x), inverse);
+}
+
+/* Four outputs of one channel. When no lane of the wave has an angle with
+ * |a*x| >= 120 or a NaN angle (the common case by far), all four take the
+ * branch-free sinf path, so the large-argument reduction costs one uniform
+ * test per group instead of a divergent branch per element. That path
+ * drops the sign of sinf: only its square is used, and the magnitude is
+ * that of sinf for every |angle| < 120. */
+__device__ __forceinline__ float4 m3_snake4(float4 x, float a, float inverse)
+{
+    const float4 angle = make_float4(a * x.x, a * x.y, a * x.z, a * x.w);
+    /* one compare per element into a lane mask, the masks OR-ed as
+     * scalars */
+    const uint64_t large = __ballot(!(fabsf(angle.x) < 120.0F)) |
+                           __ballot(!(fabsf(angle.y) < 120.0F)) |
+                           __ballot(!(fabsf(angle.z) < 120.0F)) |
+                           __ballot(!(fabsf(angle.w) < 120.0F));
+    float4 sine;
+
+    if (large != 0U) {
+        sine = make_float4(m3_sinf(angle.x), m3_sinf(angle.y),
+                           m3_sinf(angle.z), m3_sinf(angle.w));
+    } else {
+        sine = make_float4(m3_sinf_medium_magnitude(angle.x),
+                           m3_sinf_medium_magnitude(angle.y),
+                           m3_sinf_medium_magnitude(angle.z),
+                           m3_sinf_medium_magnitude(angle.w));
+    }
+    return make_float4(m3_snake_finish(x.x, sine.x, inverse),
+                       m3_snake_finish(x.y, sine.y, inverse),
+                       m3_snake_finish(x.z, sine.z, inverse),
+                       m3_snake_finish(x.w, sine.w, inverse));
 }
 
 __device__ __forceinline__ float m3_snake_inverse(float a)
@@ -61,7 +99,34 @@ __global__ __launch_bounds__(256) void m3_snake1d_vec_kernel(
 
     for (uint32_t first = blockIdx.x * kThreads * kUnroll + threadIdx.x;
          first < a.groups; first += step) {
+        const uint32_t last = first + (kUnroll - 1U) * kThreads;
+        const uint32_t row = m3_fast_div_q(a.length_in_groups, first);
         float4 x[kUnroll];
+
+        /* The row b*C + c of group g is nondecreasing in g, so when the
+         * first and last group of a lane share a row, all of its groups
+         * do: one channel, one alpha and one division for the lane. */
+        if (__all(last < a.groups &&
+                  m3_fast_div_q(a.length_in_groups, last) == row)) {
+            const uint32_t channel =
+                row - m3_fast_div_q(a.channels, row) * a.channels.divisor;
+            const float alpha = *(const float *)(
+                a.alpha + (int64_t)channel * a.alpha_stride);
+
+#pragma unroll
+            for (uint32_t u = 0U; u < kUnroll; ++u) {
+                x[u] = a.input[first + u * kThreads];
+            }
+            const float inverse = m3_snake_inverse(alpha);
+
+#pragma unroll
+            for (uint32_t u = 0U; u < kUnroll; ++u) {
+                m3_stream_store(&a.output[first + u * kThreads],
+                                m3_snake4(x[u], alpha, inverse));
+            }
+            continue;
+        }
+
         float alpha[kUnroll];
 
 #pragma unroll
@@ -84,13 +149,9 @@ __global__ __launch_bounds__(256) void m3_snake1d_vec_kernel(
 
             if (g < a.groups) {
                 float inverse = m3_snake_inverse(alpha[u]);
-                float4 y;
 
-                y.x = m3_snake(x[u].x, alpha[u], inverse);
-                y.y = m3_snake(x[u].y, alpha[u], inverse);
-                y.z = m3_snake(x[u].z, alpha[u], inverse);
-                y.w = m3_snake(x[u].w, alpha[u], inverse);
-                m3_stream_store(&a.output[g], y);
+                m3_stream_store(&a.output[g],
+                                m3_snake4(x[u], alpha[u], inverse));
             }
         }
     }

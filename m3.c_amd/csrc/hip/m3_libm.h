@@ -219,10 +219,9 @@ M3_HD float m3_sinf_large(float y)
     return (float)m3_sinf_eval(x * sign, x * x, n & 1, (quadrant & 2) != 0);
 }
 
-/* sinf of the libm, for every float input (NaN and infinities give NaN).
- *
- * For |y| < 120 every input runs one branch-free sequence, which gives
- * the library's result bit for bit (checked on all floats):
+/* sinf of the libm for |y| < 120 (m3_sinf_top12(y) < m3_sinf_top12(120)),
+ * as one branch-free sequence that gives the library's result bit for bit
+ * (checked on all floats through m3_sinf):
  *   - the library's separate path for |y| < 0.75 evaluates the sine
  *     polynomial on y itself; the reduction below gives n = 0 there and
  *     fma(-0, pi/2, y) = y exactly, so it is the same evaluation;
@@ -233,8 +232,10 @@ M3_HD float m3_sinf_large(float y)
  *     round-to-nearest both equal negating the polynomial's result, so
  *     quadrant n gives (n odd ? cosine : sine), negated when n & 2.
  * Both polynomials are evaluated and one is selected, so SIMD lanes in
- * different quadrants do not diverge. */
-M3_HD float m3_sinf(float y)
+ * different quadrants do not diverge. m3_sinf_medium_unsigned returns the
+ * selected polynomial before the sign of quadrants 2 and 3 is applied, and
+ * the quadrant in *quadrant. */
+M3_HD double m3_sinf_medium_unsigned(float y, int32_t *quadrant)
 {
     const double half_pi = 0x1.921FB54442D18p0;
     const double s1 = -0x1.555545995a603p-3;
@@ -245,21 +246,13 @@ M3_HD float m3_sinf(float y)
     const double c2 = 0x1.55553e1068f19p-5;
     const double c3 = -0x1.6c087e89a359dp-10;
     const double c4 = 0x1.99343027bf8c3p-16;
-    uint32_t top = m3_sinf_top12(y);
-    double x;
-    double r;
-    int32_t n;
+    double x = (double)y;
+    double r = x * 0x1.45F306DC9C883p+23;
+    int32_t n = ((int32_t)r + 0x800000) >> 24;
     double x2;
     double sine;
     double cosine;
-    double value;
 
-    if (top >= m3_sinf_top12(120.0F)) {
-        return m3_sinf_large(y);
-    }
-    x = (double)y;
-    r = x * 0x1.45F306DC9C883p+23;
-    n = ((int32_t)r + 0x800000) >> 24;
     x = fma(-(double)n, half_pi, x);
     x2 = x * x;
     {
@@ -279,9 +272,38 @@ M3_HD float m3_sinf(float y)
 
         cosine = fma(x6, t2, c);
     }
-    value = (n & 1) != 0 ? cosine : sine;
+    *quadrant = n;
+    return (n & 1) != 0 ? cosine : sine;
+}
+
+M3_HD float m3_sinf_medium(float y)
+{
+    int32_t n;
+    double value = m3_sinf_medium_unsigned(y, &n);
+
     value = (n & 2) != 0 ? -value : value;
-    return top < m3_sinf_top12(0x1p-12F) ? y : (float)value;
+    return m3_sinf_top12(y) < m3_sinf_top12(0x1p-12F) ? y : (float)value;
+}
+
+/* |sinf(y)| for |y| < 120, for callers that only use the magnitude (a
+ * square): the sign flip and the |y| < 2^-12 select of m3_sinf_medium are
+ * left out. Below 2^-12 the polynomial's terms past y are under 2^-26 of y,
+ * so (float) rounds back to +-y; the magnitude equals |m3_sinf(y)| for every
+ * float with |y| < 120 (checked exhaustively). */
+M3_HD float m3_sinf_medium_magnitude(float y)
+{
+    int32_t n;
+
+    return (float)m3_sinf_medium_unsigned(y, &n);
+}
+
+/* sinf of the libm, for every float input (NaN and infinities give NaN). */
+M3_HD float m3_sinf(float y)
+{
+    if (m3_sinf_top12(y) >= m3_sinf_top12(120.0F)) {
+        return m3_sinf_large(y);
+    }
+    return m3_sinf_medium(y);
 }
 
 #endif

@@ -22,7 +22,9 @@
  *   numeric_tables libm <stride>
  *       Compares m3_expf and m3_sinf with the C library's expf and sinf
  *       on every stride-th float (expf on floats <= 0.5, the softmax
- *       domain; sinf on all floats) and prints the mismatch counts.
+ *       domain; sinf on all floats), and the magnitude of
+ *       m3_sinf_medium_magnitude with that of sinf where |x| < 120, and
+ *       prints the mismatch counts.
  *
  * Table hash: the inputs are split into blocks of 2^16 consecutive bit
  * patterns; each block's outputs (little-endian, 2 or 4 bytes each) are
@@ -288,9 +290,12 @@ static int libm(uint64_t stride)
     unsigned long long exp_bad = 0ULL;
     unsigned long long sin_checked = 0ULL;
     unsigned long long sin_bad = 0ULL;
+    unsigned long long magnitude_checked = 0ULL;
+    unsigned long long magnitude_bad = 0ULL;
 
 #pragma omp parallel for reduction(+ : exp_checked, exp_bad, sin_checked, \
-                                       sin_bad) schedule(static)
+                                       sin_bad, magnitude_checked,         \
+                                       magnitude_bad) schedule(static)
     for (int64_t u = 0; u <= (int64_t)0xffffffffLL; u += (int64_t)stride) {
         uint32_t b = (uint32_t)u;
         float x;
@@ -309,12 +314,24 @@ static int libm(uint64_t stride)
 
             sin_checked += 1U;
             sin_bad += memcmp(&got, &want, sizeof(got)) != 0;
+            if (fabsf(x) < 120.0F) {
+                float magnitude = fabsf(m3_sinf_medium_magnitude(x));
+
+                want = fabsf(want);
+                magnitude_checked += 1U;
+                magnitude_bad +=
+                    memcmp(&magnitude, &want, sizeof(magnitude)) != 0;
+            }
         }
     }
     printf("{\"expf_checked\": %llu, \"expf_mismatches\": %llu, "
-           "\"sinf_checked\": %llu, \"sinf_mismatches\": %llu}\n",
-           exp_checked, exp_bad, sin_checked, sin_bad);
-    return exp_bad == 0ULL && sin_bad == 0ULL ? 0 : 1;
+           "\"sinf_checked\": %llu, \"sinf_mismatches\": %llu, "
+           "\"sinf_magnitude_checked\": %llu, "
+           "\"sinf_magnitude_mismatches\": %llu}\n",
+           exp_checked, exp_bad, sin_checked, sin_bad, magnitude_checked,
+           magnitude_bad);
+    return exp_bad == 0ULL && sin_bad == 0ULL && magnitude_bad == 0ULL ? 0
+                                                                        : 1;
 }
 
 int main(int argc, char **argv)

@@ -329,7 +329,7 @@ def test_softmax_strided_and_in_place(hip):
 # ---- snake1d -------------------------------------------------------------------
 
 @pytest.mark.parametrize("shape", [(2, 16, 1024), (1, 3, 5), (3, 7, 12),
-                                   (2, 96, 4096)])
+                                   (2, 96, 4096), (2, 40, 1200)])
 def test_snake1d_layouts(hip, shape):
     rng = np.random.default_rng(10000 + sum(shape))
     count = int(np.prod(shape))

@@ -76,6 +76,8 @@ def test_libm_restatements_match_c_library():
     assert result["expf_checked"] > 400_000_000
     assert result["expf_mismatches"] == 0
     assert result["sinf_mismatches"] == 0
+    assert result["sinf_magnitude_checked"] > 300_000_000
+    assert result["sinf_magnitude_mismatches"] == 0
 
 
 def test_hash_discriminates_a_planted_rounding_error(reference_hashes):
