@@ -55,6 +55,12 @@ constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
 constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
 constexpr uint32_t kSumLanes = 16U;       /* lanes that run the in-order sums */
 
+/* Four F32 -inf: what a load past the end of a row reads instead. Never
+ * written; not const, so that it is in the global address space like the
+ * rows and a select between the two stays a global load. */
+__device__ float4 m3_minus_inf4 = {-INFINITY, -INFINITY, -INFINITY,
+                                   -INFINITY};
+
 struct m3_softmax_args {
     const uint8_t *input;
     uint8_t *output;
@@ -427,28 +433,45 @@ __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
         /* rows of this task that exist (the last task may be partial) */
         const uint32_t present =
             (uint32_t)min((uint64_t)R, a.rows - first_row);
-        /* this lane's first column of the task's first row; chunk j of a
-         * row is a constant offset from it */
-        const uint8_t *in = a.input + first_row * a.row_stride +
-                            (uint64_t)lane * 4U * in_size;
+        const uint8_t *rows = a.input + first_row * a.row_stride;
         float4 v[R][VPL];
         float maximum[R];
         uint32_t length[R]; /* elements up to the last nonzero e_j */
 
+        /* Every load is issued and none is under a branch, so the wave
+         * waits for each row's data alone: row 0 is reduced and
+         * exponentiated while the later rows are still arriving. A row past
+         * the end of the tensor (the last task) reads the task's first row
+         * and is never stored. A column past the width reads four F32 -inf
+         * from m3_minus_inf4 (16-bit inputs: column 0, replaced by -inf).
+         * A variant serves widths above 256 * VPL / 2, so its chunks
+         * j < VPL / 2 are always inside the row. */
 #pragma unroll
         for (int k = 0; k < R; ++k) {
+            const uint8_t *row =
+                rows + (uint64_t)((uint32_t)k < present ? (uint32_t)k : 0U) *
+                           a.row_stride;
+
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
                 const uint32_t c = lane * 4U + kChunk * j;
+                const bool inside = (VPL > 1 && j < VPL / 2) || c < width;
 
-                v[k][j] = make_float4(-INFINITY, -INFINITY, -INFINITY,
-                                      -INFINITY);
-                if ((uint32_t)k < present && c < width) {
-                    v[k][j] = m3_softmax_load4<F32IO>(
-                        in, (uint64_t)kChunk * j, in_dtype);
+                if (F32IO || in_dtype == M3N_F32) {
+                    const float4 *source =
+                        inside ? (const float4 *)(row + (uint64_t)c * 4U)
+                               : &m3_minus_inf4;
+
+                    v[k][j] = *source;
+                } else {
+                    const float4 x = m3_softmax_load4<F32IO>(
+                        row, inside ? c : 0U, in_dtype);
+
+                    v[k][j] = inside ? x
+                                     : make_float4(-INFINITY, -INFINITY,
+                                                   -INFINITY, -INFINITY);
                 }
             }
-            in += a.row_stride;
         }
 #pragma unroll
         for (int k = 0; k < R; ++k) {
