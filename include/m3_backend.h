@@ -20,7 +20,10 @@
  *     m3_storage_data() returns NULL and m3_storage_write/read go through
  *     the hooks. `reserve` lets the session compiler ask for one arena that
  *     later allocations are carved from;
- *   - SUB and DIV command descriptors (M3_OP_SUB/M3_OP_DIV).
+ *   - SUB and DIV command descriptors (M3_OP_SUB/M3_OP_DIV);
+ *   - the internal command kind M3_OP_ELEMENTWISE_PROGRAM, which the
+ *     session compiler forms from runs of ADD/SUB/MUL/DIV commands; it has
+ *     no counterpart in the reference and never appears in a graph.
  */
 #ifndef M3_BACKEND_H
 #define M3_BACKEND_H
@@ -234,7 +237,27 @@ typedef struct {
     uint64_t output_padding;
 } m3_op_conv_transpose1d;
 
+/* A run of F32 ADD/SUB/MUL/DIV commands over one element space that the
+ * session compiler fused into one elementwise program (layout: see
+ * m3_hip_launch_program in m3_hip.h). `commands` are the original
+ * commands, in order: they are validated as usual and define the result.
+ * `words` is the program in host memory; the same words are in `storage`
+ * at `byte_offset`. Intermediate values that only the run reads are not
+ * written to their slots. */
+#define M3_OP_ELEMENTWISE_PROGRAM ((m3_op_kind)0x1000)
+
+struct m3_command_s;
+
 typedef struct {
+    const struct m3_command_s *commands;
+    size_t command_count;
+    const uint32_t *words;
+    size_t word_count;
+    m3_storage *storage;
+    size_t byte_offset;
+} m3_op_elementwise_program;
+
+typedef struct m3_command_s {
     m3_op_kind kind;
     union {
         m3_op_unary copy;
@@ -259,6 +282,7 @@ typedef struct {
         m3_op_unary tanh;
         m3_op_binary sub;
         m3_op_binary div;
+        m3_op_elementwise_program elementwise_program;
     } descriptor;
 } m3_command;
 

@@ -35,6 +35,11 @@
  *                                   src/m3_op_data_preflight.c:8-64)
  *   m3_hip_synchronize           <- commit + waitUntilCompleted
  *                                   (src/m3_backend_metal.m:210-216)
+ *   m3_hip_launch_program        no counterpart: runs a run of ADD/SUB/
+ *                                   MUL/DIV commands (per-element semantics
+ *                                   of src/m3_op_execute_basic.c:61-77) that
+ *                                   the session compiler fused into one
+ *                                   elementwise program
  *
  * All launches of one device go to that device's single HIP stream, in call
  * order, so a command list executes in order and m3_hip_synchronize waits
@@ -157,6 +162,47 @@ int m3_hip_launch_snake1d(m3_hip_device *device, const m3_hip_view *input,
                           const m3_hip_view *alpha,
                           const m3_hip_view *output, char *message,
                           size_t capacity);
+
+/* Elementwise program: a run of F32 ADD/SUB/MUL/DIV operations over one
+ * element space of `count` elements, executed per element with the
+ * intermediate values in registers. Layout of the 32-bit words:
+ *   [0] M3_HIP_PROGRAM_MAGIC
+ *   [1] P, operand count (at most M3_HIP_PROGRAM_MAX_OPERANDS)
+ *   [2] I, instruction word count (at most M3_HIP_PROGRAM_MAX_WORDS)
+ *   [3] count, low 32 bits     [4] count, high 32 bits
+ *   [5..7] zero
+ *   [8 .. 8+2P) operand p: device address, low word then high word. Bit 0
+ *       of the low word set: a scalar, one F32 read by every element (the
+ *       address is 4-byte aligned). Clear: an F32 array of `count` elements
+ *       (16-byte aligned), element e at address + 4e.
+ *   [8+2P .. 8+2P+I) instructions.
+ * Registers per element: values R0..R3 and fetched operands F0..F3.
+ * Instructions (bits 0-1 opcode):
+ *   FETCH (two words): bits 2-3 n-1; the second word holds operand
+ *       indices f0..f{n-1} in its bytes 0..n-1. Loads array operand fk
+ *       into Fk for k < n; all n loads are issued together.
+ *   OP: bits 2-3 the m3_hip_binary_op; bits 4-5 destination R; bits 8-11
+ *       left source, bits 12-15 right source (0-3: R0-R3, 4-7: F0-F3,
+ *       8: the scalar operand in bits 16-23). dst = left (op) right as one
+ *       F32 operation with the reference's NaN rules.
+ *   STORE: bits 4-5 source R; bits 8-15 array operand; writes the value.
+ * m3_hip_launch_program checks the words on the host (magic, counts,
+ * indices, operand kinds and alignment) before launching; device_words must
+ * hold the same words in device memory. */
+#define M3_HIP_PROGRAM_MAGIC 0x4d335031U /* "M3P1" */
+#define M3_HIP_PROGRAM_HEADER_WORDS 8U
+#define M3_HIP_PROGRAM_MAX_OPERANDS 255U
+#define M3_HIP_PROGRAM_MAX_WORDS 4096U
+
+typedef enum {
+    M3_HIP_PROGRAM_FETCH = 0,
+    M3_HIP_PROGRAM_OP = 1,
+    M3_HIP_PROGRAM_STORE = 2
+} m3_hip_program_opcode;
+
+int m3_hip_launch_program(m3_hip_device *device, const uint32_t *words,
+                          const void *device_words, size_t word_count,
+                          char *message, size_t capacity);
 
 /* Scans view i for the condition kinds[i] (an m3_hip_scan_kind), waits, and
  * writes flags[i] = 1 when view i holds an offending element, else 0. */

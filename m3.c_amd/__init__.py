@@ -191,6 +191,7 @@ EXPORTS_HIP = [
     "m3_hip_launch_copy", "m3_hip_launch_softmax", "m3_hip_launch_snake1d",
     "m3_hip_scan_views", "m3_hip_synchronize", "m3_hip_timing_enable",
     "m3_hip_timing_reset", "m3_hip_timing_read", "m3_hip_stream",
+    "m3_hip_launch_program",
 ]
 
 _LIB = None
@@ -290,6 +291,8 @@ def load():
              ctypes.c_char_p, sz)
     _declare(hip, "m3_hip_stream", vp, vp)
     _declare(hip, "m3_hip_synchronize", st, vp, ctypes.c_char_p, sz)
+    _declare(hip, "m3_hip_launch_program", st, vp, P(ctypes.c_uint32), vp,
+             sz, ctypes.c_char_p, sz)
     _LIB, _HIP = lib, hip
     return lib, hip
 

@@ -417,7 +417,6 @@ __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
     const uint32_t width = a.width;
     const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
     const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
-    const uint32_t in_size = in_dtype == M3N_F32 ? 4U : 2U;
     const uint32_t out_size = out_dtype == M3N_F32 ? 4U : 2U;
     const uint64_t out_pitch = (uint64_t)width * out_size;
     const uint64_t tasks = (a.rows + R - 1U) / R;

@@ -303,19 +303,62 @@ static const m3_tensor_view *m3_hip_checked_input(const m3_command *command,
     return NULL;
 }
 
+/* True when `command` writes `storage`: its output, or for a fused
+ * elementwise program the output of any fused command (also those the
+ * program keeps in registers, which is conservative). */
+static bool m3_hip_writes(const m3_command *command,
+                          const m3_storage *storage)
+{
+    const m3_tensor_view *output = m3_op_output_of(command);
+
+    if (command->kind == M3_OP_ELEMENTWISE_PROGRAM) {
+        const m3_op_elementwise_program *program =
+            &command->descriptor.elementwise_program;
+        size_t k;
+
+        for (k = 0U; k < program->command_count; ++k) {
+            if (m3_hip_writes(&program->commands[k], storage)) {
+                return true;
+            }
+        }
+        return false;
+    }
+    return output != NULL && output->storage == storage;
+}
+
 static bool m3_hip_written_before(const m3_command *commands, size_t index,
                                   const m3_storage *storage)
 {
     size_t i;
 
     for (i = 0U; i < index; ++i) {
-        const m3_tensor_view *output = m3_op_output_of(&commands[i]);
-
-        if (output != NULL && output->storage == storage) {
+        if (m3_hip_writes(&commands[i], storage)) {
             return true;
         }
     }
     return false;
+}
+
+/* Drops the clean-scan memory of every storage `command` writes. */
+static void m3_hip_forget_outputs(m3_hip_backend_context *context,
+                                  const m3_command *command)
+{
+    const m3_tensor_view *output = m3_op_output_of(command);
+
+    if (command->kind == M3_OP_ELEMENTWISE_PROGRAM) {
+        const m3_op_elementwise_program *program =
+            &command->descriptor.elementwise_program;
+        size_t k;
+
+        for (k = 0U; k < program->command_count; ++k) {
+            m3_hip_forget_outputs(context, &program->commands[k]);
+        }
+        return;
+    }
+    if (output != NULL) {
+        m3_hip_forget_storage(context,
+                              m3_storage_device_data(output->storage));
+    }
 }
 
 static m3_status m3_hip_grow_scans(m3_hip_backend_context *context,
@@ -439,6 +482,16 @@ static int m3_hip_enqueue(m3_hip_backend_context *context,
     m3_hip_view b;
     m3_hip_view c;
 
+    if (command->kind == M3_OP_ELEMENTWISE_PROGRAM) {
+        const m3_op_elementwise_program *program =
+            &command->descriptor.elementwise_program;
+
+        return m3_hip_launch_program(
+            context->device, program->words,
+            (const uint8_t *)m3_storage_device_data(program->storage) +
+                program->byte_offset,
+            program->word_count, message, capacity);
+    }
     if (binary != NULL) {
         static const uint32_t ops[] = {M3_HIP_ADD, M3_HIP_MUL, M3_HIP_SUB,
                                        M3_HIP_DIV};
@@ -475,6 +528,7 @@ static int m3_hip_enqueue(m3_hip_backend_context *context,
         m3_hip_view_of(command->descriptor.snake1d.output, &c);
         return m3_hip_launch_snake1d(context->device, &a, &b, &c, message,
                                      capacity);
+
     default:
         (void)snprintf(message, capacity,
                        "HIP does not implement operation %d",
@@ -499,12 +553,7 @@ static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
         return status;
     }
     for (i = 0U; i < count && code == M3_HIP_OK; ++i) {
-        const m3_tensor_view *output = m3_op_output_of(&commands[i]);
-
-        if (output != NULL) {
-            m3_hip_forget_storage(context,
-                                  m3_storage_device_data(output->storage));
-        }
+        m3_hip_forget_outputs(context, &commands[i]);
         code = m3_hip_enqueue(context, &commands[i], message,
                               sizeof(message));
     }

@@ -1,0 +1,85 @@
+/*
+ * m3_fuse.h - elementwise fusion planner of the session compiler.
+ *
+ * The planner sees the graph as values (role, dtype, element count) and
+ * nodes in execution order, and groups consecutive F32 ADD/SUB/MUL/DIV
+ * nodes of one element space into programs for m3_hip_launch_program
+ * (word layout in m3_hip.h). It works on value indices only; the session
+ * compiler resolves operands to device addresses. Nothing here touches a
+ * device, so the planner is tested on the host.
+ *
+ * Rules, in the order nodes run:
+ *   - a node may join a group when it is eligible (its provider executes
+ *     programs), is ADD/SUB/MUL/DIV with F32 operands and output, and each
+ *     operand has the output's element count (an array read at the same
+ *     flat index) or one element (a scalar read by every element);
+ *   - a group is a run of consecutive such nodes with the same element
+ *     count; a value produced in the group lives in one of four registers
+ *     from its producer to its last use, and a node joins only if a
+ *     register is free for its output after its operands' last uses;
+ *   - a value produced in the group is stored unless it is a TEMPORARY
+ *     whose every use is inside the group (those never reach memory);
+ *   - operands produced before the group are fetched in batches of up to
+ *     four arrays covering the next nodes, so their loads overlap.
+ * Groups of one node are not formed. The per-element order of operations,
+ * the operations themselves and every stored value are the unfused ones.
+ */
+#ifndef M3_FUSE_H
+#define M3_FUSE_H
+
+#include "m3_internal.h"
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+typedef struct {
+    m3_graph_value_role role;
+    m3_dtype dtype;
+    uint64_t element_count;
+} m3_fuse_value;
+
+typedef struct {
+    m3_op_kind kind;
+    uint32_t left;
+    uint32_t right;
+    uint32_t output;
+    bool eligible;
+} m3_fuse_node;
+
+/* An operand of a group's program: value index and whether it is read as
+ * a scalar. Operand i of the group is entry operand_first + i. */
+typedef struct {
+    uint32_t value;
+    bool scalar;
+} m3_fuse_operand;
+
+typedef struct {
+    size_t first_node;
+    size_t node_count;
+    uint64_t element_count;
+    size_t operand_first;
+    size_t operand_count;
+    size_t code_first;
+    size_t code_count;
+} m3_fuse_group;
+
+typedef struct {
+    m3_fuse_group *groups;
+    size_t group_count;
+    m3_fuse_operand *operands;
+    size_t operand_count;
+    uint32_t *code;
+    size_t code_count;
+} m3_fuse_plan;
+
+/* Plans the groups of `nodes` (execution order). Values are referenced by
+ * index; every node's operands and output must be < value_count. On
+ * success *plan owns its arrays (free with m3_fuse_plan_free); a plan
+ * with no groups is valid. */
+m3_status m3_fuse_plan_build(const m3_fuse_value *values, size_t value_count,
+                             const m3_fuse_node *nodes, size_t node_count,
+                             m3_fuse_plan *plan, m3_error *error);
+void m3_fuse_plan_free(m3_fuse_plan *plan);
+
+#endif

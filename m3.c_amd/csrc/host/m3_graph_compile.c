@@ -12,6 +12,8 @@
  *   views and constant upload                :350-377
  *   bind + provider + validation per node    :379-440
  *   m3_session_create                        :442-531
+ * After the nodes are bound, the run list (fused elementwise programs) is
+ * planned by m3_graph_fuse.c.
  * The slot plan is the reference's: every INPUT, CONSTANT and OUTPUT value
  * owns a slot for the whole session; each TEMPORARY takes the smallest slot
  * that is free before its producer runs and large enough, or a new slot.
@@ -353,6 +355,7 @@ void m3_session_free(m3_session *session)
     if (session == NULL) {
         return;
     }
+    m3_session_free_runs(session);
     for (s = 0U; session->slots != NULL && s < session->slot_count; ++s) {
         m3_storage_free(session->slots[s].storage);
     }
@@ -444,6 +447,9 @@ m3_status m3_session_create(m3_session **session_output,
     }
     if (status == M3_STATUS_OK) {
         status = m3_compile_nodes(session, graph, error);
+    }
+    if (status == M3_STATUS_OK) {
+        status = m3_session_plan_runs(session, graph, error);
     }
     free(producers);
     free(last_uses);

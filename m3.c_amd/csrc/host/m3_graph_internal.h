@@ -49,6 +49,14 @@ struct m3_session {
     m3_provider_kind *providers;
     m3_command *commands;
     size_t node_count;
+    /* What m3_session_run executes: the commands, with each fused run of
+     * ADD/SUB/MUL/DIV commands replaced by one elementwise-program command
+     * whose words live in program_words (host) and program_storage. */
+    m3_command *run_commands;
+    m3_provider_kind *run_providers;
+    size_t run_count;
+    uint32_t *program_words;
+    m3_storage *program_storage;
     void *scratch;
     size_t scratch_capacity;
     size_t allocated_bytes;
@@ -57,5 +65,9 @@ struct m3_session {
 m3_status m3_graph_bind_command(const m3_graph_node_desc *description,
                                 m3_tensor_view *views, size_t value_count,
                                 m3_command *command, m3_error *error);
+/* Builds run_commands/run_providers (m3_graph_fuse.c). */
+m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
+                               m3_error *error);
+void m3_session_free_runs(m3_session *session);
 
 #endif

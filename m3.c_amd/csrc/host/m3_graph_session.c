@@ -8,6 +8,8 @@
  * A run groups each maximal stretch of consecutive nodes with the same
  * provider into one command list. With the HIP provider every node of a
  * stretch is enqueued on one stream and the list waits once at its end.
+ * The list executed is the session's run list, in which fused runs of
+ * elementwise nodes appear as one elementwise-program command each.
  */
 #include "m3_graph_internal.h"
 
@@ -80,21 +82,22 @@ m3_status m3_session_run(m3_session *session, m3_error *error)
         return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
                             "session is null");
     }
-    while (begin < session->node_count) {
+    while (begin < session->run_count) {
         m3_scratch_arena scratch;
         size_t end = begin + 1U;
         m3_status status;
 
-        while (end < session->node_count &&
-               session->providers[end] == session->providers[begin]) {
+        while (end < session->run_count &&
+               session->run_providers[end] == session->run_providers[begin]) {
             ++end;
         }
         status = m3_scratch_arena_init(&scratch, session->scratch,
                                        session->scratch_capacity, error);
         if (status == M3_STATUS_OK) {
             status = m3_provider_execute_regular(
-                session->backend, session->providers[begin],
-                &session->commands[begin], end - begin, &scratch, error);
+                session->backend, session->run_providers[begin],
+                &session->run_commands[begin], end - begin, &scratch,
+                error);
         }
         if (status != M3_STATUS_OK) {
             return status;

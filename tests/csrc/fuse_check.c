@@ -1,0 +1,633 @@
+/*
+ * fuse_check.c - host check of the session compiler's elementwise fusion
+ * planner (m3.c_amd/csrc/host/m3_fuse.c) and of the program format it
+ * emits (m3_hip_launch_program in include/m3_hip.h).
+ *
+ * A graph is executed twice on the host: node by node, and with every
+ * group the planner forms replaced by its program, interpreted per element
+ * exactly as the kernel does (registers R0-R3 and F0-F3, FETCH, OP, STORE,
+ * m3_binary_f32_bits for each operation). Each value gets its own buffer;
+ * buffers the node-by-node run writes start as a sentinel NaN in the fused
+ * run, so a missing STORE or a read of an unwritten register shows. Every
+ * value that must reach memory (OUTPUT values, values read outside their
+ * producer's group, INPUT and CONSTANT values) is compared bit for bit.
+ * The words are also checked structurally (the rules of the launcher).
+ *
+ * Modes (one JSON line on stdout; exit status 1 on any mismatch):
+ *   fuse_check random <graphs> <seed> [planted]
+ *       Random graphs of ADD/SUB/MUL/DIV over F32 and F16 values with
+ *       array, scalar and differently sized operands, OUTPUT and TEMPORARY
+ *       roles, COPY nodes and nodes on another provider between them.
+ *       `planted` corrupts each plan before it runs (the first STORE is
+ *       turned into a store of another register, and the sources of
+ *       every SUB/DIV are swapped): the comparison must then fail.
+ *   fuse_check euler <steps>
+ *       The Euler CFG graph of the flow solver, 6 nodes per step; reports
+ *       the plan's shape and checks its result.
+ */
+#include "m3_fuse.h"
+#include "m3_hip.h"
+#include "m3_numeric.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define SENTINEL 0x7fbadbadU
+#define NO_GROUP SIZE_MAX
+
+typedef struct {
+    m3_fuse_value *values;
+    size_t value_count;
+    size_t value_capacity;
+    m3_fuse_node *nodes;
+    size_t node_count;
+    size_t node_capacity;
+    uint32_t **data; /* per value: element_count raw elements */
+} graph_t;
+
+static uint64_t rng_state;
+
+static uint64_t next_random(void)
+{
+    uint64_t z = (rng_state += 0x9e3779b97f4a7c15ULL);
+
+    z = (z ^ (z >> 30U)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27U)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31U);
+}
+
+static uint32_t below(uint32_t n)
+{
+    return (uint32_t)(next_random() % n);
+}
+
+static void *grow(void *array, size_t *capacity, size_t needed, size_t size)
+{
+    if (needed > *capacity) {
+        *capacity = needed * 2U;
+        array = realloc(array, *capacity * size);
+        if (array == NULL) {
+            fprintf(stderr, "out of memory\n");
+            exit(2);
+        }
+    }
+    return array;
+}
+
+static uint32_t add_value(graph_t *g, m3_graph_value_role role,
+                          m3_dtype dtype, uint64_t count)
+{
+    g->values = grow(g->values, &g->value_capacity, g->value_count + 1U,
+                     sizeof(*g->values));
+    g->values[g->value_count].role = role;
+    g->values[g->value_count].dtype = dtype;
+    g->values[g->value_count].element_count = count;
+    return (uint32_t)g->value_count++;
+}
+
+static void add_node(graph_t *g, m3_op_kind kind, uint32_t left,
+                     uint32_t right, uint32_t output, bool eligible)
+{
+    g->nodes = grow(g->nodes, &g->node_capacity, g->node_count + 1U,
+                    sizeof(*g->nodes));
+    g->nodes[g->node_count].kind = kind;
+    g->nodes[g->node_count].left = left;
+    g->nodes[g->node_count].right = right;
+    g->nodes[g->node_count].output = output;
+    g->nodes[g->node_count].eligible = eligible;
+    g->node_count += 1U;
+}
+
+/* Random F32 bits: mostly normal values near 1, with zeros, infinities,
+ * NaN payloads of both signs and subnormals. */
+static uint32_t random_f32(void)
+{
+    uint32_t pick = below(100U);
+    uint32_t bits = (uint32_t)next_random();
+
+    if (pick < 4U) {
+        return (bits & 0x80000000U) | 0x7f800000U | (bits & 0x7fffffU) | 1U;
+    }
+    if (pick < 6U) {
+        return (bits & 0x80000000U) | 0x7f800000U;
+    }
+    if (pick < 8U) {
+        return bits & 0x80000000U;
+    }
+    if (pick < 10U) {
+        return bits & 0x807fffffU;
+    }
+    return (bits & 0x807fffffU) | ((120U + below(14U)) << 23U);
+}
+
+static uint32_t load_f32(const graph_t *g, uint32_t value, uint64_t e)
+{
+    const m3_fuse_value *v = &g->values[value];
+    uint32_t raw = g->data[value][v->element_count == 1U ? 0U : e];
+
+    return m3_load_as_f32_bits(raw, (uint32_t)v->dtype);
+}
+
+static uint32_t op_of(m3_op_kind kind)
+{
+    return kind == M3_OP_ADD   ? M3N_ADD
+           : kind == M3_OP_MUL ? M3N_MUL
+           : kind == M3_OP_SUB ? M3N_SUB
+                               : M3N_DIV;
+}
+
+/* One node over all its elements, as the unfused provider runs it. */
+static void run_node(graph_t *g, size_t n)
+{
+    const m3_fuse_node *node = &g->nodes[n];
+    const m3_fuse_value *out = &g->values[node->output];
+    uint64_t e;
+
+    for (e = 0U; e < out->element_count; ++e) {
+        uint32_t result;
+
+        if (node->kind == M3_OP_COPY) {
+            result = load_f32(g, node->left, e);
+        } else {
+            result = m3_binary_f32_bits(op_of(node->kind),
+                                        load_f32(g, node->left, e),
+                                        load_f32(g, node->right, e));
+        }
+        g->data[node->output][e] =
+            m3_store_from_f32_bits(result, (uint32_t)out->dtype);
+    }
+}
+
+/* Structural check of a group's words (the launcher's rules). Returns
+ * the number of violations. */
+static size_t check_words(const m3_fuse_plan *plan, const m3_fuse_group *gr,
+                          const graph_t *g)
+{
+    const uint32_t *code = plan->code + gr->code_first;
+    size_t bad = 0U;
+    size_t pc = 0U;
+
+    if (gr->operand_count > M3_HIP_PROGRAM_MAX_OPERANDS ||
+        gr->code_count > M3_HIP_PROGRAM_MAX_WORDS) {
+        return 1U;
+    }
+    for (size_t p = 0U; p < gr->operand_count; ++p) {
+        const m3_fuse_operand *o = &plan->operands[gr->operand_first + p];
+
+        bad += o->value >= g->value_count;
+        bad += o->scalar != (g->values[o->value].element_count == 1U &&
+                             gr->element_count > 1U);
+    }
+    while (pc < gr->code_count) {
+        uint32_t w = code[pc];
+
+        switch (w & 3U) {
+        case M3_HIP_PROGRAM_FETCH: {
+            uint32_t n = ((w >> 2U) & 3U) + 1U;
+
+            bad += (w >> 4U) != 0U || pc + 1U >= gr->code_count;
+            for (uint32_t k = 0U; k < n && pc + 1U < gr->code_count; ++k) {
+                uint32_t index = (code[pc + 1U] >> (8U * k)) & 0xffU;
+
+                bad += index >= gr->operand_count ||
+                       plan->operands[gr->operand_first + index].scalar;
+            }
+            pc += 2U;
+            break;
+        }
+        case M3_HIP_PROGRAM_OP: {
+            uint32_t left = (w >> 8U) & 15U;
+            uint32_t right = (w >> 12U) & 15U;
+            uint32_t scalar = (w >> 16U) & 0xffU;
+
+            bad += (w & 0xc0U) != 0U || (w >> 24U) != 0U || left > 8U ||
+                   right > 8U;
+            if (left == 8U || right == 8U) {
+                bad += scalar >= gr->operand_count ||
+                       !plan->operands[gr->operand_first + scalar].scalar;
+            } else {
+                bad += scalar != 0U;
+            }
+            pc += 1U;
+            break;
+        }
+        case M3_HIP_PROGRAM_STORE: {
+            uint32_t index = (w >> 8U) & 0xffU;
+
+            bad += (w & 0xccU) != 0U || (w >> 16U) != 0U ||
+                   index >= gr->operand_count ||
+                   plan->operands[gr->operand_first + index].scalar;
+            pc += 1U;
+            break;
+        }
+        default:
+            bad += 1U;
+            pc += 1U;
+            break;
+        }
+    }
+    return bad;
+}
+
+/* The group's program over every element, as the kernel runs it. */
+static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
+                          const m3_fuse_group *gr)
+{
+    const uint32_t *code = plan->code + gr->code_first;
+    const m3_fuse_operand *operands = plan->operands + gr->operand_first;
+    size_t unwritten = 0U;
+    uint64_t e;
+
+    for (e = 0U; e < gr->element_count; ++e) {
+        uint32_t r[4] = {SENTINEL, SENTINEL, SENTINEL, SENTINEL};
+        uint32_t f[4] = {SENTINEL, SENTINEL, SENTINEL, SENTINEL};
+        bool r_set[4] = {false, false, false, false};
+        bool f_set[4] = {false, false, false, false};
+        size_t pc = 0U;
+
+        while (pc < gr->code_count) {
+            uint32_t w = code[pc];
+
+            if ((w & 3U) == M3_HIP_PROGRAM_FETCH) {
+                uint32_t n = ((w >> 2U) & 3U) + 1U;
+
+                for (uint32_t k = 0U; k < n; ++k) {
+                    uint32_t index = (code[pc + 1U] >> (8U * k)) & 0xffU;
+
+                    f[k] = load_f32(g, operands[index].value, e);
+                    f_set[k] = true;
+                }
+                pc += 2U;
+            } else if ((w & 3U) == M3_HIP_PROGRAM_OP) {
+                uint32_t kinds[2] = {(w >> 8U) & 15U, (w >> 12U) & 15U};
+                uint32_t x[2];
+
+                for (int k = 0; k < 2; ++k) {
+                    if (kinds[k] < 4U) {
+                        x[k] = r[kinds[k]];
+                        unwritten += !r_set[kinds[k]];
+                    } else if (kinds[k] < 8U) {
+                        x[k] = f[kinds[k] - 4U];
+                        unwritten += !f_set[kinds[k] - 4U];
+                    } else {
+                        x[k] = load_f32(
+                            g, operands[(w >> 16U) & 0xffU].value, 0U);
+                    }
+                }
+                r[(w >> 4U) & 3U] =
+                    m3_binary_f32_bits((w >> 2U) & 3U, x[0], x[1]);
+                r_set[(w >> 4U) & 3U] = true;
+                pc += 1U;
+            } else {
+                uint32_t src = (w >> 4U) & 3U;
+
+                g->data[operands[(w >> 8U) & 0xffU].value][e] = r[src];
+                unwritten += !r_set[src];
+                pc += 1U;
+            }
+        }
+    }
+    return unwritten;
+}
+
+/* Corrupts a plan: the first STORE stores another register, and the
+ * sources of every SUB and DIV are swapped. */
+static void plant(m3_fuse_plan *plan)
+{
+    bool first = true;
+
+    for (size_t gi = 0U; gi < plan->group_count; ++gi) {
+        const m3_fuse_group *gr = &plan->groups[gi];
+        uint32_t *code = plan->code + gr->code_first;
+        size_t pc = 0U;
+
+        while (pc < gr->code_count) {
+            uint32_t w = code[pc];
+
+            if ((w & 3U) == M3_HIP_PROGRAM_FETCH) {
+                pc += 2U;
+                continue;
+            }
+            if ((w & 3U) == M3_HIP_PROGRAM_OP &&
+                ((w >> 2U) & 3U) >= M3N_SUB) {
+                uint32_t left = (w >> 8U) & 15U;
+                uint32_t right = (w >> 12U) & 15U;
+
+                code[pc] = (w & ~0xff00U) | (right << 8U) | (left << 12U);
+            }
+            if ((w & 3U) == M3_HIP_PROGRAM_STORE && first) {
+                code[pc] = w ^ (1U << 4U);
+                first = false;
+            }
+            pc += 1U;
+        }
+    }
+}
+
+typedef struct {
+    size_t groups;
+    size_t fused_nodes;
+    size_t stores;
+    size_t internal;
+    size_t compared;
+    size_t mismatches;
+    size_t structure;
+    size_t unwritten;
+} stats_t;
+
+static void allocate_data(graph_t *g, uint32_t **data)
+{
+    for (size_t v = 0U; v < g->value_count; ++v) {
+        data[v] = malloc((size_t)g->values[v].element_count *
+                         sizeof(uint32_t));
+        if (data[v] == NULL) {
+            fprintf(stderr, "out of memory\n");
+            exit(2);
+        }
+    }
+}
+
+/* Plans g, runs it both ways and compares. */
+static void check_graph(graph_t *g, bool planted, stats_t *st)
+{
+    uint32_t **reference = calloc(g->value_count, sizeof(*reference));
+    uint32_t **fused = calloc(g->value_count, sizeof(*fused));
+    size_t *group_of = malloc(g->node_count * sizeof(*group_of));
+    m3_fuse_plan plan;
+    m3_error error;
+    size_t v;
+    size_t n;
+
+    allocate_data(g, reference);
+    allocate_data(g, fused);
+    for (v = 0U; v < g->value_count; ++v) {
+        const m3_fuse_value *val = &g->values[v];
+        bool given = val->role == M3_GRAPH_INPUT ||
+                     val->role == M3_GRAPH_CONSTANT;
+
+        for (uint64_t e = 0U; e < val->element_count; ++e) {
+            uint32_t bits = random_f32();
+
+            if (val->dtype == M3_DTYPE_F16) {
+                bits = m3_f32_to_f16_bits(bits);
+            }
+            reference[v][e] = given ? bits : SENTINEL;
+            fused[v][e] = reference[v][e];
+        }
+    }
+    if (m3_fuse_plan_build(g->values, g->value_count, g->nodes,
+                           g->node_count, &plan, &error) != M3_STATUS_OK) {
+        fprintf(stderr, "plan failed: %s\n", error.message);
+        exit(2);
+    }
+    if (planted) {
+        plant(&plan);
+    }
+    for (n = 0U; n < g->node_count; ++n) {
+        group_of[n] = NO_GROUP;
+    }
+    for (size_t gi = 0U; gi < plan.group_count; ++gi) {
+        const m3_fuse_group *gr = &plan.groups[gi];
+
+        st->groups += 1U;
+        st->fused_nodes += gr->node_count;
+        st->structure += check_words(&plan, gr, g);
+        for (size_t pc = 0U; pc < gr->code_count;) {
+            uint32_t w = plan.code[gr->code_first + pc];
+
+            st->stores += (w & 3U) == M3_HIP_PROGRAM_STORE;
+            pc += (w & 3U) == M3_HIP_PROGRAM_FETCH ? 2U : 1U;
+        }
+        for (n = gr->first_node; n < gr->first_node + gr->node_count; ++n) {
+            group_of[n] = gi;
+        }
+    }
+    g->data = reference;
+    for (n = 0U; n < g->node_count; ++n) {
+        run_node(g, n);
+    }
+    g->data = fused;
+    n = 0U;
+    while (n < g->node_count) {
+        if (group_of[n] != NO_GROUP) {
+            const m3_fuse_group *gr = &plan.groups[group_of[n]];
+
+            st->unwritten += run_program(g, &plan, gr);
+            n = gr->first_node + gr->node_count;
+        } else {
+            run_node(g, n);
+            n += 1U;
+        }
+    }
+    for (v = 0U; v < g->value_count; ++v) {
+        const m3_fuse_value *val = &g->values[v];
+        size_t producer = SIZE_MAX;
+        bool needed = val->role != M3_GRAPH_TEMPORARY;
+
+        for (n = 0U; n < g->node_count; ++n) {
+            if (g->nodes[n].output == v) {
+                producer = n;
+            }
+        }
+        for (n = 0U; n < g->node_count && !needed; ++n) {
+            const m3_fuse_node *node = &g->nodes[n];
+
+            if ((node->left == v || node->right == v) &&
+                (producer == SIZE_MAX || group_of[n] == NO_GROUP ||
+                 group_of[n] != group_of[producer])) {
+                needed = true;
+            }
+        }
+        if (!needed) {
+            st->internal += producer != SIZE_MAX &&
+                            group_of[producer] != NO_GROUP;
+            continue;
+        }
+        st->compared += 1U;
+        if (memcmp(reference[v], fused[v],
+                   (size_t)val->element_count * sizeof(uint32_t)) != 0) {
+            st->mismatches += 1U;
+        }
+    }
+    for (v = 0U; v < g->value_count; ++v) {
+        free(reference[v]);
+        free(fused[v]);
+    }
+    free(reference);
+    free(fused);
+    free(group_of);
+    m3_fuse_plan_free(&plan);
+}
+
+static void random_graph(graph_t *g)
+{
+    static const m3_op_kind kinds[] = {M3_OP_ADD, M3_OP_MUL, M3_OP_SUB,
+                                       M3_OP_DIV};
+    const uint64_t counts[3] = {1U + below(40U), 1U, 1U + below(12U)};
+    size_t nodes = 2U + below(40U);
+
+    memset(g, 0, sizeof(*g));
+    for (int k = 0; k < 3; ++k) {
+        (void)add_value(g, below(2U) ? M3_GRAPH_INPUT : M3_GRAPH_CONSTANT,
+                        M3_DTYPE_F32, counts[0]);
+    }
+    (void)add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, 1U);
+    (void)add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, 1U);
+    (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_F32, counts[2]);
+    (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_F16, counts[0]);
+    for (size_t n = 0U; n < nodes; ++n) {
+        uint32_t left = below((uint32_t)g->value_count);
+        uint64_t lc = g->values[left].element_count;
+        uint32_t right;
+        uint64_t rc;
+        m3_dtype dtype = M3_DTYPE_F32;
+        bool copy = below(100U) < 10U;
+        m3_graph_value_role role =
+            n + 1U == nodes || below(100U) < 15U ? M3_GRAPH_OUTPUT
+                                                 : M3_GRAPH_TEMPORARY;
+
+        do {
+            right = below((uint32_t)g->value_count);
+            rc = g->values[right].element_count;
+        } while (!(rc == lc || rc == 1U || lc == 1U));
+        if (g->values[left].dtype == M3_DTYPE_F16 ||
+            g->values[right].dtype == M3_DTYPE_F16) {
+            dtype = below(2U) ? M3_DTYPE_F16 : M3_DTYPE_F32;
+        }
+        if (copy) {
+            uint32_t out = add_value(g, role, g->values[left].dtype, lc);
+
+            add_node(g, M3_OP_COPY, left, left, out, false);
+            continue;
+        }
+        add_node(g, kinds[below(4U)], left, right,
+                 add_value(g, role, dtype, lc > rc ? lc : rc),
+                 below(100U) >= 5U);
+    }
+}
+
+static void euler_graph(graph_t *g, size_t steps, uint64_t count)
+{
+    uint32_t x;
+    uint32_t minus_one;
+    uint32_t scale;
+    uint32_t dt;
+
+    memset(g, 0, sizeof(*g));
+    x = add_value(g, M3_GRAPH_INPUT, M3_DTYPE_F32, count);
+    minus_one = add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, 1U);
+    scale = add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, 1U);
+    dt = add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, 1U);
+    for (size_t k = 0U; k < steps; ++k) {
+        uint32_t vu = add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, count);
+        uint32_t vc = add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, count);
+        uint32_t t[5];
+        uint32_t next;
+
+        for (int i = 0; i < 5; ++i) {
+            t[i] = add_value(g, M3_GRAPH_TEMPORARY, M3_DTYPE_F32, count);
+        }
+        next = add_value(g,
+                         k + 1U == steps ? M3_GRAPH_OUTPUT
+                                         : M3_GRAPH_TEMPORARY,
+                         M3_DTYPE_F32, count);
+        add_node(g, M3_OP_MUL, vu, minus_one, t[0], true);
+        add_node(g, M3_OP_ADD, vc, t[0], t[1], true);
+        add_node(g, M3_OP_MUL, t[1], scale, t[2], true);
+        add_node(g, M3_OP_ADD, vu, t[2], t[3], true);
+        add_node(g, M3_OP_MUL, t[3], dt, t[4], true);
+        add_node(g, M3_OP_ADD, x, t[4], next, true);
+        x = next;
+    }
+}
+
+static void free_graph(graph_t *g)
+{
+    free(g->values);
+    free(g->nodes);
+}
+
+static void print_stats(const char *mode, size_t graphs, const stats_t *st)
+{
+    printf("{\"mode\": \"%s\", \"graphs\": %zu, \"groups\": %zu, "
+           "\"fused_nodes\": %zu, \"stores\": %zu, \"internal_values\": %zu, "
+           "\"compared_values\": %zu, \"mismatches\": %zu, "
+           "\"structure_errors\": %zu, \"unwritten_reads\": %zu",
+           mode, graphs, st->groups, st->fused_nodes, st->stores,
+           st->internal, st->compared, st->mismatches, st->structure,
+           st->unwritten);
+}
+
+int main(int argc, char **argv)
+{
+    stats_t st;
+
+    memset(&st, 0, sizeof(st));
+    if (argc >= 4 && strcmp(argv[1], "random") == 0) {
+        size_t graphs = strtoull(argv[2], NULL, 10);
+        bool planted = argc >= 5 && strcmp(argv[4], "planted") == 0;
+
+        rng_state = strtoull(argv[3], NULL, 10);
+        for (size_t i = 0U; i < graphs; ++i) {
+            graph_t g;
+
+            random_graph(&g);
+            check_graph(&g, planted, &st);
+            free_graph(&g);
+        }
+        print_stats(planted ? "planted" : "random", graphs, &st);
+        printf("}\n");
+        return st.mismatches == 0U && st.structure == 0U &&
+                       st.unwritten == 0U
+                   ? 0
+                   : 1;
+    }
+    if (argc == 3 && strcmp(argv[1], "euler") == 0) {
+        size_t steps = strtoull(argv[2], NULL, 10);
+        graph_t g;
+        m3_fuse_plan plan;
+        m3_error error;
+        size_t fetch_loads = 0U;
+
+        rng_state = 7U;
+        euler_graph(&g, steps, 37U);
+        if (m3_fuse_plan_build(g.values, g.value_count, g.nodes, g.node_count,
+                               &plan, &error) != M3_STATUS_OK) {
+            fprintf(stderr, "plan failed: %s\n", error.message);
+            return 2;
+        }
+        for (size_t gi = 0U; gi < plan.group_count; ++gi) {
+            const m3_fuse_group *gr = &plan.groups[gi];
+            size_t pc = 0U;
+
+            while (pc < gr->code_count) {
+                uint32_t w = plan.code[gr->code_first + pc];
+
+                if ((w & 3U) == M3_HIP_PROGRAM_FETCH) {
+                    fetch_loads += ((w >> 2U) & 3U) + 1U;
+                    pc += 2U;
+                } else {
+                    pc += 1U;
+                }
+            }
+        }
+        check_graph(&g, false, &st);
+        print_stats("euler", 1U, &st);
+        printf(", \"first_group_nodes\": %zu, \"first_group_operands\": %zu, "
+               "\"first_group_words\": %zu, \"fetched_arrays\": %zu}\n",
+               plan.group_count ? plan.groups[0].node_count : 0U,
+               plan.group_count ? plan.groups[0].operand_count : 0U,
+               plan.group_count ? plan.groups[0].code_count : 0U,
+               fetch_loads);
+        m3_fuse_plan_free(&plan);
+        free_graph(&g);
+        return st.mismatches == 0U && st.structure == 0U &&
+                       st.unwritten == 0U
+                   ? 0
+                   : 1;
+    }
+    fprintf(stderr, "usage: fuse_check random <graphs> <seed> [planted] | "
+                    "euler <steps>\n");
+    return 2;
+}

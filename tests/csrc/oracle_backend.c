@@ -7,6 +7,10 @@
  * planner, scheduler and session I/O of libm3.so can be tested on the CPU.
  * It reports itself as M3_BACKEND_HIP so the scheduler treats it as the GPU
  * provider, records every executed list, and is never part of the product.
+ * Elementwise programs (the session compiler's fused runs) are interpreted
+ * from their words, whose operand addresses are host addresses here, with
+ * the oracle's binary operation for each F32 operation; the words in
+ * storage must equal the host copy.
  */
 #include "m3_backend.h"
 #include "m3_oracle.h"
@@ -27,12 +31,14 @@ static size_t g_list_count;
 static size_t g_allocations;
 static size_t g_fail_allocation_at; /* 0: never */
 static size_t g_reserved;
+static size_t g_programs;
 
 void oracle_backend_reset(void);
 size_t oracle_backend_log(int *kinds, int *lists, size_t capacity);
 size_t oracle_backend_lists(void);
 size_t oracle_backend_reserved(void);
 void oracle_backend_fail_allocation_at(size_t index);
+size_t oracle_backend_programs(void);
 m3_status oracle_backend_create(m3_backend **backend, m3_error *error);
 
 void oracle_backend_reset(void)
@@ -42,6 +48,12 @@ void oracle_backend_reset(void)
     g_allocations = 0U;
     g_fail_allocation_at = 0U;
     g_reserved = 0U;
+    g_programs = 0U;
+}
+
+size_t oracle_backend_programs(void)
+{
+    return g_programs;
 }
 
 size_t oracle_backend_log(int *kinds, int *lists, size_t capacity)
@@ -132,6 +144,98 @@ static void to_oracle(const m3_tensor_view *view, oracle_view *out)
     }
 }
 
+/* One F32 operation through the oracle, on one-element views. */
+static uint32_t oracle_op1(uint32_t op, uint32_t a, uint32_t b)
+{
+    uint32_t values[3] = {a, b, 0U};
+    oracle_view v[3];
+    int k;
+
+    for (k = 0; k < 3; ++k) {
+        memset(&v[k], 0, sizeof(v[k]));
+        v[k].data = &values[k];
+        v[k].dtype = ORACLE_F32;
+        v[k].rank = 1U;
+        v[k].shape[0] = 1U;
+        v[k].byte_strides[0] = 4U;
+    }
+    (void)oracle_binary(op, &v[0], &v[1], &v[2]);
+    return values[2];
+}
+
+static const uint32_t *operand_address(const uint32_t *operands,
+                                       uint32_t index)
+{
+    uint64_t low = operands[2U * index];
+    uint64_t high = operands[2U * index + 1U];
+
+    return (const uint32_t *)(uintptr_t)(((high << 32U) | low) &
+                                         ~(uint64_t)1U);
+}
+
+/* Runs an elementwise program (layout in m3_hip.h) element by element. */
+static int run_program(const m3_op_elementwise_program *program)
+{
+    const uint32_t *words = program->words;
+    const uint32_t operand_count = words[1];
+    const uint32_t code_words = words[2];
+    const uint64_t count = (uint64_t)words[3] | ((uint64_t)words[4] << 32U);
+    const uint32_t *operands = words + 8;
+    const uint32_t *code = operands + 2U * operand_count;
+    const uint8_t *stored =
+        (const uint8_t *)m3_storage_data(program->storage);
+    uint64_t e;
+
+    if (stored == NULL ||
+        memcmp(stored + program->byte_offset, words,
+               program->word_count * sizeof(uint32_t)) != 0 ||
+        program->word_count != 8U + 2U * operand_count + code_words) {
+        return (int)M3_STATUS_INTERNAL;
+    }
+    for (e = 0U; e < count; ++e) {
+        uint32_t r[4] = {0U, 0U, 0U, 0U};
+        uint32_t f[4] = {0U, 0U, 0U, 0U};
+        uint32_t pc = 0U;
+
+        while (pc < code_words) {
+            uint32_t w = code[pc];
+
+            if ((w & 3U) == 0U) { /* FETCH */
+                uint32_t n = ((w >> 2U) & 3U) + 1U;
+                uint32_t k;
+
+                for (k = 0U; k < n; ++k) {
+                    f[k] = operand_address(
+                        operands, (code[pc + 1U] >> (8U * k)) & 0xffU)[e];
+                }
+                pc += 2U;
+            } else if ((w & 3U) == 1U) { /* OP */
+                uint32_t kinds[2] = {(w >> 8U) & 15U, (w >> 12U) & 15U};
+                uint32_t x[2];
+                int k;
+
+                for (k = 0; k < 2; ++k) {
+                    x[k] = kinds[k] < 4U   ? r[kinds[k]]
+                           : kinds[k] < 8U ? f[kinds[k] - 4U]
+                                           : operand_address(
+                                                 operands,
+                                                 (w >> 16U) & 0xffU)[0];
+                }
+                r[(w >> 4U) & 3U] = oracle_op1((w >> 2U) & 3U, x[0], x[1]);
+                pc += 1U;
+            } else { /* STORE */
+                uint32_t *out = (uint32_t *)(uintptr_t)operand_address(
+                    operands, (w >> 8U) & 0xffU);
+
+                out[e] = r[(w >> 4U) & 3U];
+                pc += 1U;
+            }
+        }
+    }
+    g_programs += 1U;
+    return 0;
+}
+
 static m3_status execute(void *context, const m3_command *commands,
                          size_t count, m3_scratch_arena *scratch,
                          m3_error *error)
@@ -147,6 +251,25 @@ static m3_status execute(void *context, const m3_command *commands,
         oracle_view o;
         int status = 0;
 
+        if (c->kind == M3_OP_ELEMENTWISE_PROGRAM) {
+            const m3_op_elementwise_program *program =
+                &c->descriptor.elementwise_program;
+            size_t k;
+
+            /* the log lists the fused commands, in order */
+            for (k = 0U; k < program->command_count &&
+                         g_log_count < ORACLE_BACKEND_LOG;
+                 ++k) {
+                g_log_kinds[g_log_count] = (int)program->commands[k].kind;
+                g_log_lists[g_log_count] = (int)g_list_count;
+                g_log_count += 1U;
+            }
+            if (run_program(program) != 0) {
+                return m3_error_set(error, M3_STATUS_INTERNAL,
+                                    "oracle backend: malformed program");
+            }
+            continue;
+        }
         if (g_log_count < ORACLE_BACKEND_LOG) {
             g_log_kinds[g_log_count] = (int)c->kind;
             g_log_lists[g_log_count] = (int)g_list_count;

@@ -1,0 +1,86 @@
+"""CPU checks of the session compiler's elementwise fusion planner
+(m3.c_amd/csrc/host/m3_fuse.c) with tests/csrc/fuse_check.c built for the
+host.
+
+Each planned graph runs twice on the host: node by node with the
+reference's per-element operation (load as F32, one F32 operation, round to
+the output dtype; src/m3_op_execute_basic.c:61-77), and with every fused
+group replaced by its program interpreted the way the kernel runs it. Every
+value that has to reach memory must agree bit for bit, NaN payloads
+included. A plan with planted mistakes (a STORE of the wrong register, SUB
+and DIV with swapped operands) must be caught by the same comparison.
+"""
+import json
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+SOURCES = [os.path.join(HERE, "csrc", "fuse_check.c"),
+           os.path.join(ROOT, "m3.c_amd", "csrc", "host", "m3_fuse.c"),
+           os.path.join(ROOT, "m3.c_amd", "csrc", "host", "m3_error.c")]
+HEADERS = [os.path.join(ROOT, "m3.c_amd", "csrc", "host", "m3_fuse.h"),
+           os.path.join(ROOT, "m3.c_amd", "csrc", "hip", "m3_numeric.h"),
+           os.path.join(ROOT, "include", "m3_hip.h"),
+           os.path.join(ROOT, "include", "m3_backend.h")]
+TOOL = os.path.join(HERE, "_build", "fuse_check")
+
+
+def build_checker():
+    newest = max(os.path.getmtime(p) for p in SOURCES + HEADERS)
+    if not os.path.exists(TOOL) or os.path.getmtime(TOOL) < newest:
+        os.makedirs(os.path.dirname(TOOL), exist_ok=True)
+        subprocess.run(
+            ["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-Werror",
+             "-ffp-contract=off", "-D_POSIX_C_SOURCE=200809L",
+             "-I" + os.path.join(ROOT, "include"),
+             "-I" + os.path.join(ROOT, "m3.c_amd", "csrc", "host"),
+             "-I" + os.path.join(ROOT, "m3.c_amd", "csrc", "hip"),
+             "-o", TOOL] + SOURCES, check=True)
+    return TOOL
+
+
+def run(*args, expect_ok=True):
+    result = subprocess.run([build_checker(), *args], capture_output=True,
+                            text=True, timeout=300)
+    assert (result.returncode == 0) == expect_ok, result.stderr
+    return json.loads(result.stdout)
+
+
+def test_random_plans_match_node_by_node():
+    for seed in (1, 2):
+        r = run("random", "3000", str(seed))
+        assert r["mismatches"] == 0
+        assert r["structure_errors"] == 0
+        assert r["unwritten_reads"] == 0
+        # the graphs do fuse, and fused temporaries stay out of memory
+        assert r["groups"] > 5000
+        assert r["internal_values"] > 5000
+        assert r["compared_values"] > 50000
+
+
+def test_planted_plan_mistakes_are_detected():
+    r = run("random", "500", "3", "planted", expect_ok=False)
+    assert r["mismatches"] > 100
+
+
+def test_euler_graph_is_one_program():
+    """30 CFG + Euler steps (6 nodes each, src/m3_flow_solver_math.c:
+    36-135): one program, every temporary in registers, one store (the
+    output), each of x and the 60 per-step tensors fetched about once."""
+    r = run("euler", "30")
+    assert r["mismatches"] == 0 and r["structure_errors"] == 0
+    assert r["groups"] == 1
+    assert r["first_group_nodes"] == 180
+    assert r["stores"] == 1
+    assert r["internal_values"] == 179
+    # x, 30 vu, 30 vc, the three scalars and the output
+    assert r["first_group_operands"] == 65
+    assert 61 <= r["fetched_arrays"] <= 64
+
+
+def test_long_chains_split_at_the_operand_limit():
+    r = run("euler", "200")
+    assert r["mismatches"] == 0 and r["structure_errors"] == 0
+    assert r["groups"] == 2
+    assert r["fused_nodes"] == 1200

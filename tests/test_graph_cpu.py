@@ -44,6 +44,7 @@ def backend_lib():
     fake.oracle_backend_lists.restype = ctypes.c_size_t
     fake.oracle_backend_reserved.restype = ctypes.c_size_t
     fake.oracle_backend_fail_allocation_at.argtypes = [ctypes.c_size_t]
+    fake.oracle_backend_programs.restype = ctypes.c_size_t
     factory = ctypes.cast(fake.oracle_backend_create, ctypes.c_void_p)
     lib.m3_provider_set_gpu_factory.argtypes = [ctypes.c_void_p]
     lib.m3_provider_set_gpu_factory(factory)
@@ -358,3 +359,155 @@ def test_command_executor_runs_flow_math(fake, backend_lib):
     for storage in storages:
         lib.m3_storage_free(storage)
     lib.m3_backend_free(backend)
+
+
+# ---- fused elementwise runs ------------------------------------------------
+
+def _session_outputs(graph_builder, fusion, fake):
+    """Builds, runs and reads a graph with fusion on or off; returns the
+    outputs, the plan and the number of programs the backend ran."""
+    previous = os.environ.get("M3_HIP_FUSION")
+    os.environ["M3_HIP_FUSION"] = "1" if fusion else "0"
+    try:
+        g, feeds, outputs = graph_builder()
+        fake.oracle_backend_reset()
+        session = m3.Session(g)
+    finally:
+        if previous is None:
+            del os.environ["M3_HIP_FUSION"]
+        else:
+            os.environ["M3_HIP_FUSION"] = previous
+    g.free()
+    plan = session.plan()
+    for vid, data in feeds:
+        session.write(vid, data)
+    session.run()
+    results = [session.read(vid, np.zeros(shape, np.float32))
+               for vid, shape in outputs]
+    programs = fake.oracle_backend_programs()
+    kinds, _ = log_of(fake)
+    session.free()
+    return results, (plan.storage_slot_count, plan.allocated_bytes), \
+        programs, kinds
+
+
+def _specials(rng, shape):
+    data = rng.standard_normal(shape).astype(np.float32)
+    bits = data.view(np.uint32)
+    pick = rng.random(shape)
+    payload = rng.integers(1, 1 << 22, shape, dtype=np.uint32)
+    bits[pick < 0.03] = (0x7f800000 | payload)[pick < 0.03]
+    bits[(pick >= 0.03) & (pick < 0.05)] = 0xff800000
+    bits[(pick >= 0.05) & (pick < 0.06)] = 0
+    return data
+
+
+def _random_chain_graph(seed):
+    """Elementwise DAGs with scalar operands, OUTPUT values read again,
+    COPY barriers and temporaries read by several nodes."""
+    def build():
+        rng = np.random.default_rng(seed)
+        shape = (3, 5, 7)
+        g = m3.Graph()
+        values = []
+        feeds = []
+        outputs = []
+        for _ in range(3):
+            vid = g.add_value(m3.INPUT, m3.F32, shape)
+            feeds.append((vid, _specials(rng, shape)))
+            values.append((vid, shape))
+        for _ in range(2):
+            vid = g.add_value(m3.CONSTANT, m3.F32, (1,))
+            g.set_constant(vid, (rng.standard_normal(1) + 2.0)
+                           .astype(np.float32))
+            values.append((vid, (1,)))
+        kinds = [m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV]
+        for n in range(30):
+            role = m3.OUTPUT if n == 29 or rng.random() < 0.2 \
+                else m3.TEMPORARY
+            a = values[rng.integers(len(values))]
+            if rng.random() < 0.1:
+                out_shape = a[1]
+                vid = g.add_value(role, m3.F32, out_shape)
+                g.add_node(m3.OP_COPY, [a[0]], [vid])
+            else:
+                b = values[rng.integers(len(values))]
+                out_shape = shape if shape in (a[1], b[1]) else (1,)
+                vid = g.add_value(role, m3.F32, out_shape)
+                g.add_node(kinds[rng.integers(4)], [a[0], b[0]], [vid])
+            values.append((vid, out_shape))
+            if role == m3.OUTPUT:
+                outputs.append((vid, out_shape))
+        return g, feeds, outputs
+    return build
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_fused_runs_equal_unfused_runs(fake, seed):
+    """Every OUTPUT, NaN payloads included, is identical with and without
+    fusion; the slot plan does not change; fused runs do execute."""
+    build = _random_chain_graph(1000 + seed)
+    fused, plan_on, programs_on, kinds_on = _session_outputs(build, True,
+                                                             fake)
+    plain, plan_off, programs_off, kinds_off = _session_outputs(build, False,
+                                                                fake)
+    assert plan_on == plan_off
+    assert programs_off == 0
+    assert kinds_on == kinds_off
+    for a, b in zip(fused, plain):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_fusion_happens_on_random_graphs(fake):
+    total = 0
+    for seed in range(8):
+        build = _random_chain_graph(1000 + seed)
+        total += _session_outputs(build, True, fake)[2]
+    assert total >= 8
+
+
+def _euler_graph(steps, shape):
+    def build():
+        rng = m3.rng_new(0, 0)
+        count = int(np.prod(shape))
+        x0 = m3.rng_fill("normal", count, seed=0, a=1.0,
+                         rng=rng).reshape(shape)
+        g = m3.Graph()
+        vx = g.add_value(m3.INPUT, m3.F32, shape)
+        consts = {}
+        for name, value in (("m1", -1.0), ("s", 3.0), ("dt", 1.0 / 30.0)):
+            vid = g.add_value(m3.CONSTANT, m3.F32, (1,))
+            g.set_constant(vid, np.array([value], np.float32))
+            consts[name] = vid
+        current = vx
+        for k in range(steps):
+            vu = g.add_value(m3.CONSTANT, m3.F32, shape)
+            vc = g.add_value(m3.CONSTANT, m3.F32, shape)
+            g.set_constant(vu, m3.rng_fill("normal", count, seed=0, a=1.0,
+                                           rng=rng).reshape(shape))
+            g.set_constant(vc, m3.rng_fill("normal", count, seed=0, a=1.0,
+                                           rng=rng).reshape(shape))
+            t = [g.add_value(m3.TEMPORARY, m3.F32, shape) for _ in range(5)]
+            nxt = g.add_value(m3.OUTPUT if k == steps - 1 else m3.TEMPORARY,
+                              m3.F32, shape)
+            g.add_node(m3.OP_MUL, [vu, consts["m1"]], [t[0]])
+            g.add_node(m3.OP_ADD, [vc, t[0]], [t[1]])
+            g.add_node(m3.OP_MUL, [t[1], consts["s"]], [t[2]])
+            g.add_node(m3.OP_ADD, [vu, t[2]], [t[3]])
+            g.add_node(m3.OP_MUL, [t[3], consts["dt"]], [t[4]])
+            g.add_node(m3.OP_ADD, [current, t[4]], [nxt])
+            current = nxt
+        return g, [(vx, x0)], [(current, shape)]
+    return build
+
+
+def test_euler_graph_runs_as_one_program(fake):
+    """The 6-step CFG + Euler graph becomes one program (every node in it,
+    in order), with the unfused slot plan and result."""
+    build = _euler_graph(6, (2, 8, 12))
+    fused, plan_on, programs, kinds = _session_outputs(build, True, fake)
+    plain, plan_off, _, kinds_off = _session_outputs(build, False, fake)
+    assert programs == 1
+    assert kinds == kinds_off and len(kinds) == 36
+    assert plan_on == plan_off
+    assert np.array_equal(fused[0].view(np.uint32), plain[0].view(np.uint32))
