@@ -554,8 +554,8 @@ def main():
         # the output: 62 tensors of HBM traffic per run
         fused_bytes = (2 * 30 + 2) * tensor
         w = Workload("euler", build_euler(x, vus, vcs), [x] + vus + vcs,
-                     nbytes, ["m3_program", "m3_binary_add",
-                              "m3_binary_mul"], 1, cpu)
+                     nbytes, ["m3_program", "m3_program_interpreted",
+                              "m3_binary_add", "m3_binary_mul"], 1, cpu)
         wall, kus, launches, kernels, run_kernel_ms = w.measure(
             max(args.steps // 4, 3), args.warmup)
         parity = None

@@ -45,7 +45,13 @@ struct m3_hip_device {
     std::vector<m3_hip_pending_time> pending;
     std::vector<hipEvent_t> spare_events;
     std::vector<m3_hip_time_total> totals;
+    char arch[64]; /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
+    /* kernels generated for elementwise programs (m3_hip_program.hip) */
+    struct m3_program_cache *programs;
 };
+
+/* Unloads the generated kernels of a device (m3_hip_program.hip). */
+void m3_program_cache_release(m3_hip_device *device);
 
 /* Writes a formatted message into a caller buffer (which may be NULL). */
 int m3_hip_fail(char *message, size_t capacity, int code, const char *format,

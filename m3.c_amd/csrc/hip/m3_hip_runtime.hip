@@ -227,6 +227,8 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
     device->ordinal = ordinal;
     std::snprintf(device->name, sizeof(device->name), "%s (%s)",
                   properties.name, properties.gcnArchName);
+    std::snprintf(device->arch, sizeof(device->arch), "%s",
+                  properties.gcnArchName);
     device->total_bytes = (uint64_t)properties.totalGlobalMem;
     device->compute_units = (uint32_t)properties.multiProcessorCount;
     device->lds_per_block = (uint32_t)properties.sharedMemPerBlock;
@@ -263,6 +265,7 @@ extern "C" void m3_hip_device_close(m3_hip_device *device)
     for (hipEvent_t event : device->spare_events) {
         (void)hipEventDestroy(event);
     }
+    m3_program_cache_release(device);
     if (device->scan_flags != nullptr) {
         (void)hipFree(device->scan_flags);
     }

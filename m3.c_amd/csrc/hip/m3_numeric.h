@@ -23,11 +23,22 @@
 #ifndef M3_NUMERIC_H
 #define M3_NUMERIC_H
 
+#if defined(__HIPCC_RTC__)
+/* runtime compilation: no system headers; its runtime header declares the
+ * fixed-width types in namespace __hip_internal */
+using __hip_internal::int32_t;
+using __hip_internal::uint16_t;
+using __hip_internal::uint32_t;
+using __hip_internal::uint64_t;
+#else
 #include <stdint.h>
 #include <string.h>
+#endif
 
 #if defined(__HIPCC__)
+#if !defined(__HIPCC_RTC__)
 #include <hip/hip_runtime.h>
+#endif
 #define M3_HD static __host__ __device__ inline __attribute__((always_inline))
 #else
 #define M3_HD static inline

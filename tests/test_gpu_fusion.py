@@ -1,12 +1,15 @@
 """Fused elementwise runs on the HIP provider (GPU).
 
 The session compiler fuses runs of F32 ADD/SUB/MUL/DIV nodes into
-elementwise programs (m3_hip_launch_program). Each test runs the same graph
-with fusion on and off (M3_HIP_FUSION=0 at session creation) and requires
-every OUTPUT to be identical bit for bit, NaN payloads included; the
-unfused path is the per-node kernels that the parity tests pin to the
-oracle. The CFG + Euler graph is also checked against the same float32
-operations in numpy and must run as one program launch.
+elementwise programs (m3_hip_launch_program), which run as kernels
+generated from the program at first use (timed as m3_program) or, with
+M3_HIP_PROGRAM_JIT=0, in the interpreter kernel (m3_program_interpreted).
+Each test runs the same graph with fusion on and off (M3_HIP_FUSION=0 at
+session creation) and requires every OUTPUT to be identical bit for bit,
+NaN payloads included; the unfused path is the per-node kernels that the
+parity tests pin to the oracle. The CFG + Euler graph is also checked
+against the same float32 operations in numpy and must run as one program
+launch.
 """
 import ctypes
 import os
@@ -19,17 +22,35 @@ from conftest import m3
 pytestmark = pytest.mark.gpu
 
 
-def run_session(build, fusion):
-    previous = os.environ.get("M3_HIP_FUSION")
-    os.environ["M3_HIP_FUSION"] = "1" if fusion else "0"
-    try:
+class environment:
+    """Sets environment variables for a block and restores them."""
+
+    def __init__(self, **values):
+        self.values = values
+        self.saved = {}
+
+    def __enter__(self):
+        for key, value in self.values.items():
+            self.saved[key] = os.environ.get(key)
+            os.environ[key] = value
+
+    def __exit__(self, *exc):
+        for key, value in self.saved.items():
+            if value is None:
+                del os.environ[key]
+            else:
+                os.environ[key] = value
+
+
+def run_session(build, fusion, generated=True):
+    with environment(M3_HIP_FUSION="1" if fusion else "0",
+                     M3_HIP_PROGRAM_JIT="1" if generated else "0"):
         g, feeds, outputs = build()
         session = m3.Session(g)
-    finally:
-        if previous is None:
-            del os.environ["M3_HIP_FUSION"]
-        else:
-            os.environ["M3_HIP_FUSION"] = previous
+        return _run(session, g, feeds, outputs)
+
+
+def _run(session, g, feeds, outputs):
     g.free()
     plan = session.plan()
     for node in range(plan.node_count):
@@ -105,21 +126,27 @@ def chain_graph(seed, shape, nodes=40):
     return build
 
 
+@pytest.mark.parametrize("generated", [True, False])
 @pytest.mark.parametrize("seed,shape", [(0, (3, 5, 7)), (1, (3, 5, 7)),
                                         (2, (2, 33, 129)),
                                         (3, (4, 1000, 37)),
                                         (4, (1, 1, 4096)), (5, (1,))])
-def test_fused_equals_unfused(gpu, seed, shape):
-    print("fusion chain graph seed", seed, "shape", shape, flush=True)
+def test_fused_equals_unfused(gpu, seed, shape, generated):
+    print("fusion chain graph seed", seed, "shape", shape, "generated",
+          generated, flush=True)
     build = chain_graph(2000 + seed, shape)
-    fused, plan_on, kernels_on = run_session(build, True)
+    fused, plan_on, kernels_on = run_session(build, True, generated)
     plain, plan_off, kernels_off = run_session(build, False)
     assert plan_on == plan_off
     assert "m3_program" not in kernels_off
+    assert "m3_program_interpreted" not in kernels_off
     for a, b in zip(fused, plain):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    ran = "m3_program" if generated else "m3_program_interpreted"
+    other = "m3_program_interpreted" if generated else "m3_program"
+    assert other not in kernels_on
     if shape != (1,):
-        assert kernels_on.get("m3_program", (0, 0.0))[0] >= 1
+        assert kernels_on.get(ran, (0, 0.0))[0] >= 1
 
 
 def euler_graph(steps, shape):
@@ -167,18 +194,20 @@ def euler_graph(steps, shape):
     return build
 
 
-def test_euler_graph_is_one_program(gpu):
+@pytest.mark.parametrize("generated", [True, False])
+def test_euler_graph_is_one_program(gpu, generated):
     """30 CFG + Euler steps (src/m3_flow_solver_math.c:36-135) at reduced
     size: one program launch per run, the numpy float32 result bit for bit,
     and the unfused plan's slots and bytes."""
     shape = (2, 64, 96)
     build = euler_graph(30, shape)
-    fused, plan_on, kernels = run_session(build, True)
+    fused, plan_on, kernels = run_session(build, True, generated)
     expected = euler_graph.expected
     plain, plan_off, _ = run_session(build, False)
+    name = "m3_program" if generated else "m3_program_interpreted"
     assert plan_on == plan_off
-    assert kernels["m3_program"][0] == 1
-    assert set(kernels) == {"m3_program"}
+    assert kernels[name][0] == 1
+    assert set(kernels) == {name}
     assert np.array_equal(fused[0].view(np.uint32), expected.view(np.uint32))
     assert np.array_equal(plain[0].view(np.uint32), expected.view(np.uint32))
 
