@@ -306,4 +306,171 @@ M3_HD float m3_sinf(float y)
     return m3_sinf_medium(y);
 }
 
+/* expf of the libm for every float input: a NaN gives itself quieted (the
+ * library returns x + x), inputs above log(2^128) = 0x1.62e42ep6 and +inf
+ * overflow to +inf (the library's overflow path), and everything else,
+ * -inf included, is m3_expf, which rounds to +0 below log(2^-150) as the
+ * library's underflow path returns. */
+M3_HD float m3_expf_any(float x)
+{
+    uint32_t bits = m3_f32_bits(x);
+
+    if ((bits & 0x7fffffffU) > 0x7f800000U) {
+        return m3_bits_f32(bits | 0x00400000U);
+    }
+    if (x > 0x1.62e42ep6F) {
+        return m3_bits_f32(0x7f800000U);
+    }
+    return m3_expf(x);
+}
+
+/* expm1f and tanhf of the libm. GNU libc 2.35 computes both with the
+ * single-precision fdlibm algorithms (Sun Microsystems, 1993; freely
+ * redistributable), in float arithmetic without fused operations:
+ *   expm1f: |x| >= 27 ln2 -> -1 (x < 0) or overflow above 0x1.62e3p6;
+ *           reduction x = k ln2 + r (hi/lo split of ln2) for |x| > ln2/2;
+ *           |x| < 2^-25 -> x; expm1(r) from a rational form in
+ *           r/2 * r with a degree-5 polynomial in (r/2 * r); the result
+ *           rebuilt with k folded into the exponent.
+ *   tanhf:  |x| >= 22 -> +-1; |x| < 2^-55 -> x (1 + x);
+ *           |x| >= 1 -> 1 - 2 / (expm1f(2|x|) + 2);
+ *           else -> -t / (t + 2) with t = expm1f(-2|x|).
+ * The statements below follow that published algorithm operation by
+ * operation; checked bit for bit against the library on all 2^32 inputs. */
+M3_HD float m3_expm1f(float x)
+{
+    const float huge = 1.0e+30F;
+    const float tiny = 1.0e-30F;
+    const float ln2_hi = 6.9313812256e-01F; /* 0x3f317180 */
+    const float ln2_lo = 9.0580006145e-06F; /* 0x3717f7d1 */
+    const float invln2 = 1.4426950216e+00F; /* 0x3fb8aa3b */
+    const float q1 = -3.3333335072e-02F;    /* 0xbd088889 */
+    const float q2 = 1.5873016091e-03F;     /* 0x3ad00d01 */
+    const float q3 = -7.9365076090e-05F;    /* 0xb8a670cd */
+    const float q4 = 4.0082177293e-06F;     /* 0x36867e54 */
+    const float q5 = -2.0109921195e-07F;    /* 0xb457edbb */
+    uint32_t hx = m3_f32_bits(x);
+    const uint32_t xsb = hx & 0x80000000U;
+    float hi;
+    float lo;
+    float c = 0.0F;
+    float t;
+    float e;
+    float hxs;
+    float hfx;
+    float r1;
+    float y;
+    int32_t k;
+
+    hx &= 0x7fffffffU;
+    if (hx >= 0x4195b844U) { /* |x| >= 27 ln2 */
+        if (hx >= 0x42b17218U) { /* |x| >= 88.721... */
+            if (hx > 0x7f800000U) {
+                return x + x; /* NaN */
+            }
+            if (hx == 0x7f800000U) {
+                return xsb == 0U ? x : -1.0F;
+            }
+            if (x > 8.8721679688e+01F) { /* 0x42b17180 */
+                return huge * huge; /* overflow */
+            }
+        }
+        if (xsb != 0U) {
+            return tiny - 1.0F;
+        }
+    }
+    if (hx > 0x3eb17218U) { /* |x| > ln2 / 2 */
+        if (hx < 0x3f851592U) { /* and |x| < 1.5 ln2 */
+            if (xsb == 0U) {
+                hi = x - ln2_hi;
+                lo = ln2_lo;
+                k = 1;
+            } else {
+                hi = x + ln2_hi;
+                lo = -ln2_lo;
+                k = -1;
+            }
+        } else {
+            k = (int32_t)(invln2 * x + (xsb == 0U ? 0.5F : -0.5F));
+            t = (float)k;
+            hi = x - t * ln2_hi; /* exact */
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000U) { /* |x| < 2^-25 */
+        t = huge + x;
+        return x - (t - (huge + x));
+    } else {
+        k = 0;
+    }
+    hfx = 0.5F * x;
+    hxs = x * hfx;
+    r1 = 1.0F + hxs * (q1 + hxs * (q2 + hxs * (q3 + hxs * (q4 + hxs * q5))));
+    t = 3.0F - r1 * hfx;
+    e = hxs * ((r1 - t) / (6.0F - x * t));
+    if (k == 0) {
+        return x - (x * e - hxs);
+    }
+    e = (x * (e - c) - c);
+    e -= hxs;
+    if (k == -1) {
+        return 0.5F * (x - e) - 0.5F;
+    }
+    if (k == 1) {
+        if (x < -0.25F) {
+            return -2.0F * (e - (x + 0.5F));
+        }
+        return 1.0F + 2.0F * (x - e);
+    }
+    if (k <= -2 || k > 56) { /* exp(x) - 1 */
+        y = 1.0F - (e - x);
+        y = m3_bits_f32(m3_f32_bits(y) + ((uint32_t)k << 23U));
+        return y - 1.0F;
+    }
+    if (k < 23) {
+        t = m3_bits_f32(0x3f800000U - (0x1000000U >> k)); /* 1 - 2^-k */
+        y = t - (e - x);
+    } else {
+        t = m3_bits_f32((uint32_t)(0x7f - k) << 23U); /* 2^-k */
+        y = x - (e + t);
+        y += 1.0F;
+    }
+    return m3_bits_f32(m3_f32_bits(y) + ((uint32_t)k << 23U));
+}
+
+M3_HD float m3_tanhf(float x)
+{
+    const uint32_t jx = m3_f32_bits(x);
+    const uint32_t ix = jx & 0x7fffffffU;
+    float t;
+    float z;
+
+    if (ix >= 0x7f800000U) { /* infinity or NaN */
+        if ((jx & 0x80000000U) == 0U) {
+            return 1.0F / x + 1.0F;
+        }
+        return 1.0F / x - 1.0F;
+    }
+    if (ix < 0x41b00000U) { /* |x| < 22 */
+        if (ix == 0U) {
+            return x;
+        }
+        if (ix < 0x24000000U) { /* |x| < 2^-55 */
+            return x * (1.0F + x);
+        }
+        if (ix >= 0x3f800000U) { /* |x| >= 1 */
+            t = m3_expm1f(2.0F * fabsf(x));
+            z = 1.0F - 2.0F / (t + 2.0F);
+        } else {
+            t = m3_expm1f(-2.0F * fabsf(x));
+            z = -t / (t + 2.0F);
+        }
+    } else {
+        z = 1.0F - 1.0e-30F;
+    }
+    return (jx & 0x80000000U) == 0U ? z : -z;
+}
+
+
 #endif

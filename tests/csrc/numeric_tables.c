@@ -22,9 +22,10 @@
  *   numeric_tables libm <stride>
  *       Compares m3_expf and m3_sinf with the C library's expf and sinf
  *       on every stride-th float (expf on floats <= 0.5, the softmax
- *       domain; sinf on all floats), and the magnitude of
+ *       domain; sinf on all floats), the magnitude of
  *       m3_sinf_medium_magnitude with that of sinf where |x| < 120, and
- *       prints the mismatch counts.
+ *       m3_expf_any, m3_expm1f and m3_tanhf with expf, expm1f and tanhf on
+ *       all floats, and prints the mismatch counts.
  *
  * Table hash: the inputs are split into blocks of 2^16 consecutive bit
  * patterns; each block's outputs (little-endian, 2 or 4 bytes each) are
@@ -292,10 +293,16 @@ static int libm(uint64_t stride)
     unsigned long long sin_bad = 0ULL;
     unsigned long long magnitude_checked = 0ULL;
     unsigned long long magnitude_bad = 0ULL;
+    unsigned long long other_checked = 0ULL;
+    unsigned long long expf_any_bad = 0ULL;
+    unsigned long long expm1f_bad = 0ULL;
+    unsigned long long tanhf_bad = 0ULL;
 
 #pragma omp parallel for reduction(+ : exp_checked, exp_bad, sin_checked, \
                                        sin_bad, magnitude_checked,         \
-                                       magnitude_bad) schedule(static)
+                                       magnitude_bad, other_checked,       \
+                                       expf_any_bad, expm1f_bad,           \
+                                       tanhf_bad) schedule(static)
     for (int64_t u = 0; u <= (int64_t)0xffffffffLL; u += (int64_t)stride) {
         uint32_t b = (uint32_t)u;
         float x;
@@ -323,15 +330,33 @@ static int libm(uint64_t stride)
                     memcmp(&magnitude, &want, sizeof(magnitude)) != 0;
             }
         }
+        {
+            float got = m3_expf_any(x);
+            float want = expf(x);
+
+            other_checked += 1U;
+            expf_any_bad += memcmp(&got, &want, sizeof(got)) != 0;
+            got = m3_expm1f(x);
+            want = expm1f(x);
+            expm1f_bad += memcmp(&got, &want, sizeof(got)) != 0;
+            got = m3_tanhf(x);
+            want = tanhf(x);
+            tanhf_bad += memcmp(&got, &want, sizeof(got)) != 0;
+        }
     }
     printf("{\"expf_checked\": %llu, \"expf_mismatches\": %llu, "
            "\"sinf_checked\": %llu, \"sinf_mismatches\": %llu, "
            "\"sinf_magnitude_checked\": %llu, "
-           "\"sinf_magnitude_mismatches\": %llu}\n",
+           "\"sinf_magnitude_mismatches\": %llu, \"all_checked\": %llu, "
+           "\"expf_any_mismatches\": %llu, \"expm1f_mismatches\": %llu, "
+           "\"tanhf_mismatches\": %llu}\n",
            exp_checked, exp_bad, sin_checked, sin_bad, magnitude_checked,
-           magnitude_bad);
-    return exp_bad == 0ULL && sin_bad == 0ULL && magnitude_bad == 0ULL ? 0
-                                                                        : 1;
+           magnitude_bad, other_checked, expf_any_bad, expm1f_bad, tanhf_bad);
+    return exp_bad == 0ULL && sin_bad == 0ULL && magnitude_bad == 0ULL &&
+                   expf_any_bad == 0ULL && expm1f_bad == 0ULL &&
+                   tanhf_bad == 0ULL
+               ? 0
+               : 1;
 }
 
 int main(int argc, char **argv)

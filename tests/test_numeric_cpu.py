@@ -7,9 +7,10 @@ m3_libm.h), using tests/csrc/numeric_tables.c built for the host.
   (tests/golden/conversion_tables.json, written by
   tests/golden/make_conversion_tables.py from the compiled reference).
 * The kernels' header and the oracle agree value by value on all inputs.
-* m3_expf and m3_sinf equal the C library's expf and sinf (the functions
-  the reference calls at src/m3_op_execute_basic.c:156,172,188) on every
-  7th float.
+* m3_expf, m3_sinf, m3_expf_any, m3_expm1f and m3_tanhf equal the C
+  library's expf, sinf, expm1f and tanhf (the functions the reference calls
+  at src/m3_op_execute_basic.c:113,156,172,188,227, tanhf through expm1f)
+  on every 7th float.
 """
 import json
 import os
@@ -78,6 +79,10 @@ def test_libm_restatements_match_c_library():
     assert result["sinf_mismatches"] == 0
     assert result["sinf_magnitude_checked"] > 300_000_000
     assert result["sinf_magnitude_mismatches"] == 0
+    assert result["all_checked"] > 600_000_000
+    assert result["expf_any_mismatches"] == 0
+    assert result["expm1f_mismatches"] == 0
+    assert result["tanhf_mismatches"] == 0
 
 
 def test_hash_discriminates_a_planted_rounding_error(reference_hashes):
