@@ -29,6 +29,16 @@
  *                                   kernel m3_softmax (:105-147)
  *   m3_hip_launch_snake1d        <- m3_metal_encode_snake1d, kernel
  *                                   m3_snake1d (:150-177)
+ *   m3_hip_launch_tanh           <- m3_metal_encode_tanh (:478-511),
+ *                                   kernel m3_tanh (:178-...); host
+ *                                   semantics src/m3_op_execute_basic.c:
+ *                                   217-229
+ *   m3_hip_launch_gated_silu     <- m3_metal_encode_gated_silu
+ *                                   (src/m3_backend_metal_dense.m:478-533),
+ *                                   kernel m3_gated_silu
+ *                                   (src/m3_backend_metal_dense_kernels.m:
+ *                                   416-...); host semantics
+ *                                   src/m3_op_execute_basic.c:104-122
  *   m3_hip_scan_views            <- the host data preflight Metal runs on
  *                                   shared memory before commit
  *                                   (src/m3_backend_metal_basic.m:274-302,
@@ -162,6 +172,20 @@ int m3_hip_launch_snake1d(m3_hip_device *device, const m3_hip_view *input,
                           const m3_hip_view *alpha,
                           const m3_hip_view *output, char *message,
                           size_t capacity);
+
+/* out = tanhf(input) on F32 of rank 1 to 8; any input strides, output
+ * contiguous, exact in-place allowed. */
+int m3_hip_launch_tanh(m3_hip_device *device, const m3_hip_view *input,
+                       const m3_hip_view *output, char *message,
+                       size_t capacity);
+/* out = round_gate(gate / (1 + expf(-gate))) * up, where round_gate rounds
+ * through the gate's dtype; gate, up and output of one shape (no
+ * broadcast), each F32/F16/BF16; any input strides, output contiguous,
+ * exact aliases allowed. */
+int m3_hip_launch_gated_silu(m3_hip_device *device, const m3_hip_view *gate,
+                             const m3_hip_view *up,
+                             const m3_hip_view *output, char *message,
+                             size_t capacity);
 
 /* Elementwise program: a run of F32 ADD/SUB/MUL/DIV operations over one
  * element space of `count` elements, executed per element with the

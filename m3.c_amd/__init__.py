@@ -191,7 +191,7 @@ EXPORTS_HIP = [
     "m3_hip_launch_copy", "m3_hip_launch_softmax", "m3_hip_launch_snake1d",
     "m3_hip_scan_views", "m3_hip_synchronize", "m3_hip_timing_enable",
     "m3_hip_timing_reset", "m3_hip_timing_read", "m3_hip_stream",
-    "m3_hip_launch_program",
+    "m3_hip_launch_program", "m3_hip_launch_tanh", "m3_hip_launch_gated_silu",
 ]
 
 _LIB = None
@@ -369,6 +369,22 @@ class Graph:
         error = Error()
         check(self.lib.m3_graph_add_node(self.handle, ctypes.byref(node),
                                          ctypes.byref(error)), error)
+
+    def add_inferred(self, kind, inputs, role, dtype, output_index=0):
+        """m3_graph_add_inferred_value: a new value whose shape (and, for
+        some kinds, dtype) is inferred from a node of `kind` over
+        `inputs`; returns its id."""
+        node = NodeDesc()
+        self.lib.m3_graph_node_desc_init(ctypes.byref(node), kind)
+        for i, value in enumerate(inputs):
+            node.inputs[i] = value
+        value = ctypes.c_uint32()
+        error = Error()
+        check(self.lib.m3_graph_add_inferred_value(
+            self.handle, ctypes.byref(node), output_index, role, dtype,
+            ctypes.byref(value), ctypes.byref(error)), error)
+        self.values[value.value] = (dtype, None, role)
+        return value.value
 
     def free(self):
         if self.handle:

@@ -1,0 +1,56 @@
+/*
+ * m3_activation.h - the GATED_SILU element function, shared by the gfx950
+ * kernels (m3_hip_activation.hip) and the host checks that compare it
+ * with the C library's arithmetic on every gate value. TANH elements are
+ * m3_tanhf_uniform (m3_libm.h).
+ *
+ * Reference semantics (src/m3_op_execute_basic.c:104-122): gate and up
+ * load as F32; activation = gate / (1 + expf(-gate)), each operation one
+ * rounded F32 operation, then rounded through the gate's dtype
+ * (src/m3_op_numeric.c:210-222); result = activation * up, stored in the
+ * output's dtype.
+ */
+#ifndef M3_ACTIVATION_H
+#define M3_ACTIVATION_H
+
+#include "m3_libm.h"
+#include "m3_numeric.h"
+
+/* F32 bits rounded through a 16-bit float dtype and back (identity for
+ * F32), with the converters of CAST. */
+M3_HD uint32_t m3_round_through_bits(uint32_t bits, uint32_t dtype)
+{
+    return dtype == M3N_F16
+               ? m3_f16_to_f32_bits(m3_f32_to_f16_bits(bits))
+           : dtype == M3N_BF16
+               ? m3_bf16_to_f32_bits(m3_f32_to_bf16_bits(bits))
+               : bits;
+}
+
+/* The unrounded activation gate / (1 + expf(-gate)). Its bits equal the
+ * host's whenever they are not NaN. */
+M3_HD float m3_silu_quotient(float gate)
+{
+    return gate / (1.0F + m3_expf_any(-gate));
+}
+
+/* One GATED_SILU element as F32 bits, NaN bits included. On the host a NaN
+ * gate passes through the division quieted (the dividend's NaN is taken),
+ * the only invalid division, -inf / inf, gives 0xffc00000, and the product
+ * activation * up takes the activation's NaN when both operands are NaN
+ * (gcc evaluates it with the activation as the first operand): the rule of
+ * m3_binary_nan_fix for a non-commutative operation, in both steps. */
+M3_HD uint32_t m3_gated_silu_bits(float gate, float up, uint32_t gate_dtype)
+{
+    const float one_plus = 1.0F + m3_expf_any(-gate);
+    const uint32_t quotient = m3_binary_nan_fix(
+        m3_f32_bits(gate / one_plus), m3_f32_bits(gate),
+        m3_f32_bits(one_plus), 0);
+    const uint32_t activation = m3_round_through_bits(quotient, gate_dtype);
+    const float product = m3_bits_f32(activation) * up;
+
+    return m3_binary_nan_fix(m3_f32_bits(product), activation,
+                             m3_f32_bits(up), 0);
+}
+
+#endif

@@ -472,5 +472,33 @@ M3_HD float m3_tanhf(float x)
     return (jx & 0x80000000U) == 0U ? z : -z;
 }
 
+/* m3_tanhf with one expm1f evaluation and one division per input: its
+ * |x| >= 1 and |x| < 1 cases differ only in the sign of the expm1f
+ * argument (2|x| or -2|x|) and in the numerator (2 or -t) of the quotient
+ * by t + 2, so both are formed with selects and a wave whose lanes fall on
+ * both sides of 1 runs expm1f once. A NaN input returns that NaN quieted,
+ * the bits 1/x + 1 gives on the host, without relying on how the device
+ * propagates NaN operands. Same bits as m3_tanhf for every input. */
+M3_HD float m3_tanhf_uniform(float x)
+{
+    const uint32_t jx = m3_f32_bits(x);
+    const uint32_t ix = jx & 0x7fffffffU;
+    const int big = ix >= 0x3f800000U;
+    const float t = m3_expm1f((big ? 2.0F : -2.0F) * m3_bits_f32(ix));
+    const float q = (big ? 2.0F : -t) / (t + 2.0F);
+    float z = big ? 1.0F - q : q;
+
+    if (ix >= 0x41b00000U) { /* |x| >= 22 and infinities */
+        z = 1.0F - 1.0e-30F;
+    }
+    z = (jx & 0x80000000U) == 0U ? z : -z;
+    if (ix < 0x24000000U) { /* |x| < 2^-55, zeros included */
+        z = ix == 0U ? x : x * (1.0F + x);
+    }
+    if (ix > 0x7f800000U) {
+        z = m3_bits_f32(jx | 0x00400000U);
+    }
+    return z;
+}
 
 #endif

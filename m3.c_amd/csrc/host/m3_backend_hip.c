@@ -528,6 +528,17 @@ static int m3_hip_enqueue(m3_hip_backend_context *context,
         m3_hip_view_of(command->descriptor.snake1d.output, &c);
         return m3_hip_launch_snake1d(context->device, &a, &b, &c, message,
                                      capacity);
+    case M3_OP_TANH:
+        m3_hip_view_of(command->descriptor.tanh.input, &a);
+        m3_hip_view_of(command->descriptor.tanh.output, &c);
+        return m3_hip_launch_tanh(context->device, &a, &c, message,
+                                  capacity);
+    case M3_OP_GATED_SILU:
+        m3_hip_view_of(command->descriptor.gated_silu.left, &a);
+        m3_hip_view_of(command->descriptor.gated_silu.right, &b);
+        m3_hip_view_of(command->descriptor.gated_silu.output, &c);
+        return m3_hip_launch_gated_silu(context->device, &a, &b, &c, message,
+                                        capacity);
 
     default:
         (void)snprintf(message, capacity,

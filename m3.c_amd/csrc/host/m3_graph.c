@@ -260,13 +260,20 @@ static m3_status m3_graph_infer_shape(const m3_graph *graph,
     case M3_OP_CAST:
     case M3_OP_SOFTMAX:
     case M3_OP_SNAKE1D:
+    case M3_OP_TANH:
         output->rank = first->rank;
         (void)memcpy(output->shape, first->shape, sizeof(output->shape));
         if (node->kind == M3_OP_COPY) {
             output->dtype = first->dtype;
-        } else if (node->kind == M3_OP_SNAKE1D) {
+        } else if (node->kind == M3_OP_SNAKE1D ||
+                   node->kind == M3_OP_TANH) {
             output->dtype = M3_DTYPE_F32;
         }
+        return M3_STATUS_OK;
+    case M3_OP_GATED_SILU:
+        /* the gate's shape; the dtype stays the requested one */
+        output->rank = first->rank;
+        (void)memcpy(output->shape, first->shape, sizeof(output->shape));
         return M3_STATUS_OK;
     case M3_OP_ADD:
     case M3_OP_MUL:

@@ -43,6 +43,7 @@ static m3_status m3_node_arity_of(m3_op_kind kind, m3_node_arity *arity,
     case M3_OP_COPY:
     case M3_OP_CAST:
     case M3_OP_SOFTMAX:
+    case M3_OP_TANH:
         arity->inputs = 1U;
         return M3_STATUS_OK;
     case M3_OP_ADD:
@@ -50,6 +51,7 @@ static m3_status m3_node_arity_of(m3_op_kind kind, m3_node_arity *arity,
     case M3_OP_SUB:
     case M3_OP_DIV:
     case M3_OP_SNAKE1D:
+    case M3_OP_GATED_SILU:
         arity->inputs = 2U;
         return M3_STATUS_OK;
     default:

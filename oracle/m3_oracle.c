@@ -385,6 +385,53 @@ int oracle_snake1d(const oracle_view *input, const oracle_view *alpha,
     return 0;
 }
 
+/* src/m3_op_numeric.c:210-222: F32 rounded through a 16-bit dtype and
+ * back (identity for F32). */
+static float round_to_dtype(uint32_t dtype, float value)
+{
+    if (dtype == ORACLE_F16) {
+        return float_of(oracle_f16_to_f32(oracle_f32_to_f16(bits_of(value))));
+    }
+    if (dtype == ORACLE_BF16) {
+        return float_of(
+            oracle_bf16_to_f32(oracle_f32_to_bf16(bits_of(value))));
+    }
+    return dtype == ORACLE_F32 ? value : NAN;
+}
+
+/* src/m3_op_execute_basic.c:104-122: activation = gate / (1 + expf(-gate))
+ * rounded to the gate's dtype, times up, stored in the output's dtype. */
+int oracle_gated_silu(const oracle_view *gate, const oracle_view *up,
+                      const oracle_view *output)
+{
+    uint64_t count = element_count(output);
+    uint64_t i;
+
+    for (i = 0U; i < count; ++i) {
+        float g = load_float(gate, element_offset(gate, i));
+        float u = load_float(up, element_offset(up, i));
+        float activation = round_to_dtype(gate->dtype,
+                                          g / (1.0F + expf(-g)));
+        float result = activation * u;
+
+        store_float(output, element_offset(output, i), result);
+    }
+    return 0;
+}
+
+/* src/m3_op_execute_basic.c:217-229: tanhf of every element. */
+int oracle_tanh(const oracle_view *input, const oracle_view *output)
+{
+    uint64_t count = element_count(input);
+    uint64_t i;
+
+    for (i = 0U; i < count; ++i) {
+        store_float(output, element_offset(output, i),
+                    tanhf(load_float(input, element_offset(input, i))));
+    }
+    return 0;
+}
+
 /* src/m3_op_data_preflight.c:48-64. */
 int oracle_preflight_nan(const oracle_view *view)
 {

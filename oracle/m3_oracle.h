@@ -24,6 +24,12 @@
  *                    vs the compiled reference (bit-exact: same libm)
  *   snake1d          reference KATs (0x3e20def4, +inf); vs the compiled
  *                    reference (bit-exact: same libm)
+ *   gated_silu       closed forms (silu(0) = 0, silu(+inf) = +inf,
+ *                    silu(-inf) = NaN, gate rounding = the converters);
+ *                    vs the compiled reference on random, special and
+ *                    NaN-payload inputs of every dtype (bit-exact: same libm)
+ *   tanh             closed forms (odd, +-1 beyond 22, x for tiny x);
+ *                    vs the compiled reference on all special classes
  *   preflight        reference KATs (NaN / non-finite / out of range)
  */
 #ifndef M3_ORACLE_H
@@ -60,6 +66,9 @@ int oracle_copy(const oracle_view *input, const oracle_view *output);
 int oracle_softmax(const oracle_view *input, const oracle_view *output);
 int oracle_snake1d(const oracle_view *input, const oracle_view *alpha,
                    const oracle_view *output);
+int oracle_gated_silu(const oracle_view *gate, const oracle_view *up,
+                      const oracle_view *output);
+int oracle_tanh(const oracle_view *input, const oracle_view *output);
 
 /* Data preflight (src/m3_op_data_preflight.c:8-64): 2 when the view holds
  * a NaN / a value that is non-finite or outside [-2^31, 2^31). */

@@ -90,6 +90,15 @@ int ref_execute(int kind, const ref_view *views, size_t count, char *message,
             command.descriptor.add.right = &tensors[1];
             command.descriptor.add.output = &tensors[2];
             break;
+        case M3_OP_GATED_SILU:
+            command.descriptor.gated_silu.left = &tensors[0];
+            command.descriptor.gated_silu.right = &tensors[1];
+            command.descriptor.gated_silu.output = &tensors[2];
+            break;
+        case M3_OP_TANH:
+            command.descriptor.tanh.input = &tensors[0];
+            command.descriptor.tanh.output = &tensors[1];
+            break;
         case M3_OP_SNAKE1D:
             command.descriptor.snake1d.input = &tensors[0];
             command.descriptor.snake1d.alpha = &tensors[1];

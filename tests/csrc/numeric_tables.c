@@ -24,14 +24,23 @@
  *       on every stride-th float (expf on floats <= 0.5, the softmax
  *       domain; sinf on all floats), the magnitude of
  *       m3_sinf_medium_magnitude with that of sinf where |x| < 120, and
- *       m3_expf_any, m3_expm1f and m3_tanhf with expf, expm1f and tanhf on
- *       all floats, and prints the mismatch counts.
+ *       m3_expf_any, m3_expm1f, m3_tanhf and m3_tanhf_uniform with expf,
+ *       expm1f and tanhf on all floats, and m3_gated_silu_bits (F32 gate)
+ *       with the same statements in C on every stride-th gate, each with
+ *       one of eight non-NaN up values (the product then has at most one
+ *       NaN operand, so its NaN bits are fixed by IEEE 754 and x86-64),
+ *       and prints the mismatch counts.
+ *   numeric_tables silu16
+ *       m3_gated_silu_bits for F16 and BF16 gates: every 16-bit gate with
+ *       each of the eight up values, against the C statements with the
+ *       activation rounded through the gate's dtype by the converters.
  *
  * Table hash: the inputs are split into blocks of 2^16 consecutive bit
  * patterns; each block's outputs (little-endian, 2 or 4 bytes each) are
  * hashed with 64-bit FNV-1a, and the block hashes (8 bytes each, in block
  * order) are hashed again with FNV-1a.
  */
+#include "m3_activation.h"
 #include "m3_libm.h"
 #include "m3_numeric.h"
 
@@ -285,6 +294,44 @@ static int compare(const char *library)
     return bad == 0ULL ? 0 : 1;
 }
 
+/* Up values of the GATED_SILU checks: signs, zero, infinities, overflow,
+ * a subnormal. */
+static const float silu_ups[8] = {1.0F, -0.75F, 0.0F, INFINITY, -INFINITY,
+                                  3.0e38F, 1.0e-40F, 2.5F};
+
+/* F16 and BF16 gates: all 2^16 gate patterns with each up value. */
+static int silu16(void)
+{
+    unsigned long long checked = 0ULL;
+    unsigned long long bad = 0ULL;
+    uint32_t dtype;
+
+    for (dtype = M3N_F16; dtype <= M3N_BF16; ++dtype) {
+        uint32_t raw;
+
+        for (raw = 0U; raw < 65536U; ++raw) {
+            float gate = m3_bits_f32(m3_load_as_f32_bits(raw, dtype));
+            int k;
+
+            for (k = 0; k < 8; ++k) {
+                volatile float denominator = 1.0F + expf(-gate);
+                volatile float quotient = gate / denominator;
+                float activation = m3_bits_f32(m3_round_through_bits(
+                    m3_f32_bits(quotient), dtype));
+                volatile float product = activation * silu_ups[k];
+                float want = product;
+                uint32_t got = m3_gated_silu_bits(gate, silu_ups[k], dtype);
+
+                checked += 1U;
+                bad += memcmp(&got, &want, sizeof(got)) != 0;
+            }
+        }
+    }
+    printf("{\"silu16_checked\": %llu, \"silu16_mismatches\": %llu}\n",
+           checked, bad);
+    return bad == 0ULL ? 0 : 1;
+}
+
 static int libm(uint64_t stride)
 {
     unsigned long long exp_checked = 0ULL;
@@ -297,12 +344,15 @@ static int libm(uint64_t stride)
     unsigned long long expf_any_bad = 0ULL;
     unsigned long long expm1f_bad = 0ULL;
     unsigned long long tanhf_bad = 0ULL;
+    unsigned long long tanhf_uniform_bad = 0ULL;
+    unsigned long long silu_bad = 0ULL;
 
 #pragma omp parallel for reduction(+ : exp_checked, exp_bad, sin_checked, \
                                        sin_bad, magnitude_checked,         \
                                        magnitude_bad, other_checked,       \
                                        expf_any_bad, expm1f_bad,           \
-                                       tanhf_bad) schedule(static)
+                                       tanhf_bad, tanhf_uniform_bad,       \
+                                       silu_bad) schedule(static)
     for (int64_t u = 0; u <= (int64_t)0xffffffffLL; u += (int64_t)stride) {
         uint32_t b = (uint32_t)u;
         float x;
@@ -342,6 +392,18 @@ static int libm(uint64_t stride)
             got = m3_tanhf(x);
             want = tanhf(x);
             tanhf_bad += memcmp(&got, &want, sizeof(got)) != 0;
+            got = m3_tanhf_uniform(x);
+            tanhf_uniform_bad += memcmp(&got, &want, sizeof(got)) != 0;
+        }
+        {
+            float up = silu_ups[(b >> 5) & 7U];
+            volatile float denominator = 1.0F + expf(-x);
+            volatile float activation = x / denominator;
+            volatile float product = activation * up;
+            float want = product;
+            uint32_t got = m3_gated_silu_bits(x, up, M3N_F32);
+
+            silu_bad += memcmp(&got, &want, sizeof(got)) != 0;
         }
     }
     printf("{\"expf_checked\": %llu, \"expf_mismatches\": %llu, "
@@ -349,12 +411,16 @@ static int libm(uint64_t stride)
            "\"sinf_magnitude_checked\": %llu, "
            "\"sinf_magnitude_mismatches\": %llu, \"all_checked\": %llu, "
            "\"expf_any_mismatches\": %llu, \"expm1f_mismatches\": %llu, "
-           "\"tanhf_mismatches\": %llu}\n",
+           "\"tanhf_mismatches\": %llu, "
+           "\"tanhf_uniform_mismatches\": %llu, "
+           "\"gated_silu_mismatches\": %llu}\n",
            exp_checked, exp_bad, sin_checked, sin_bad, magnitude_checked,
-           magnitude_bad, other_checked, expf_any_bad, expm1f_bad, tanhf_bad);
+           magnitude_bad, other_checked, expf_any_bad, expm1f_bad, tanhf_bad,
+           tanhf_uniform_bad, silu_bad);
     return exp_bad == 0ULL && sin_bad == 0ULL && magnitude_bad == 0ULL &&
                    expf_any_bad == 0ULL && expm1f_bad == 0ULL &&
-                   tanhf_bad == 0ULL
+                   tanhf_bad == 0ULL && tanhf_uniform_bad == 0ULL &&
+                   silu_bad == 0ULL
                ? 0
                : 1;
 }
@@ -370,6 +436,9 @@ int main(int argc, char **argv)
     if (argc == 3 && strcmp(argv[1], "libm") == 0) {
         return libm(strtoull(argv[2], NULL, 10));
     }
-    fprintf(stderr, "usage: numeric_tables tables|compare|libm ...\n");
+    if (argc == 2 && strcmp(argv[1], "silu16") == 0) {
+        return silu16();
+    }
+    fprintf(stderr, "usage: numeric_tables tables|compare|libm|silu16 ...\n");
     return 2;
 }

@@ -312,6 +312,17 @@ static m3_status execute(void *context, const m3_command *commands,
             to_oracle(c->descriptor.snake1d.output, &o);
             status = oracle_snake1d(&a, &b, &o);
             break;
+        case M3_OP_GATED_SILU:
+            to_oracle(c->descriptor.gated_silu.left, &a);
+            to_oracle(c->descriptor.gated_silu.right, &b);
+            to_oracle(c->descriptor.gated_silu.output, &o);
+            status = oracle_gated_silu(&a, &b, &o);
+            break;
+        case M3_OP_TANH:
+            to_oracle(c->descriptor.tanh.input, &a);
+            to_oracle(c->descriptor.tanh.output, &o);
+            status = oracle_tanh(&a, &o);
+            break;
         default:
             return m3_error_set(error, M3_STATUS_UNSUPPORTED,
                                 "oracle backend: kind %d", (int)c->kind);

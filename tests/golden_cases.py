@@ -363,4 +363,89 @@ def _(status, s):
     assert list(out_f32(s, 0, 3)) == [1.0, -2.0, 3.0]
 
 
+# ---- TANH -------------------------------------------------------------------
+
+_TANH_IN = bits_f32([0x00000000, 0x80000000, _bits(1.0), _bits(-1.0),
+                     0x7f800000, 0xff800000, 0x7fc12345, _bits(0.5)])
+
+
+@case("tanh_special_bits", "tests/test_vocoder_activations.c:188-236",
+      m3.OP_TANH,
+      [as_bytes(_TANH_IN), as_bytes(np.zeros(8, np.float32))],
+      [ViewSpec(0, m3.F32, (8,)), ViewSpec(1, m3.F32, (8,))])
+def _(status, s):
+    _expect_ok(status)
+    bits = [int(b) for b in out_f32(s, 1, 8).view(np.uint32)]
+    assert bits[:6] == [0x00000000, 0x80000000, 0x3f42f7d6, 0xbf42f7d6,
+                        0x3f800000, 0xbf800000]
+    assert (bits[6] & 0x7f800000) == 0x7f800000 and (bits[6] & 0x7fffff)
+    assert bits[7] == 0x3eec9a9f
+
+
+@case("tanh_exact_in_place", "tests/test_vocoder_activations.c:237-243",
+      m3.OP_TANH, [as_bytes(_TANH_IN)],
+      [ViewSpec(0, m3.F32, (8,)), ViewSpec(0, m3.F32, (8,))])
+def _(status, s):
+    _expect_ok(status)
+    bits = [int(b) for b in out_f32(s, 0, 8).view(np.uint32)]
+    assert bits[1] == 0x80000000 and bits[2] == 0x3f42f7d6
+
+
+@case("tanh_empty_rank8", "tests/test_vocoder_activations.c:313-340",
+      m3.OP_TANH, [np.zeros(0, np.uint8), np.zeros(0, np.uint8)],
+      [ViewSpec(0, m3.F32, (0, 1 << 32, 1, 1, 1, 1, 1, 1)),
+       ViewSpec(1, m3.F32, (0, 1 << 32, 1, 1, 1, 1, 1, 1))])
+def _(status, s):
+    _expect_ok(status)
+
+
+# ---- GATED_SILU -------------------------------------------------------------
+
+@case("gated_silu_strided_f32", "tests/test_metal_dense_norm.c:304-356",
+      m3.OP_GATED_SILU,
+      [as_bytes(f32([0.0, 91.0, 1.0])), as_bytes(f32([2.0, 92.0, 2.0])),
+       as_bytes(np.zeros(2, np.float32))],
+      [ViewSpec(0, m3.F32, (2,), (8,)), ViewSpec(1, m3.F32, (2,), (8,)),
+       ViewSpec(2, m3.F32, (2,))])
+def _(status, s):
+    _expect_ok(status)
+    out = out_f32(s, 2, 2)
+    assert int(out.view(np.uint32)[0]) == 0
+    # 2 / (1 + e^-1), within the reference test's 1e-7 tolerance
+    assert abs(float(out[1]) - 2.0 / (1.0 + math.exp(-1.0))) <= 2.0e-7
+
+
+@case("gated_silu_bf16_rounds_activation",
+      "tests/test_metal_dense_norm.c:357-377", m3.OP_GATED_SILU,
+      [as_bytes(u16([0x3f00])), as_bytes(u16([0x3f40])),
+       as_bytes(u16([0]))],
+      [ViewSpec(0, m3.BF16, (1,)), ViewSpec(1, m3.BF16, (1,)),
+       ViewSpec(2, m3.BF16, (1,))])
+def _(status, s):
+    _expect_ok(status)
+    assert int(out_u16(s, 2, 1)[0]) == 0x3e6e
+
+
+@case("gated_silu_gate_alias", "tests/test_metal_dense_norm.c:400-409",
+      m3.OP_GATED_SILU,
+      [as_bytes(u16([0x3f00])), as_bytes(u16([0x3f40]))],
+      [ViewSpec(0, m3.BF16, (1,)), ViewSpec(1, m3.BF16, (1,)),
+       ViewSpec(0, m3.BF16, (1,))])
+def _(status, s):
+    _expect_ok(status)
+    assert int(out_u16(s, 0, 1)[0]) == 0x3e6e
+
+
+@case("gated_silu_up_alias_f16", "tests/test_metal_dense_norm.c:378-418",
+      m3.OP_GATED_SILU,
+      [as_bytes(u16([0x3800])), as_bytes(u16([0x3a00]))],
+      [ViewSpec(0, m3.F16, (1,)), ViewSpec(1, m3.F16, (1,)),
+       ViewSpec(1, m3.F16, (1,))])
+def _(status, s):
+    _expect_ok(status)
+    # silu(0.5) = 0.31122 rounds to the F16 0x34fb (0.311279296875);
+    # times 0.75 = 0.23345947265625 rounds to 0x3378
+    assert int(out_u16(s, 1, 1)[0]) == 0x3378
+
+
 CASE_IDS = [c.name for c in CASES]

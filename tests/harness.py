@@ -84,6 +84,8 @@ def oracle():
         lib.oracle_copy.argtypes = [P, P]
         lib.oracle_softmax.argtypes = [P, P]
         lib.oracle_snake1d.argtypes = [P, P, P]
+        lib.oracle_gated_silu.argtypes = [P, P, P]
+        lib.oracle_tanh.argtypes = [P, P]
         lib.oracle_preflight_nan.argtypes = [P]
         lib.oracle_preflight_i32.argtypes = [P]
         for name in ("oracle_f32_to_f16_array", "oracle_f32_to_bf16_array",
@@ -152,6 +154,10 @@ def run_oracle(kind, storages, views):
         lib.oracle_softmax(*refs)
     elif kind == m3.OP_SNAKE1D:
         lib.oracle_snake1d(*refs)
+    elif kind == m3.OP_GATED_SILU:
+        lib.oracle_gated_silu(*refs)
+    elif kind == m3.OP_TANH:
+        lib.oracle_tanh(*refs)
     else:
         raise ValueError(kind)
     return m3.OK, out

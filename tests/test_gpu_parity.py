@@ -357,3 +357,145 @@ def test_snake1d_strided_input_and_alias(hip):
     compare(hip, m3.OP_SNAKE1D, [as_bytes(x), as_bytes(alpha[:8])],
             [ViewSpec(0, m3.F32, (2, 8, 64)), ViewSpec(1, m3.F32, (1, 8, 1)),
              ViewSpec(0, m3.F32, (2, 8, 64))], "snake in place")
+
+
+# ---- TANH -------------------------------------------------------------------
+
+TANH_EDGES = np.array([0x41b00000, 0xc1b00000, 0x41afffff, 0x3f800000,
+                       0x3f7fffff, 0xbf800000, 0x24000000, 0x23ffffff,
+                       0xa3ffffff, 0x3eb17218, 0x3f851592, 0x33000000,
+                       0x32ffffff, 0x7fc12345, 0xff812345, 0x7f800000,
+                       0xff800000, 0x00000000, 0x80000000, 0x00000001],
+                      np.uint32)
+
+TANH_SHAPES = [(1,), (3,), (4,), (7,), (1021,), (8, 64, 96), (1000003,),
+               (2, 1, 3, 1, 5, 1, 7, 2)]
+
+
+@pytest.mark.parametrize("shape", TANH_SHAPES)
+def test_tanh_layouts(hip, shape):
+    rng = np.random.default_rng(20000 + int(np.prod(shape)))
+    count = int(np.prod(shape))
+    x = random_f32(rng, count, scale=3.0, specials=0.05)
+    head = min(count, TANH_EDGES.size)
+    x.view(np.uint32)[:head] = TANH_EDGES[:head]
+    views = [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, shape)]
+    storages = [as_bytes(x), np.zeros(x.nbytes, np.uint8)]
+    compare(hip, m3.OP_TANH, storages, views, "tanh %s" % (shape,))
+
+
+def test_tanh_dense_bit_sweep(hip):
+    """2^24 inputs spread over every exponent and sign: bit patterns
+    k * 256 + r with a random low byte r."""
+    rng = np.random.default_rng(21)
+    bits = ((np.arange(1 << 24, dtype=np.uint64) << np.uint64(8)) |
+            rng.integers(0, 256, 1 << 24, dtype=np.uint64)).astype(np.uint32)
+    views = [ViewSpec(0, m3.F32, (1 << 24,)), ViewSpec(1, m3.F32, (1 << 24,))]
+    storages = [as_bytes(bits), np.zeros(bits.nbytes, np.uint8)]
+    compare(hip, m3.OP_TANH, storages, views, "tanh dense sweep")
+
+
+def test_tanh_strided_offset_and_in_place(hip):
+    rng = np.random.default_rng(22)
+    x = random_f32(rng, 1001, scale=2.0)
+    # every other element of a [10, 100] block, 4 bytes in
+    views = [ViewSpec(0, m3.F32, (10, 50), (400, 8), 4),
+             ViewSpec(1, m3.F32, (10, 50))]
+    compare(hip, m3.OP_TANH, [as_bytes(x), np.zeros(2000, np.uint8)], views,
+            "tanh strided")
+    for offset in (0, 4):  # vector path, then the unaligned general path
+        views = [ViewSpec(0, m3.F32, (997,), None, offset),
+                 ViewSpec(0, m3.F32, (997,), None, offset)]
+        compare(hip, m3.OP_TANH, [as_bytes(x)], views,
+                "tanh in place offset %d" % offset)
+
+
+# ---- GATED_SILU -------------------------------------------------------------
+
+FLOAT_DTYPES = [m3.F32, m3.F16, m3.BF16]
+
+
+def nan_heavy_f32(rng, count, fraction=0.45, scale=8.0):
+    values = (rng.standard_normal(count) * scale).astype(np.float32)
+    bits = values.view(np.uint32)
+    pick = rng.random(count) < fraction
+    payload = rng.integers(1, 1 << 23, count, dtype=np.uint32)
+    sign = rng.integers(0, 2, count, dtype=np.uint32) << np.uint32(31)
+    bits[pick] = (sign | np.uint32(0x7f800000) | payload)[pick]
+    return values
+
+
+@pytest.mark.parametrize("dtypes", [(g, u, o) for g in FLOAT_DTYPES
+                                    for u in FLOAT_DTYPES
+                                    for o in FLOAT_DTYPES])
+@pytest.mark.parametrize("count", [5, 4099])
+def test_gated_silu_dtypes(hip, dtypes, count):
+    rng = np.random.default_rng(30000 + 100 * sum(dtypes) + count)
+    views = [ViewSpec(i, d, (count,)) for i, d in enumerate(dtypes)]
+    storages = [storage_for(rng, dtypes[0], count, specials=0.1),
+                storage_for(rng, dtypes[1], count, specials=0.1),
+                np.zeros(count * m3.DTYPE_SIZES[dtypes[2]], np.uint8)]
+    compare(hip, m3.OP_GATED_SILU, storages, views,
+            "gated silu %s count %d" % (dtypes, count))
+
+
+@pytest.mark.parametrize("shape", [(8, 64, 96), (1000003,), (3, 1, 5, 7),
+                                   ()])
+def test_gated_silu_f32_layouts(hip, shape):
+    rng = np.random.default_rng(31000 + int(np.prod(shape)))
+    count = int(np.prod(shape))
+    gate = random_f32(rng, count, scale=12.0, specials=0.05)
+    up = random_f32(rng, count, scale=2.0, specials=0.05)
+    views = [ViewSpec(i, m3.F32, shape) for i in range(3)]
+    storages = [as_bytes(gate), as_bytes(up), np.zeros(4 * count, np.uint8)]
+    compare(hip, m3.OP_GATED_SILU, storages, views,
+            "gated silu %s" % (shape,))
+
+
+@pytest.mark.parametrize("count", [4000, 4003])
+def test_gated_silu_nan_operands(hip, count):
+    """Both operands mostly NaN with random payloads and signs, plus the
+    invalid cases (-inf gate; zero or infinite activation times an
+    infinite or zero up)."""
+    rng = np.random.default_rng(32000 + count)
+    gate = nan_heavy_f32(rng, count)
+    up = nan_heavy_f32(rng, count)
+    gate.view(np.uint32)[:6] = [0xff800000, 0x7f800000, 0x00000000,
+                                0xc2f00000, 0x7f800000, 0xff800000]
+    up.view(np.uint32)[:6] = [0x7fa00005, 0x00000000, 0x7f800000,
+                              0xff800000, 0x80000000, 0x3f800000]
+    views = [ViewSpec(i, m3.F32, (count,)) for i in range(3)]
+    storages = [as_bytes(gate), as_bytes(up), np.zeros(4 * count, np.uint8)]
+    compare(hip, m3.OP_GATED_SILU, storages, views, "gated silu NaN")
+
+
+def test_gated_silu_dense_gate_sweep(hip):
+    rng = np.random.default_rng(33)
+    gate = ((np.arange(1 << 24, dtype=np.uint64) << np.uint64(8)) |
+            rng.integers(0, 256, 1 << 24, dtype=np.uint64)).astype(np.uint32)
+    up = random_f32(rng, 1 << 24, scale=2.0, specials=0.02)
+    views = [ViewSpec(i, m3.F32, (1 << 24,)) for i in range(3)]
+    storages = [as_bytes(gate), as_bytes(up), np.zeros(4 << 24, np.uint8)]
+    compare(hip, m3.OP_GATED_SILU, storages, views, "gated silu sweep")
+
+
+def test_gated_silu_strided_and_aliases(hip):
+    rng = np.random.default_rng(34)
+    gate = random_f32(rng, 2000, scale=6.0)
+    up = random_f32(rng, 2000, scale=2.0)
+    views = [ViewSpec(0, m3.F32, (20, 40), (320, 8), 4),
+             ViewSpec(1, m3.F32, (20, 40), (160, 4), 0),
+             ViewSpec(2, m3.F32, (20, 40))]
+    compare(hip, m3.OP_GATED_SILU,
+            [as_bytes(gate), as_bytes(up), np.zeros(3200, np.uint8)], views,
+            "gated silu strided")
+    exact = [ViewSpec(0, m3.F32, (1999,)), ViewSpec(1, m3.F32, (1999,))]
+    compare(hip, m3.OP_GATED_SILU, [as_bytes(gate), as_bytes(up)],
+            exact + [exact[0]], "gated silu gate alias")
+    compare(hip, m3.OP_GATED_SILU, [as_bytes(gate), as_bytes(up)],
+            exact + [exact[1]], "gated silu up alias")
+    g16 = storage_for(rng, m3.BF16, 1001)
+    u16 = storage_for(rng, m3.BF16, 1001)
+    exact = [ViewSpec(0, m3.BF16, (1001,)), ViewSpec(1, m3.BF16, (1001,))]
+    compare(hip, m3.OP_GATED_SILU, [g16, u16], exact + [exact[1]],
+            "gated silu bf16 up alias")

@@ -7,6 +7,7 @@ oracle or against numpy where a float32 IEEE operation is the definition.
 Each benchmark configuration runs here at a reduced size.
 """
 import ctypes
+import ctypes.util
 
 import numpy as np
 import pytest
@@ -36,22 +37,33 @@ def run_graph(graph, feeds, outputs, **options):
     return results
 
 
+_LIBM = ctypes.CDLL(ctypes.util.find_library("m"))
+_LIBM.tanhf.restype = ctypes.c_float
+_LIBM.tanhf.argtypes = [ctypes.c_float]
+
+
+def c_tanhf(values):
+    """The C library's tanhf, which the reference calls."""
+    return np.array([_LIBM.tanhf(float(v)) for v in values], np.float32)
+
+
 def test_reference_graph_plan_and_result(gpu):
-    """tests/test_graph_runtime.c:87-160 on the GPU, TANH replaced by COPY
-    (the plan depends only on topology and sizes): 6 values, 4 nodes,
-    5 slots, 80 bytes; every node on the HIP provider."""
+    """tests/test_graph_runtime.c:87-160 on the GPU: x + c -> tanh -> * c
+    -> + x with inferred values; 6 values, 4 nodes, 5 slots, 80 bytes;
+    every node on the HIP provider; the C library's tanhf, tolerance
+    zero."""
     g = m3.Graph()
     x = g.add_value(m3.INPUT, m3.F32, (4,))
     c = g.add_value(m3.CONSTANT, m3.F32, (4,))
-    t0 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
-    t1 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
-    t2 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
-    y = g.add_value(m3.OUTPUT, m3.F32, (4,))
     constant = np.array([0.5, -1.0, 2.0, 3.0], np.float32)
     g.set_constant(c, constant)
+    t0 = g.add_inferred(m3.OP_ADD, [x, c], m3.TEMPORARY, m3.F32)
     g.add_node(m3.OP_ADD, [x, c], [t0])
-    g.add_node(m3.OP_COPY, [t0], [t1])
+    t1 = g.add_inferred(m3.OP_TANH, [t0], m3.TEMPORARY, m3.F32)
+    g.add_node(m3.OP_TANH, [t0], [t1])
+    t2 = g.add_inferred(m3.OP_MUL, [t1, c], m3.TEMPORARY, m3.F32)
     g.add_node(m3.OP_MUL, [t1, c], [t2])
+    y = g.add_inferred(m3.OP_ADD, [t2, x], m3.OUTPUT, m3.F32)
     g.add_node(m3.OP_ADD, [t2, x], [y])
     session = m3.Session(g)
     g.free()
@@ -63,7 +75,8 @@ def test_reference_graph_plan_and_result(gpu):
     session.write(x, data)
     session.run()
     out = session.read(y, np.zeros(4, np.float32))
-    expected = ((data + constant) * constant + data).astype(np.float32)
+    expected = ((c_tanhf(data + constant) * constant).astype(np.float32)
+                + data).astype(np.float32)
     assert np.array_equal(bits(out), bits(expected))
     # repeated runs on unchanged inputs give the same bits
     session.run()

@@ -7,6 +7,7 @@ Restates the reference's graph tests (tests/test_graph_runtime.c:87-248)
 and adds brute-force checks of the liveness plan on random graphs.
 """
 import ctypes
+import ctypes.util
 import os
 import subprocess
 
@@ -66,22 +67,32 @@ def log_of(fake):
 
 
 def reference_graph():
-    """tests/test_graph_runtime.c:30-85 with TANH replaced by COPY: the
-    liveness plan depends only on the topology and the sizes."""
+    """tests/test_graph_runtime.c:30-85: x + c -> tanh -> * c -> + x, every
+    later value added by shape inference."""
     g = m3.Graph()
     x = g.add_value(m3.INPUT, m3.F32, (4,))
     c = g.add_value(m3.CONSTANT, m3.F32, (4,))
-    t0 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
-    t1 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
-    t2 = g.add_value(m3.TEMPORARY, m3.F32, (4,))
-    y = g.add_value(m3.OUTPUT, m3.F32, (4,))
     constant = np.array([0.5, -1.0, 2.0, 3.0], np.float32)
     g.set_constant(c, constant)
+    t0 = g.add_inferred(m3.OP_ADD, [x, c], m3.TEMPORARY, m3.F32)
     g.add_node(m3.OP_ADD, [x, c], [t0])
-    g.add_node(m3.OP_COPY, [t0], [t1])
+    t1 = g.add_inferred(m3.OP_TANH, [t0], m3.TEMPORARY, m3.F32)
+    g.add_node(m3.OP_TANH, [t0], [t1])
+    t2 = g.add_inferred(m3.OP_MUL, [t1, c], m3.TEMPORARY, m3.F32)
     g.add_node(m3.OP_MUL, [t1, c], [t2])
+    y = g.add_inferred(m3.OP_ADD, [t2, x], m3.OUTPUT, m3.F32)
     g.add_node(m3.OP_ADD, [t2, x], [y])
     return g, x, y, constant
+
+
+_LIBM = ctypes.CDLL(ctypes.util.find_library("m"))
+_LIBM.tanhf.restype = ctypes.c_float
+_LIBM.tanhf.argtypes = [ctypes.c_float]
+
+
+def c_tanhf(values):
+    """The C library's tanhf, which the reference calls."""
+    return np.array([_LIBM.tanhf(float(v)) for v in values], np.float32)
 
 
 def test_liveness_plan_kat_and_execution(fake):
@@ -97,10 +108,12 @@ def test_liveness_plan_kat_and_execution(fake):
     session.write(x, data)
     session.run()
     out = session.read(y, np.zeros(4, np.float32))
-    expected = ((data + constant) * constant + data).astype(np.float32)
+    # tests/test_graph_runtime.c:139-146, tolerance zero
+    expected = ((c_tanhf(data + constant) * constant).astype(np.float32)
+                + data).astype(np.float32)
     assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
     kinds, lists = log_of(fake)
-    assert kinds == [m3.OP_ADD, m3.OP_COPY, m3.OP_MUL, m3.OP_ADD]
+    assert kinds == [m3.OP_ADD, m3.OP_TANH, m3.OP_MUL, m3.OP_ADD]
     assert lists == [0, 0, 0, 0]  # one partition, one list per run
     session.free()
 
@@ -238,7 +251,7 @@ def test_out_of_scope_operation_is_unsupported(fake):
     g = m3.Graph()
     x = g.add_value(m3.INPUT, m3.F32, (3,))
     y = g.add_value(m3.OUTPUT, m3.F32, (3,))
-    g.add_node(m3.OP_TANH, [x], [y])
+    g.add_node(m3.OP_NEAREST_RESIZE1D, [x], [y])
     status, made, _ = _session_status(g)
     assert status == m3.UNSUPPORTED and not made
     g.free()

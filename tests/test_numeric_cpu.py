@@ -22,7 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCE = os.path.join(HERE, "csrc", "numeric_tables.c")
 HEADERS = [os.path.join(ROOT, "m3.c_amd", "csrc", "hip", name)
-           for name in ("m3_numeric.h", "m3_libm.h")]
+           for name in ("m3_numeric.h", "m3_libm.h", "m3_activation.h")]
 TOOL = os.path.join(HERE, "_build", "numeric_tables")
 
 
@@ -83,6 +83,14 @@ def test_libm_restatements_match_c_library():
     assert result["expf_any_mismatches"] == 0
     assert result["expm1f_mismatches"] == 0
     assert result["tanhf_mismatches"] == 0
+    assert result["tanhf_uniform_mismatches"] == 0
+    assert result["gated_silu_mismatches"] == 0
+
+
+def test_gated_silu_16bit_gates_match_c_statements():
+    result = run("silu16")
+    assert result["silu16_checked"] == 2 * 65536 * 8
+    assert result["silu16_mismatches"] == 0
 
 
 def test_hash_discriminates_a_planted_rounding_error(reference_hashes):
