@@ -274,6 +274,27 @@ def build_snake(x, alpha):
     return build
 
 
+def build_tanh(x):
+    def build():
+        graph = m3.Graph()
+        vx = graph.add_value(m3.INPUT, m3.F32, x.shape)
+        vy = graph.add_value(m3.OUTPUT, m3.F32, x.shape)
+        graph.add_node(m3.OP_TANH, [vx], [vy])
+        return graph, [(vx, x)], (vy, x.shape, np.float32)
+    return build
+
+
+def build_gated_silu(gate, up, dtype, out_np):
+    def build():
+        graph = m3.Graph()
+        vg = graph.add_value(m3.INPUT, dtype, gate.shape)
+        vu = graph.add_value(m3.INPUT, dtype, up.shape)
+        vy = graph.add_value(m3.OUTPUT, dtype, gate.shape)
+        graph.add_node(m3.OP_GATED_SILU, [vg, vu], [vy])
+        return graph, [(vg, gate), (vu, up)], (vy, gate.shape, out_np)
+    return build
+
+
 def build_euler(x, vus, vcs, scale=3.0, dt=1.0 / 30.0):
     """30-step CFG + Euler graph in the reference's op order
     (src/m3_flow_solver_math.c:36-135): a = vu*(-1); a = vc + a; a = a*s;
@@ -356,7 +377,9 @@ def main():
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--rotate", type=int, default=4)
-    parser.add_argument("--classes", default="softmax,mul,cast,copy,snake,euler",
+    parser.add_argument("--classes",
+                        default="softmax,mul,cast,copy,snake,tanh,gated_silu,"
+                                "euler",
                         help="comma-separated op classes to run")
     parser.add_argument("--no-cpu", action="store_true",
                         help="skip the CPU baseline and CPU parity check")
@@ -534,6 +557,85 @@ def main():
             cpu_seconds, 2 * x[:, :96, :].nbytes)
         w.free()
         log("snake:", json.dumps(results["snake"]))
+
+    if "tanh" in classes:
+        log("tanh: generating x[2,1536,65536]")
+        rng = m3.rng_new(0, 1)
+        x = m3.rng_fill("normal", 2 * 1536 * 65536, seed=0, a=1.5,
+                        rng=rng).reshape(2, 1536, 65536)
+        nbytes = 2 * x.nbytes
+        w = Workload("tanh", build_tanh(x), [x], nbytes, ["m3_tanh"], 1,
+                     cpu)
+        wall, kus, launches, _, _ = w.measure(max(args.steps // 4, 3),
+                                              args.warmup)
+        parity = None
+        cpu_seconds = None
+        if cpu is not None:
+            out = w.read_output()
+            sample = x[:, :96, :]
+            status, storages, cpu_seconds = cpu.timed(
+                m3.OP_TANH, [as_bytes(sample),
+                             np.zeros(sample.nbytes, np.uint8)],
+                [spec(0, m3.F32, sample.shape),
+                 spec(1, m3.F32, sample.shape)])
+            ref = storages[1].view(np.uint32).reshape(sample.shape)
+            mismatches = int(np.count_nonzero(
+                ref != out[:, :96, :].view(np.uint32)))
+            parity = ("bit-exact on the CPU sample (channels 0-95)"
+                      if mismatches == 0 else
+                      "%d of %d sampled elements differ" %
+                      (mismatches, sample.size))
+        results["tanh"] = result_entry(
+            "tanh", w, wall, kus, launches, nbytes, nbytes, parity,
+            cpu_seconds, 2 * x[:, :96, :].nbytes)
+        w.free()
+        log("tanh:", json.dumps(results["tanh"]))
+
+    if "gated_silu" in classes:
+        shape = (16384, 3072)
+        log("gated_silu: generating gate and up [16384,3072] F32 and BF16")
+        rng = m3.rng_new(0, 2)
+        count = shape[0] * shape[1]
+        gate = m3.rng_fill("normal", count, seed=0, a=3.0,
+                           rng=rng).reshape(shape)
+        up = m3.rng_fill("normal", count, seed=0, a=1.0,
+                         rng=rng).reshape(shape)
+        gate16 = (gate.view(np.uint32) >> 16).astype(np.uint16)
+        up16 = (up.view(np.uint32) >> 16).astype(np.uint16)
+        for name, dtype, g, u, out_np, kernel in (
+                ("gated_silu", m3.F32, gate, up, np.float32,
+                 "m3_gated_silu"),
+                ("gated_silu_bf16", m3.BF16, gate16, up16, np.uint16,
+                 "m3_gated_silu_bf16")):
+            nbytes = 3 * g.nbytes
+            w = Workload(name, build_gated_silu(g, u, dtype, out_np), [g, u],
+                         nbytes, [kernel], 1, cpu)
+            wall, kus, launches, _, _ = w.measure(max(args.steps // 4, 3),
+                                                  args.warmup)
+            parity = None
+            cpu_seconds = None
+            if cpu is not None:
+                out = w.read_output()
+                rows = 1024
+                size = g.itemsize
+                status, storages, cpu_seconds = cpu.timed(
+                    m3.OP_GATED_SILU,
+                    [as_bytes(g[:rows]), as_bytes(u[:rows]),
+                     np.zeros(rows * shape[1] * size, np.uint8)],
+                    [spec(0, dtype, (rows, shape[1])),
+                     spec(1, dtype, (rows, shape[1])),
+                     spec(2, dtype, (rows, shape[1]))])
+                ref = storages[2].view(out_np).reshape(rows, shape[1])
+                mismatches = int(np.count_nonzero(
+                    ref.view(np.uint8) != out[:rows].view(np.uint8)))
+                parity = ("bit-exact on the CPU sample (rows 0-1023)"
+                          if mismatches == 0 else
+                          "%d sampled bytes differ" % mismatches)
+            results[name] = result_entry(
+                name, w, wall, kus, launches, nbytes, nbytes, parity,
+                cpu_seconds, 3 * g[:1024].nbytes)
+            w.free()
+            log(name + ":", json.dumps(results[name]))
 
     if "euler" in classes:
         log("euler: generating x and 30 x (vu, vc) [2,4096,1536]")

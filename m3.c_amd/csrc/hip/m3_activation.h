@@ -34,6 +34,41 @@ M3_HD float m3_silu_quotient(float gate)
     return gate / (1.0F + m3_expf_any(-gate));
 }
 
+/* The unrounded activation as the vector kernels form it: expf with the
+ * table `table` (a copy in LDS on the device) and its overflow as a select
+ * instead of a branch, and the division as m3_div_normal where its
+ * operands allow it. Both operands are scaled by 2^-32 first (exact, and
+ * the quotient is unchanged), so that the reciprocal of a denominator up
+ * to 2^128 (gates down to -88.7) stays normal. Gates below 2^-60 in
+ * magnitude (zeros, subnormals) take gate * 0.5, the exact quotient by
+ * 1 + expf(-gate) = 2, and an infinite denominator takes gate * 0 (-0, or
+ * NaN for gate = -inf). For
+ * every gate whose activation is not NaN on the host the result has the
+ * host's bits, except that on the device an infinite or near-overflow
+ * quotient (gate near +inf, divided by 1) comes out NaN; NaN results carry
+ * no defined payload. Callers recompute every NaN with m3_gated_silu_bits. */
+M3_HD float m3_silu_quotient_fast(float gate, const uint64_t *table)
+{
+    const float threshold = 0x1.62e42ep6F; /* expf overflows above */
+    const float minus = -gate;
+    const float exp_minus = minus > threshold
+                                ? m3_bits_f32(0x7f800000U)
+                                : m3_expf_with_table(
+                                      fminf(minus, threshold), table);
+    const float denominator = 1.0F + exp_minus;
+    float quotient =
+        m3_div_normal(gate * 0x1p-32F, denominator * 0x1p-32F);
+
+    quotient = fabsf(gate) < 0x1p-60F ? gate * 0.5F : quotient;
+    return m3_f32_bits(denominator) == 0x7f800000U ? gate * 0.0F : quotient;
+}
+
+/* F32 bits rounded through BF16 and back, for bits that are not NaN. */
+M3_HD uint32_t m3_round_through_bf16_finite(uint32_t bits)
+{
+    return (bits + 0x7fffU + ((bits >> 16U) & 1U)) & 0xffff0000U;
+}
+
 /* One GATED_SILU element as F32 bits, NaN bits included. On the host a NaN
  * gate passes through the division quieted (the dividend's NaN is taken),
  * the only invalid division, -inf / inf, gives 0xffc00000, and the product

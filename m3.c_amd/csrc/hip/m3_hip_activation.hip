@@ -198,18 +198,22 @@ struct m3_silu_vec_args {
     uint32_t tail;
 };
 
-/* Four GATED_SILU elements with a gate of dtype D, as F32 bits. */
+/* Four GATED_SILU elements with a gate of dtype D, as F32 bits; `table`
+ * is the expf table in LDS. */
 template <uint32_t D>
 __device__ __forceinline__ void m3_silu4(const float g[4], const float u[4],
-                                         uint32_t r[4])
+                                         const uint64_t *table, uint32_t r[4])
 {
     float p[4];
 
 #pragma unroll
     for (uint32_t k = 0U; k < 4U; ++k) {
-        float activation = m3_silu_quotient(g[k]);
+        float activation = m3_silu_quotient_fast(g[k], table);
 
-        if (D != M3N_F32) {
+        if (D == M3N_BF16) {
+            activation = m3_bits_f32(
+                m3_round_through_bf16_finite(m3_f32_bits(activation)));
+        } else if (D == M3N_F16) {
             activation = m3_bits_f32(
                 m3_round_through_bits(m3_f32_bits(activation), D));
         }
@@ -236,7 +240,12 @@ __global__ __launch_bounds__(256) void m3_gated_silu_vec_kernel(
 {
     const uint32_t step = gridDim.x * kThreads * kUnroll;
     constexpr uint32_t size = D == M3N_F32 ? 4U : 2U;
+    __shared__ uint64_t table[32];
 
+    if (threadIdx.x < 32U) {
+        table[threadIdx.x] = m3_expf_table[threadIdx.x];
+    }
+    __syncthreads();
     for (uint32_t first = blockIdx.x * kThreads * kUnroll + threadIdx.x;
          first < a.groups; first += step) {
         float g[kUnroll][4];
@@ -256,7 +265,7 @@ __global__ __launch_bounds__(256) void m3_gated_silu_vec_kernel(
             if (index < a.groups) {
                 uint32_t r[4];
 
-                m3_silu4<D>(g[k], u[k], r);
+                m3_silu4<D>(g[k], u[k], table, r);
                 m3_store4<D>(a.output, index, r);
             }
         }

@@ -472,20 +472,114 @@ M3_HD float m3_tanhf(float x)
     return (jx & 0x80000000U) == 0U ? z : -z;
 }
 
-/* m3_tanhf with one expm1f evaluation and one division per input: its
- * |x| >= 1 and |x| < 1 cases differ only in the sign of the expm1f
- * argument (2|x| or -2|x|) and in the numerator (2 or -t) of the quotient
- * by t + 2, so both are formed with selects and a wave whose lanes fall on
- * both sides of 1 runs expm1f once. A NaN input returns that NaN quieted,
- * the bits 1/x + 1 gives on the host, without relying on how the device
- * propagates NaN operands. Same bits as m3_tanhf for every input. */
+/* a / b rounded to nearest even, for callers that guarantee a, b, 1 / b
+ * and the quotient are normal (|b| < 2^126) and the quotient is far from
+ * overflow. On the device this is the
+ * Newton-Raphson iteration of the compiler's IEEE division (reciprocal
+ * estimate, one refinement, two correction steps) without its operand
+ * scaling and special-value fixup, which leave such operands unchanged;
+ * on the host it is the C division. */
+M3_HD float m3_div_normal(float a, float b)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    float y = __builtin_amdgcn_rcpf(b);
+    const float e = fmaf(-b, y, 1.0F);
+    float q;
+    float r;
+
+    y = fmaf(e, y, y);
+    q = a * y;
+    r = fmaf(-b, q, a);
+    q = fmaf(r, y, q);
+    r = fmaf(-b, q, a);
+    return fmaf(r, y, q);
+#else
+    return a / b;
+#endif
+}
+
+/* m3_expm1f for the arguments tanhf passes, v in (-2, 0) or [2, 44], as
+ * straight-line code: every case of the reduction is the general one with
+ * k = 0 (no reduction, c = 0), k = +-1 below 1.5 ln2, or k = round(v/ln2),
+ * which gives the same hi, lo, x and c bit for bit; the reconstructions
+ * of the cases k = 0, k = -1, k <= -2 or k > 56, 2 <= k < 23 and
+ * 23 <= k <= 56 are all formed and one is selected, as is v itself for
+ * |v| < 2^-25. (k = 1 needs v in (ln2/2, 1.5 ln2), outside that domain.)
+ * The quotient of the polynomial step has operands near -2 and 6, so
+ * m3_div_normal applies. */
+M3_HD float m3_expm1f_tanh(float v)
+{
+    const float ln2_hi = 6.9313812256e-01F;
+    const float ln2_lo = 9.0580006145e-06F;
+    const float invln2 = 1.4426950216e+00F;
+    const float q1 = -3.3333335072e-02F;
+    const float q2 = 1.5873016091e-03F;
+    const float q3 = -7.9365076090e-05F;
+    const float q4 = 4.0082177293e-06F;
+    const float q5 = -2.0109921195e-07F;
+    const uint32_t hv = m3_f32_bits(v);
+    const uint32_t hx = hv & 0x7fffffffU;
+    const int negative = (hv & 0x80000000U) != 0U;
+    int32_t k = (int32_t)(invln2 * v + (negative ? -0.5F : 0.5F));
+
+    if (hx <= 0x3eb17218U) { /* |v| <= ln2 / 2 */
+        k = 0;
+    } else if (hx < 0x3f851592U) { /* |v| < 1.5 ln2 */
+        k = negative ? -1 : 1;
+    }
+    const float kf = (float)k;
+    const float hi = v - kf * ln2_hi;
+    const float lo = kf * ln2_lo;
+    const float x = hi - lo;
+    const float c = (hi - x) - lo;
+    const float hfx = 0.5F * x;
+    const float hxs = x * hfx;
+    const float r1 =
+        1.0F + hxs * (q1 + hxs * (q2 + hxs * (q3 + hxs * (q4 + hxs * q5))));
+    const float t = 3.0F - r1 * hfx;
+    const float e = hxs * m3_div_normal(r1 - t, 6.0F - x * t);
+    const float zero_k = x - (x * e - hxs);
+    float f = x * (e - c) - c;
+    const uint32_t kbits = (uint32_t)k << 23U;
+
+    f -= hxs;
+    const float minus_one_k = 0.5F * (x - f) - 0.5F;
+    const float outer =
+        m3_bits_f32(m3_f32_bits(1.0F - (f - x)) + kbits) - 1.0F;
+    const float low_t =
+        m3_bits_f32(0x3f800000U - (0x1000000U >> ((uint32_t)k & 31U)));
+    const float low = m3_bits_f32(m3_f32_bits(low_t - (f - x)) + kbits);
+    const float high_t = m3_bits_f32((uint32_t)(0x7f - k) << 23U);
+    float high = x - (f + high_t);
+
+    high += 1.0F;
+    high = m3_bits_f32(m3_f32_bits(high) + kbits);
+    float result = (k <= -2 || k > 56) ? outer : k < 23 ? low : high;
+
+    result = k == -1 ? minus_one_k : result;
+    result = k == 0 ? zero_k : result;
+    return hx < 0x33000000U ? v : result; /* |v| < 2^-25 */
+}
+
+/* m3_tanhf as straight-line code with one expm1f evaluation and one
+ * division per input: its |x| >= 1 and |x| < 1 cases differ only in the
+ * sign of the expm1f argument (2|x| or -2|x|) and in the numerator (2 or
+ * -t) of the quotient by t + 2, so both are formed with selects. |x| is
+ * clamped at 22 first (results there are the constant 1 - 1e-30, with the
+ * sign), so expm1f sees only its tanhf domain. A NaN input returns that
+ * NaN quieted, the bits 1/x + 1 gives on the host, without relying on how
+ * the device propagates NaN operands. The quotient's operands are normal
+ * wherever its result is used (numerator 2 or at least 2^-54 in
+ * magnitude, denominator in [1.1, 2^64)). Same bits as m3_tanhf for every
+ * input. */
 M3_HD float m3_tanhf_uniform(float x)
 {
     const uint32_t jx = m3_f32_bits(x);
     const uint32_t ix = jx & 0x7fffffffU;
     const int big = ix >= 0x3f800000U;
-    const float t = m3_expm1f((big ? 2.0F : -2.0F) * m3_bits_f32(ix));
-    const float q = (big ? 2.0F : -t) / (t + 2.0F);
+    const float magnitude = fminf(m3_bits_f32(ix), 22.0F);
+    const float t = m3_expm1f_tanh((big ? 2.0F : -2.0F) * magnitude);
+    const float q = m3_div_normal(big ? 2.0F : -t, t + 2.0F);
     float z = big ? 1.0F - q : q;
 
     if (ix >= 0x41b00000U) { /* |x| >= 22 and infinities */

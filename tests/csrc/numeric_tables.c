@@ -26,6 +26,7 @@
  *       m3_sinf_medium_magnitude with that of sinf where |x| < 120, and
  *       m3_expf_any, m3_expm1f, m3_tanhf and m3_tanhf_uniform with expf,
  *       expm1f and tanhf on all floats, and m3_gated_silu_bits (F32 gate)
+ *       and m3_silu_quotient_fast (its quotient alone, NaN as a class)
  *       with the same statements in C on every stride-th gate, each with
  *       one of eight non-NaN up values (the product then has at most one
  *       NaN operand, so its NaN bits are fixed by IEEE 754 and x86-64),
@@ -346,13 +347,15 @@ static int libm(uint64_t stride)
     unsigned long long tanhf_bad = 0ULL;
     unsigned long long tanhf_uniform_bad = 0ULL;
     unsigned long long silu_bad = 0ULL;
+    unsigned long long silu_fast_bad = 0ULL;
 
 #pragma omp parallel for reduction(+ : exp_checked, exp_bad, sin_checked, \
                                        sin_bad, magnitude_checked,         \
                                        magnitude_bad, other_checked,       \
                                        expf_any_bad, expm1f_bad,           \
                                        tanhf_bad, tanhf_uniform_bad,       \
-                                       silu_bad) schedule(static)
+                                       silu_bad, silu_fast_bad)            \
+    schedule(static)
     for (int64_t u = 0; u <= (int64_t)0xffffffffLL; u += (int64_t)stride) {
         uint32_t b = (uint32_t)u;
         float x;
@@ -404,6 +407,15 @@ static int libm(uint64_t stride)
             uint32_t got = m3_gated_silu_bits(x, up, M3N_F32);
 
             silu_bad += memcmp(&got, &want, sizeof(got)) != 0;
+            {
+                float quotient = activation;
+                float fast = m3_silu_quotient_fast(x, m3_expf_table);
+
+                silu_fast_bad += isnan(quotient)
+                                     ? !isnan(fast)
+                                     : memcmp(&fast, &quotient,
+                                              sizeof(fast)) != 0;
+            }
         }
     }
     printf("{\"expf_checked\": %llu, \"expf_mismatches\": %llu, "
@@ -413,14 +425,15 @@ static int libm(uint64_t stride)
            "\"expf_any_mismatches\": %llu, \"expm1f_mismatches\": %llu, "
            "\"tanhf_mismatches\": %llu, "
            "\"tanhf_uniform_mismatches\": %llu, "
-           "\"gated_silu_mismatches\": %llu}\n",
+           "\"gated_silu_mismatches\": %llu, "
+           "\"silu_fast_mismatches\": %llu}\n",
            exp_checked, exp_bad, sin_checked, sin_bad, magnitude_checked,
            magnitude_bad, other_checked, expf_any_bad, expm1f_bad, tanhf_bad,
-           tanhf_uniform_bad, silu_bad);
+           tanhf_uniform_bad, silu_bad, silu_fast_bad);
     return exp_bad == 0ULL && sin_bad == 0ULL && magnitude_bad == 0ULL &&
                    expf_any_bad == 0ULL && expm1f_bad == 0ULL &&
                    tanhf_bad == 0ULL && tanhf_uniform_bad == 0ULL &&
-                   silu_bad == 0ULL
+                   silu_bad == 0ULL && silu_fast_bad == 0ULL
                ? 0
                : 1;
 }

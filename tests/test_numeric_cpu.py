@@ -85,6 +85,7 @@ def test_libm_restatements_match_c_library():
     assert result["tanhf_mismatches"] == 0
     assert result["tanhf_uniform_mismatches"] == 0
     assert result["gated_silu_mismatches"] == 0
+    assert result["silu_fast_mismatches"] == 0
 
 
 def test_gated_silu_16bit_gates_match_c_statements():
