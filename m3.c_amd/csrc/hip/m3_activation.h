@@ -51,10 +51,10 @@ M3_HD float m3_silu_quotient_fast(float gate, const uint64_t *table)
 {
     const float threshold = 0x1.62e42ep6F; /* expf overflows above */
     const float minus = -gate;
-    const float exp_minus = minus > threshold
-                                ? m3_bits_f32(0x7f800000U)
-                                : m3_expf_with_table(
-                                      fminf(minus, threshold), table);
+    /* formed for every gate and then selected, not branched on */
+    const float clamped = m3_expf_with_table(fminf(minus, threshold), table);
+    const float exp_minus =
+        minus > threshold ? m3_bits_f32(0x7f800000U) : clamped;
     const float denominator = 1.0F + exp_minus;
     float quotient =
         m3_div_normal(gate * 0x1p-32F, denominator * 0x1p-32F);

@@ -113,11 +113,12 @@ __global__ __launch_bounds__(256) void m3_tanh_vec_kernel(m3_tanh_vec_args a)
          first < a.groups; first += step) {
         float x[kUnroll][4];
 
+        /* unconditional loads (groups past the end re-read the last one)
+         * so that all of them are in flight before the first use */
 #pragma unroll
         for (uint32_t u = 0U; u < kUnroll; ++u) {
-            if (first + u * kThreads < a.groups) {
-                m3_load4<M3N_F32>(a.input, first + u * kThreads, x[u]);
-            }
+            m3_load4<M3N_F32>(a.input, min(first + u * kThreads,
+                                            a.groups - 1U), x[u]);
         }
 #pragma unroll
         for (uint32_t u = 0U; u < kUnroll; ++u) {
@@ -251,12 +252,14 @@ __global__ __launch_bounds__(256) void m3_gated_silu_vec_kernel(
         float g[kUnroll][4];
         float u[kUnroll][4];
 
+        /* unconditional loads (groups past the end re-read the last one)
+         * so that all of them are in flight before the first use */
 #pragma unroll
         for (uint32_t k = 0U; k < kUnroll; ++k) {
-            if (first + k * kThreads < a.groups) {
-                m3_load4<D>(a.gate, first + k * kThreads, g[k]);
-                m3_load4<D>(a.up, first + k * kThreads, u[k]);
-            }
+            const uint32_t index = min(first + k * kThreads, a.groups - 1U);
+
+            m3_load4<D>(a.gate, index, g[k]);
+            m3_load4<D>(a.up, index, u[k]);
         }
 #pragma unroll
         for (uint32_t k = 0U; k < kUnroll; ++k) {
