@@ -55,7 +55,6 @@ typedef struct {
     m3_hip_view *scan_views;
     uint32_t *scan_kinds;
     uint32_t *scan_flags;
-    size_t *scan_commands;
     size_t scan_capacity;
     /* views whose last data check passed and whose storage has not been
      * written since (host write, kernel output or free) */
@@ -161,7 +160,6 @@ static void m3_hip_destroy(void *opaque)
     free(context->scan_views);
     free(context->scan_kinds);
     free(context->scan_flags);
-    free(context->scan_commands);
     free(context);
 }
 
@@ -367,7 +365,6 @@ static m3_status m3_hip_grow_scans(m3_hip_backend_context *context,
     m3_hip_view *views;
     uint32_t *kinds;
     uint32_t *flags;
-    size_t *commands;
 
     if (count <= context->scan_capacity) {
         return M3_STATUS_OK;
@@ -384,11 +381,7 @@ static m3_status m3_hip_grow_scans(m3_hip_backend_context *context,
     if (flags != NULL) {
         context->scan_flags = flags;
     }
-    commands = realloc(context->scan_commands, count * sizeof(*commands));
-    if (commands != NULL) {
-        context->scan_commands = commands;
-    }
-    if (views == NULL || kinds == NULL || flags == NULL || commands == NULL) {
+    if (views == NULL || kinds == NULL || flags == NULL) {
         return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY,
                             "cannot grow HIP preflight state");
     }
@@ -396,11 +389,24 @@ static m3_status m3_hip_grow_scans(m3_hip_backend_context *context,
     return M3_STATUS_OK;
 }
 
+static m3_status m3_hip_scan_failure(uint32_t kind, m3_error *error)
+{
+    return m3_error_set(error, M3_STATUS_OUT_OF_RANGE,
+                        kind == M3_HIP_SCAN_NAN
+                            ? "softmax input contains NaN"
+                            : "float-to-I32 cast value is invalid");
+}
+
+/* The list-atomic part of the data preflight: every checked input that no
+ * earlier command of the list writes is scanned before anything runs, and
+ * the first failing one in list order fails the whole list with nothing
+ * executed (the Metal contract, src/m3_backend_metal_basic.m:274-302).
+ * Checked inputs that an earlier command writes are scanned later, when
+ * their producers have run (m3_hip_scan_produced). */
 static m3_status m3_hip_preflight(m3_hip_backend_context *context,
                                   const m3_command *commands, size_t count,
                                   m3_error *error)
 {
-    size_t rejected = SIZE_MAX; /* first producer-dependent check */
     size_t scans = 0U;
     size_t i;
     m3_status status;
@@ -410,14 +416,8 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
         const m3_tensor_view *input = m3_hip_checked_input(&commands[i],
                                                            &kind);
 
-        if (input == NULL) {
-            continue;
-        }
-        if (m3_hip_written_before(commands, i, input->storage)) {
-            rejected = i;
-            break;
-        }
-        if (input->metadata.element_count == 0U) {
+        if (input == NULL || input->metadata.element_count == 0U ||
+            m3_hip_written_before(commands, i, input->storage)) {
             continue;
         }
         status = m3_hip_grow_scans(context, scans + 1U, error);
@@ -429,7 +429,6 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
             continue;
         }
         context->scan_kinds[scans] = kind;
-        context->scan_commands[scans] = i;
         scans += 1U;
     }
     for (i = 0U; i < scans; i += 64U) {
@@ -452,24 +451,45 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
     }
     for (i = 0U; i < scans; ++i) {
         if (context->scan_flags[i] != 0U) {
-            if (context->scan_commands[i] > rejected) {
-                break;
-            }
-            return m3_error_set(
-                error, M3_STATUS_OUT_OF_RANGE,
-                context->scan_kinds[i] == M3_HIP_SCAN_NAN
-                    ? "softmax input contains NaN"
-                    : "float-to-I32 cast value is invalid");
+            return m3_hip_scan_failure(context->scan_kinds[i], error);
         }
     }
-    if (rejected != SIZE_MAX) {
-        return m3_error_set(error, M3_STATUS_UNSUPPORTED,
-                            commands[rejected].kind == M3_OP_CAST
-                                ? "HIP float-to-I32 cast depends on an "
-                                  "earlier output"
-                                : "HIP softmax depends on an earlier "
-                                  "output");
+    return M3_STATUS_OK;
+}
+
+/* Scans the checked input of commands[index] when an earlier command of
+ * the list writes it. The scan runs on the stream after every command
+ * enqueued so far and its flag is read back, so it sees the produced
+ * values. On failure the commands before `index` have run and it and the
+ * rest do not: the reference CPU provider's order, preflight right before
+ * each command (src/m3_op_execute_host.c:5-60), where Metal rejects such a
+ * list outright. */
+static m3_status m3_hip_scan_produced(m3_hip_backend_context *context,
+                                      const m3_command *commands,
+                                      size_t index, m3_error *error)
+{
+    uint32_t kind = 0U;
+    uint32_t flag = 0U;
+    const m3_tensor_view *input = m3_hip_checked_input(&commands[index],
+                                                       &kind);
+    char message[M3_HIP_MESSAGE] = "";
+    m3_hip_view view;
+    int code;
+
+    if (input == NULL || input->metadata.element_count == 0U ||
+        !m3_hip_written_before(commands, index, input->storage)) {
+        return M3_STATUS_OK;
     }
+    m3_hip_view_of(input, &view);
+    code = m3_hip_scan_views(context->device, &kind, &view, 1U, &flag,
+                             message, sizeof(message));
+    if (code != M3_HIP_OK) {
+        return m3_hip_status(code, message, error);
+    }
+    if (flag != 0U) {
+        return m3_hip_scan_failure(kind, error);
+    }
+    m3_hip_remember_clean(context, &view, kind);
     return M3_STATUS_OK;
 }
 
@@ -564,6 +584,10 @@ static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
         return status;
     }
     for (i = 0U; i < count && code == M3_HIP_OK; ++i) {
+        status = m3_hip_scan_produced(context, commands, i, error);
+        if (status != M3_STATUS_OK) {
+            return status;
+        }
         m3_hip_forget_outputs(context, &commands[i]);
         code = m3_hip_enqueue(context, &commands[i], message,
                               sizeof(message));

@@ -1,12 +1,16 @@
 """Command-list semantics of the HIP provider (GPU).
 
 Restates the GPU-provider list contracts the reference tests for Metal:
-data preflight is list-atomic, a softmax or float-to-I32 cast whose input
-is written earlier in the same list is rejected with UNSUPPORTED before
-anything runs, and the first failing command in list order decides the
+data preflight of inputs that no command of the list writes is
+list-atomic, and the first failing command in list order decides the
 status (tests/test_metal_basic_softmax.c:242-357,
-tests/test_metal_cast.c:294-424). Also covers the provider's cache of
-clean inputs: a later host write or kernel output must be rescanned.
+tests/test_metal_cast.c:294-424). A softmax or float-to-I32 cast whose
+input IS written earlier in the list, which Metal rejects with UNSUPPORTED,
+runs here with the reference CPU provider's order instead (preflight right
+before the command, src/m3_op_execute_host.c:5-60): its producers run, its
+input is scanned on the device, and a failing scan stops the list there
+with OUT_OF_RANGE. Also covers the provider's cache of clean inputs: a
+later host write or kernel output must be rescanned.
 """
 import math
 import sys
@@ -15,7 +19,7 @@ import numpy as np
 import pytest
 
 from conftest import m3
-from harness import HipFixture, ViewSpec, as_bytes
+from harness import HipFixture, ViewSpec, as_bytes, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -64,21 +68,44 @@ def test_softmax_preflight_order(hip):
                              (m3.OP_SOFTMAX, [sm_in, sm_out])])
     assert status == m3.OK
     assert list(values(hip, h[2], 3)) == [6, 8, 10]
-    # A producer of the softmax input earlier in the list is rejected.
+    # The softmax input is produced earlier in the list (over a NaN the host
+    # wrote): the producer runs, the produced input is scanned on the
+    # device, and the softmax runs on it.
     write(hip, h[3], f32([0, math.nan, 1]))
     write(hip, h[4], sentinel)
     status, message = hip.execute([(m3.OP_ADD, [left, right, sm_in]),
                                    (m3.OP_SOFTMAX, [sm_in, sm_out])])
-    assert status == m3.UNSUPPORTED
-    assert "depends on an earlier output" in message
+    assert status == m3.OK, message
+    assert list(values(hip, h[3], 3)) == [5, 6, 7]
+    expected = softmax_oracle(f32([5, 6, 7]))
+    assert np.array_equal(values(hip, h[4], 3).view(np.uint32),
+                          expected.view(np.uint32))
+    # A producer that writes a NaN: it runs, the softmax does not.
+    write(hip, h[2], f32([1, math.nan, 1]))
+    write(hip, h[4], sentinel)
+    status, message = hip.execute([(m3.OP_MUL, [left, unrelated, sm_in]),
+                                   (m3.OP_SOFTMAX, [sm_in, sm_out])])
+    assert status == m3.OUT_OF_RANGE
+    assert "NaN" in message
     got = values(hip, h[3], 3)
-    assert got[0] == 0 and math.isnan(got[1]) and got[2] == 1
+    assert got[0] == 3 and math.isnan(got[1]) and got[2] == 5
     assert list(values(hip, h[4], 3)) == [-9, -9, -9]
-    # A softmax output is a prior writer too.
+    # A softmax output is a producer too: softmax of a softmax.
     status, _ = hip.execute([(m3.OP_SOFTMAX, [left, sm_in]),
                              (m3.OP_SOFTMAX, [sm_in, sm_out])])
-    assert status == m3.UNSUPPORTED
-    assert list(values(hip, h[4], 3)) == [-9, -9, -9]
+    assert status == m3.OK
+    expected = softmax_oracle(softmax_oracle(f32([3, 4, 5])))
+    assert np.array_equal(values(hip, h[4], 3).view(np.uint32),
+                          expected.view(np.uint32))
+
+
+def softmax_oracle(row):
+    views = [ViewSpec(0, m3.F32, (row.size,)), ViewSpec(1, m3.F32, (row.size,))]
+    status, out = run_oracle(m3.OP_SOFTMAX, [as_bytes(row),
+                                             np.zeros(row.nbytes, np.uint8)],
+                             views)
+    assert status == m3.OK
+    return out[1].view(np.float32)
 
 
 def test_float_to_i32_cast_atomic(hip):
@@ -92,18 +119,30 @@ def test_float_to_i32_cast_atomic(hip):
     status, _ = hip.execute([(m3.OP_CAST, [src, dst])])
     assert status == m3.OUT_OF_RANGE
     assert list(values(hip, h[2], 4, np.int32)) == [77, 78, 79, 80]
-    # COPY then CAST of the copied (produced) values: rejected, untouched.
-    status, _ = hip.execute([(m3.OP_COPY, [src, middle]),
-                             (m3.OP_CAST, [middle, dst])])
-    assert status == m3.UNSUPPORTED
-    assert list(values(hip, h[1], 4)) == [9, 8, 7, 6]
-    assert list(values(hip, h[2], 4, np.int32)) == [77, 78, 79, 80]
-    # Earlier invalid cast wins over a later dependent one.
+    # Earlier invalid cast of a list input wins over a later dependent
+    # one, and nothing runs.
     status, _ = hip.execute([(m3.OP_CAST, [src, dst]),
                              (m3.OP_COPY, [src, middle]),
                              (m3.OP_CAST, [middle, dst])])
     assert status == m3.OUT_OF_RANGE
     assert list(values(hip, h[1], 4)) == [9, 8, 7, 6]
+    assert list(values(hip, h[2], 4, np.int32)) == [77, 78, 79, 80]
+    # COPY then CAST of the copied (produced) invalid values: the COPY
+    # runs, the CAST is rejected on the device scan and writes nothing.
+    status, message = hip.execute([(m3.OP_COPY, [src, middle]),
+                                   (m3.OP_CAST, [middle, dst])])
+    assert status == m3.OUT_OF_RANGE
+    assert "invalid" in message
+    got = values(hip, h[1], 4)
+    assert got[0] == 1 and math.isnan(got[1]) and got[2] == 2 and \
+        math.isinf(got[3])
+    assert list(values(hip, h[2], 4, np.int32)) == [77, 78, 79, 80]
+    # Valid produced values are cast.
+    write(hip, h[0], f32([1.5, -2.5, 3e9 / 2, -7.0]))
+    status, message = hip.execute([(m3.OP_COPY, [src, middle]),
+                                   (m3.OP_CAST, [middle, dst])])
+    assert status == m3.OK, message
+    assert list(values(hip, h[2], 4, np.int32)) == [1, -2, 1500000000, -7]
 
 
 def test_clean_input_cache_sees_later_writes(hip):

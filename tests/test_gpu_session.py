@@ -370,3 +370,52 @@ def test_two_sessions_interleave(gpu):
                                  np.float32)
         assert np.array_equal(bits(got), bits(expected))
         session.free()
+
+
+def test_scaled_scores_then_softmax(gpu):
+    """A softmax whose input a MUL produces in the same run (attention
+    scores times a scale): the MUL runs, its output is scanned on the
+    device, and the softmax runs on it, equal to the oracle's MUL then
+    softmax bit for bit. With a producer that makes a NaN (inf * 0) the run
+    fails with OUT_OF_RANGE and the softmax output keeps its old bits."""
+    from harness import ViewSpec, as_bytes, run_oracle
+    rng = np.random.default_rng(77)
+    shape = (64, 200)
+    scores = (rng.standard_normal(shape) * 4).astype(np.float32)
+    scale = np.array([0.125], np.float32)
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, shape)
+    c = g.add_value(m3.INPUT, m3.F32, (1,))
+    t = g.add_inferred(m3.OP_MUL, [x, c], m3.TEMPORARY, m3.F32)
+    g.add_node(m3.OP_MUL, [x, c], [t])
+    y = g.add_inferred(m3.OP_SOFTMAX, [t], m3.OUTPUT, m3.F32)
+    g.add_node(m3.OP_SOFTMAX, [t], [y])
+    session = m3.Session(g)
+    g.free()
+    assert [session.provider(i) for i in range(2)] == [m3.PROVIDER_HIP] * 2
+    session.write(x, scores)
+    session.write(c, scale)
+    session.run()
+    out = session.read(y, np.zeros(shape, np.float32))
+    views = [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, (1,)),
+             ViewSpec(2, m3.F32, shape)]
+    _, mul = run_oracle(m3.OP_MUL, [as_bytes(scores), as_bytes(scale),
+                                    np.zeros(scores.nbytes, np.uint8)], views)
+    views = [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, shape)]
+    status, soft = run_oracle(m3.OP_SOFTMAX, [mul[2], np.zeros(
+        scores.nbytes, np.uint8)], views)
+    assert status == m3.OK
+    assert np.array_equal(out.view(np.uint32).reshape(-1),
+                          soft[1].view(np.uint32))
+    # inf * 0 = NaN reaches the softmax input: the run stops there
+    bad = scores.copy()
+    bad[3, 7] = np.inf
+    session.write(x, bad)
+    session.write(c, np.zeros(1, np.float32))
+    with pytest.raises(m3.M3Error) as failure:
+        session.run()
+    assert failure.value.status == m3.OUT_OF_RANGE
+    assert "NaN" in failure.value.message
+    again = session.read(y, np.zeros(shape, np.float32))
+    assert np.array_equal(again.view(np.uint32), out.view(np.uint32))
+    session.free()
