@@ -4,8 +4,10 @@ A step is one ``m3_session_run`` of a graph built through the public API
 (include/m3.h), with its inputs already resident in HBM. The headline
 workload is last-axis softmax F32 on an attention-score tensor
 [16, 1024, 1024] (logits ~ N(0, 3), strict upper triangle -inf); the other
-op classes (broadcast MUL, the four casts, Snake1d, the 30-step Euler CFG
-graph) are measured the same way and reported under ``op_classes``.
+op classes (broadcast MUL, the four casts, Snake1d, TANH, GATED_SILU, the
+30-step Euler CFG graph) are measured the same way and reported under
+``op_classes``; ``executor`` times the reference's flow math issued one
+command per m3_command_executor_execute call.
 
 For every class:
   * ms_per_run    wall time of m3_session_run (includes the softmax NaN
@@ -331,6 +333,118 @@ def build_euler(x, vus, vcs, scale=3.0, dt=1.0 / 30.0):
     return build
 
 
+class FlowExecutor:
+    """The flow math of the reference run the way its flow code runs it
+    (src/m3_flow_solver_math.c:36-135): one command per
+    m3_command_executor_execute call on a HIP backend, the one-element
+    scalar rewritten from the host between commands. Buffers: velocity
+    [2, L, C] (conditional half, unconditional half), latent and arithmetic
+    [1, L, C]."""
+
+    def __init__(self, length, channels):
+        self.lib, self.hip = m3.load()
+        self.backend = ctypes.c_void_p()
+        error = m3.Error()
+        m3.check(self.lib.m3_backend_create_hip(ctypes.byref(self.backend),
+                                                ctypes.byref(error)), error)
+        self.shape = (1, length, channels)
+        self.bytes = 4 * length * channels
+        self.storages = {}
+        for name, size in (("velocity", 2 * self.bytes),
+                           ("latent", self.bytes), ("arith", self.bytes),
+                           ("scalar", 4)):
+            storage = ctypes.c_void_p()
+            m3.check(self.lib.m3_storage_allocate(
+                self.backend, size, 256, ctypes.byref(storage),
+                ctypes.byref(error)), error)
+            self.storages[name] = storage
+        self.views = {}
+        for name, storage, shape, offset in (
+                ("cond", "velocity", self.shape, 0),
+                ("uncond", "velocity", self.shape, self.bytes),
+                ("latent", "latent", self.shape, 0),
+                ("arith", "arith", self.shape, 0),
+                ("scalar", "scalar", (1,), 0)):
+            view = m3.TensorView()
+            dims = (ctypes.c_uint64 * 8)(*shape)
+            m3.check(self.lib.m3_tensor_view_contiguous(
+                ctypes.byref(view), self.storages[storage], m3.F32,
+                len(shape), dims, offset, ctypes.byref(error)), error)
+            self.views[name] = view
+        self.executor = (ctypes.c_uint8 * 64)()
+        self.lib.m3_command_executor_init(self.executor, self.backend)
+        self.lib.m3_command_executor_execute.argtypes = [
+            ctypes.c_void_p, ctypes.POINTER(m3.Command), ctypes.c_size_t,
+            ctypes.POINTER(m3.Error)]
+        self.finish_each = False
+
+    def write(self, name, array):
+        array = np.ascontiguousarray(array, np.float32)
+        error = m3.Error()
+        m3.check(self.lib.m3_storage_write(
+            self.storages[name], 0, array.ctypes.data_as(ctypes.c_void_p),
+            array.nbytes, ctypes.byref(error)), error)
+
+    def read(self, name):
+        out = np.zeros(self.shape, np.float32)
+        error = m3.Error()
+        m3.check(self.lib.m3_storage_read(
+            self.storages[name], 0, out.ctypes.data_as(ctypes.c_void_p),
+            out.nbytes, ctypes.byref(error)), error)
+        return out
+
+    def finish(self):
+        error = m3.Error()
+        m3.check(self.lib.m3_backend_finish(self.backend,
+                                            ctypes.byref(error)), error)
+
+    def op(self, kind, left, right, output):
+        command = m3.Command()
+        command.kind = kind
+        for i, name in enumerate((left, right, output)):
+            command.descriptor.views[i] = ctypes.pointer(self.views[name])
+        error = m3.Error()
+        m3.check(self.lib.m3_command_executor_execute(
+            self.executor, ctypes.byref(command), 1, ctypes.byref(error)),
+            error)
+        if self.finish_each:
+            self.finish()
+
+    def step(self, guidance, delta):
+        """Guided velocity then one Euler step: 3 scalar writes, 6 lists."""
+        self.write("scalar", [-1.0])
+        self.op(m3.OP_MUL, "uncond", "scalar", "arith")
+        self.op(m3.OP_ADD, "cond", "arith", "arith")
+        self.write("scalar", [guidance])
+        self.op(m3.OP_MUL, "arith", "scalar", "arith")
+        self.op(m3.OP_ADD, "uncond", "arith", "arith")
+        self.write("scalar", [delta])
+        self.op(m3.OP_MUL, "arith", "scalar", "arith")
+        self.op(m3.OP_ADD, "latent", "arith", "latent")
+
+    def timing(self, enabled):
+        device = self.lib.m3_backend_hip_device(self.backend)
+        self.hip.m3_hip_timing_reset(device)
+        self.hip.m3_hip_timing_enable(device, 1 if enabled else 0)
+
+    def kernel_ms(self):
+        device = self.lib.m3_backend_hip_device(self.backend)
+        entries = (m3.HipKernelTime * 64)()
+        count = ctypes.c_size_t()
+        message = ctypes.create_string_buffer(256)
+        self.hip.m3_hip_timing_read(device, entries, 64, ctypes.byref(count),
+                                    message, 256)
+        return {entries[i].name.decode(): (entries[i].launches,
+                                           entries[i].total_ms)
+                for i in range(count.value)}
+
+    def free(self):
+        self.lib.m3_command_executor_dispose(self.executor)
+        for storage in self.storages.values():
+            self.lib.m3_storage_free(storage)
+        self.lib.m3_backend_free(self.backend)
+
+
 def spec(storage, dtype, shape, strides=None):
     return baseline_harness().ViewSpec(storage, dtype, tuple(shape), strides)
 
@@ -379,7 +493,7 @@ def main():
     parser.add_argument("--rotate", type=int, default=4)
     parser.add_argument("--classes",
                         default="softmax,mul,cast,copy,snake,tanh,gated_silu,"
-                                "euler",
+                                "euler,executor",
                         help="comma-separated op classes to run")
     parser.add_argument("--no-cpu", action="store_true",
                         help="skip the CPU baseline and CPU parity check")
@@ -676,6 +790,70 @@ def main():
         results["euler"] = entry
         w.free()
         log("euler:", json.dumps(results["euler"]))
+
+    if "executor" in classes:
+        length, channels, steps = 4096, 128, 30
+        log("executor: flow math through m3_command_executor_execute, "
+            "latent [1,%d,%d], %d steps" % (length, channels, steps))
+        rng = np.random.default_rng(5)
+        velocity = rng.standard_normal((2, length, channels)).astype(
+            np.float32)
+        latent0 = rng.standard_normal((1, length, channels)).astype(
+            np.float32)
+        guidance, delta = 3.0, 1.0 / steps
+        flow = FlowExecutor(length, channels)
+        flow.write("velocity", velocity)
+        timings = {}
+        for mode in ("queued", "finish_each"):
+            flow.finish_each = mode == "finish_each"
+            flow.write("latent", latent0)
+            flow.step(guidance, delta)  # warm-up
+            flow.write("latent", latent0)
+            flow.finish()
+            start = time.perf_counter()
+            for _ in range(steps):
+                flow.step(guidance, delta)
+            flow.finish()
+            timings[mode] = 1000.0 * (time.perf_counter() - start) / steps
+        flow.finish_each = False
+        flow.write("latent", latent0)
+        flow.timing(True)
+        for _ in range(steps):
+            flow.step(guidance, delta)
+        kernels = flow.kernel_ms()
+        flow.timing(False)
+        out = flow.read("latent")
+        f = np.float32
+        expected = latent0.copy()
+        cond, uncond = velocity[0:1], velocity[1:2]
+        for _ in range(steps):
+            a = (uncond * f(-1.0)).astype(f)
+            a = (cond + a).astype(f)
+            a = (a * f(guidance)).astype(f)
+            a = (uncond + a).astype(f)
+            a = (a * f(delta)).astype(f)
+            expected = (expected + a).astype(f)
+        parity = ("bit-exact vs the same float32 operations in numpy"
+                  if np.array_equal(out.view(np.uint32),
+                                    expected.view(np.uint32))
+                  else "latent differs")
+        flow.free()
+        tensor = 4 * length * channels
+        results["executor"] = {
+            "op_class": "executor",
+            "workload": "per Euler step: guided velocity and one Euler "
+                        "update, 3 host scalar writes and 6 single-command "
+                        "lists (src/m3_flow_solver_math.c:36-135)",
+            "algorithmic_bytes_per_step": 15 * tensor,
+            "ms_per_step": round(timings["queued"], 4),
+            "ms_per_step_finish_each_list": round(timings["finish_each"], 4),
+            "kernel_ms_per_step": round(
+                sum(ms for _, ms in kernels.values()) / steps, 4),
+            "kernels": {name: [count // steps, round(ms / max(count, 1), 4)]
+                        for name, (count, ms) in kernels.items()},
+            "parity": parity,
+        }
+        log("executor:", json.dumps(results["executor"]))
 
     if headline is None:
         print(json.dumps({"metric": METRIC, "op_classes": results}))

@@ -331,12 +331,15 @@ typedef struct {
     size_t peak_storage_count;
 } m3_backend_allocation_stats;
 
-/* Backend lifetime contract (src/m3_backend_internal.h:9-18) plus three
+/* Backend lifetime contract (src/m3_backend_internal.h:9-18) plus four
  * optional hooks. destroy_context, allocate, free_storage and execute are
  * required. write/read copy between host memory and storage `data` at a
  * byte offset; both set means the storage is device memory. reserve asks
  * for one arena of `byte_count` bytes from which later allocations may be
- * carved. */
+ * carved. finish waits until every command executed so far has completed
+ * and reports a failure that surfaced while they ran; a backend with a
+ * finish hook may return from execute once the commands are queued (write,
+ * read and destroy_context still see their results). */
 typedef struct {
     void (*destroy_context)(void *context);
     m3_status (*allocate)(void *context, size_t byte_count, size_t alignment,
@@ -352,6 +355,7 @@ typedef struct {
                       void *destination, size_t byte_count,
                       m3_error *error);
     m3_status (*reserve)(void *context, size_t byte_count, m3_error *error);
+    m3_status (*finish)(void *context, m3_error *error);
 } m3_backend_vtable;
 
 m3_status m3_backend_create_internal(const m3_backend_vtable *vtable,
@@ -372,6 +376,12 @@ m3_status m3_backend_get_allocation_stats(
 m3_status m3_backend_reserve(m3_backend *backend, size_t byte_count,
                              m3_error *error);
 void *m3_backend_context_internal(const m3_backend *backend);
+/* Waits until every command executed on `backend` so far has completed
+ * (no-op for backends that complete commands inside execute). Sessions
+ * call it at the end of m3_session_run; callers of m3_backend_execute or
+ * m3_command_executor_execute call it when they need the commands done
+ * without reading a storage. */
+m3_status m3_backend_finish(m3_backend *backend, m3_error *error);
 
 m3_status m3_storage_allocate(m3_backend *backend, size_t byte_count,
                               size_t alignment, m3_storage **storage,

@@ -136,7 +136,10 @@ int m3_hip_arena_reserve(m3_hip_device *device, size_t byte_count,
 void m3_hip_arena_release(m3_hip_device *device, void *base);
 
 /* Stream-ordered copies. Both return once the host buffer may be reused
- * (h2d) or holds the data (d2h). */
+ * (h2d) or holds the data (d2h). A host-to-device copy of at most 256
+ * bytes (a scalar the host rewrites between commands) travels in a
+ * kernel's arguments and does not wait for the stream; a larger one waits
+ * for the copy to complete. */
 int m3_hip_copy_h2d(m3_hip_device *device, void *device_destination,
                     const void *host_source, size_t byte_count,
                     char *message, size_t capacity);

@@ -168,7 +168,7 @@ EXPORTS_M3 = [
     "m3_tensor_element_offset", "m3_tensor_slice", "m3_tensor_reshape",
     "m3_tensor_permute", "m3_scratch_arena_init", "m3_scratch_arena_mark",
     "m3_scratch_arena_rewind", "m3_command_validate",
-    "m3_commands_scratch_bytes", "m3_backend_execute",
+    "m3_commands_scratch_bytes", "m3_backend_execute", "m3_backend_finish",
     "m3_backend_create_internal", "m3_backend_create_hip", "m3_backend_free",
     "m3_backend_get_info", "m3_backend_get_allocation_stats",
     "m3_backend_reserve", "m3_backend_context_internal",
@@ -261,6 +261,7 @@ def load():
     _declare(lib, "m3_command_validate", st, vp, P(Command), err)
     _declare(lib, "m3_backend_execute", st, vp, P(Command), sz,
              P(ScratchArena), err)
+    _declare(lib, "m3_backend_finish", st, vp, err)
     _declare(lib, "m3_backend_create_hip", st, P(vp), err)
     _declare(lib, "m3_backend_free", None, vp)
     _declare(lib, "m3_backend_get_info", st, vp, P(BackendInfo), err)

@@ -397,6 +397,25 @@ extern "C" void m3_hip_arena_release(m3_hip_device *device, void *base)
     (void)hipFree(base);
 }
 
+/* A host-to-device copy of at most kSmallCopy bytes carried in the
+ * kernel's arguments: stream-ordered like any launch, and the host buffer
+ * is free as soon as the launch returns, so the caller does not wait. */
+constexpr uint32_t kSmallCopy = 256U;
+
+struct m3_small_copy_args {
+    uint8_t *destination;
+    uint32_t count;
+    uint8_t bytes[kSmallCopy];
+};
+
+__global__ __launch_bounds__(256) void m3_small_copy_kernel(
+    m3_small_copy_args a)
+{
+    if (threadIdx.x < a.count) {
+        a.destination[threadIdx.x] = a.bytes[threadIdx.x];
+    }
+}
+
 extern "C" int m3_hip_copy_h2d(m3_hip_device *device,
                                void *device_destination,
                                const void *host_source, size_t byte_count,
@@ -413,6 +432,23 @@ extern "C" int m3_hip_copy_h2d(m3_hip_device *device,
     if (byte_count == 0U) {
         return M3_HIP_OK;
     }
+    if (byte_count <= kSmallCopy) {
+        m3_small_copy_args args;
+
+        std::memset(&args, 0, sizeof(args));
+        args.destination = (uint8_t *)device_destination;
+        args.count = (uint32_t)byte_count;
+        std::memcpy(args.bytes, host_source, byte_count);
+        return m3_hip_launch(
+            device, "m3_small_copy",
+            [&](hipEvent_t start, hipEvent_t stop) {
+                hipExtLaunchKernelGGL(m3_small_copy_kernel, dim3(1),
+                                      dim3(kSmallCopy), 0, device->stream,
+                                      start, stop, 0U, args);
+            },
+            message, capacity);
+    }
+    /* pageable source: the copy is complete before the buffer is free */
     code = m3_hip_check(hipMemcpyAsync(device_destination, host_source,
                                        byte_count, hipMemcpyHostToDevice,
                                        device->stream),

@@ -72,6 +72,19 @@ m3_status m3_backend_create_internal(const m3_backend_vtable *vtable,
     return M3_STATUS_OK;
 }
 
+m3_status m3_backend_finish(m3_backend *backend, m3_error *error)
+{
+    if (backend == NULL) {
+        return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
+                            "backend is null");
+    }
+    if (backend->vtable->finish == NULL) {
+        m3_error_reset(error);
+        return M3_STATUS_OK;
+    }
+    return backend->vtable->finish(backend->context, error);
+}
+
 m3_status m3_backend_execute(m3_backend *backend, const m3_command *commands,
                              size_t command_count, m3_scratch_arena *scratch,
                              m3_error *error)

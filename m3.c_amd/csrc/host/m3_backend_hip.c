@@ -153,6 +153,8 @@ static void m3_hip_destroy(void *opaque)
     m3_hip_backend_context *context = opaque;
     size_t i;
 
+    /* queued commands may still use the arenas */
+    (void)m3_hip_synchronize(context->device, NULL, 0U);
     for (i = 0U; i < context->arena_count; ++i) {
         m3_hip_arena_release(context->device, context->arenas[i].base);
     }
@@ -233,6 +235,8 @@ static void m3_hip_free_storage(void *opaque, void *handle, void *data)
 
     m3_hip_forget_storage(context, data);
     if (handle != NULL) {
+        /* queued commands may still use the memory */
+        (void)m3_hip_synchronize(context->device, NULL, 0U);
         m3_hip_arena_release(context->device, handle);
     }
 }
@@ -593,18 +597,30 @@ static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
                               sizeof(message));
     }
     if (code == M3_HIP_OK) {
-        code = m3_hip_synchronize(context->device, message, sizeof(message));
-    } else {
-        (void)m3_hip_synchronize(context->device, NULL, 0U);
+        /* queued; m3_hip_finish, a storage read or write, a data scan or
+         * destroy waits for it */
+        m3_error_reset(error);
+        return M3_STATUS_OK;
     }
+    (void)m3_hip_synchronize(context->device, NULL, 0U);
     return m3_hip_status(code, message, error);
+}
+
+static m3_status m3_hip_finish(void *opaque, m3_error *error)
+{
+    m3_hip_backend_context *context = opaque;
+    char message[M3_HIP_MESSAGE] = "";
+    int code = m3_hip_synchronize(context->device, message, sizeof(message));
+
+    return code == M3_HIP_OK ? M3_STATUS_OK
+                             : m3_hip_status(code, message, error);
 }
 
 m3_status m3_backend_create_hip(m3_backend **backend, m3_error *error)
 {
     static const m3_backend_vtable vtable = {
         m3_hip_destroy, m3_hip_allocate, m3_hip_free_storage, m3_hip_execute,
-        m3_hip_write,   m3_hip_read,     m3_hip_reserve};
+        m3_hip_write,   m3_hip_read,     m3_hip_reserve,      m3_hip_finish};
     m3_hip_backend_context *context;
     m3_backend_info info;
     char message[M3_HIP_MESSAGE] = "";

@@ -104,8 +104,8 @@ m3_status m3_session_run(m3_session *session, m3_error *error)
         }
         begin = end;
     }
-    m3_error_reset(error);
-    return M3_STATUS_OK;
+    /* a run is complete when it returns, as on the reference's providers */
+    return m3_backend_finish(session->backend, error);
 }
 
 m3_status m3_session_get_plan_info(const m3_session *session,
