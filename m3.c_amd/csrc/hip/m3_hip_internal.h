@@ -41,6 +41,10 @@ struct m3_hip_device {
     uint32_t *scan_flags;
     size_t scan_capacity;
     uint32_t *host_flags;
+    /* completion word in coherent pinned host memory (may be null) and the
+     * last sequence number a kernel was queued to store there */
+    uint32_t *done_word;
+    uint32_t done_sequence;
     bool timing;
     std::vector<m3_hip_pending_time> pending;
     std::vector<hipEvent_t> spare_events;
