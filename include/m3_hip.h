@@ -190,32 +190,42 @@ int m3_hip_launch_gated_silu(m3_hip_device *device, const m3_hip_view *gate,
                              const m3_hip_view *output, char *message,
                              size_t capacity);
 
-/* Elementwise program: a run of F32 ADD/SUB/MUL/DIV operations over one
- * element space of `count` elements, executed per element with the
- * intermediate values in registers. Layout of the 32-bit words:
+/* Elementwise program: a run of ADD/SUB/MUL/DIV and float-to-float CAST
+ * (or F32 COPY) operations over one element space of `count` elements,
+ * executed per element with the intermediate values in registers as F32.
+ * Layout of the 32-bit words:
  *   [0] M3_HIP_PROGRAM_MAGIC
  *   [1] P, operand count (at most M3_HIP_PROGRAM_MAX_OPERANDS)
  *   [2] I, instruction word count (at most M3_HIP_PROGRAM_MAX_WORDS)
  *   [3] count, low 32 bits     [4] count, high 32 bits
  *   [5..7] zero
- *   [8 .. 8+2P) operand p: device address, low word then high word. Bit 0
- *       of the low word set: a scalar, one F32 read by every element (the
- *       address is 4-byte aligned). Clear: an F32 array of `count` elements
- *       (16-byte aligned), element e at address + 4e.
+ *   [8 .. 8+2P) operand p: device address, low word then high word. Bits
+ *       30-31 of the high word: the element dtype (M3_HIP_F32, M3_HIP_F16
+ *       or M3_HIP_BF16). Bit 0 of the low word set: a scalar, one element
+ *       read by every element (aligned to its size). Clear: an array of
+ *       `count` elements (16-byte aligned for F32, 8-byte for 16-bit),
+ *       element e at address + e * size.
  *   [8+2P .. 8+2P+I) instructions.
  * Registers per element: values R0..R3 and fetched operands F0..F3.
  * Instructions (bits 0-1 opcode):
  *   FETCH (two words): bits 2-3 n-1; the second word holds operand
- *       indices f0..f{n-1} in its bytes 0..n-1. Loads array operand fk
- *       into Fk for k < n; all n loads are issued together.
+ *       indices f0..f{n-1} in its bytes 0..n-1. Loads array operand fk,
+ *       converted to F32, into Fk for k < n; all n loads are issued
+ *       together.
  *   OP: bits 2-3 the m3_hip_binary_op; bits 4-5 destination R; bits 8-11
  *       left source, bits 12-15 right source (0-3: R0-R3, 4-7: F0-F3,
- *       8: the scalar operand in bits 16-23). dst = left (op) right as one
- *       F32 operation with the reference's NaN rules.
- *   STORE: bits 4-5 source R; bits 8-15 array operand; writes the value.
+ *       8: the scalar operand in bits 16-23); bits 24-25 a rounding dtype.
+ *       dst = left (op) right as one F32 operation with the reference's
+ *       NaN rules, then rounded through the rounding dtype (F16/BF16: the
+ *       value a store to it and a load back give; F32: unchanged).
+ *   ROUND: bits 4-5 destination R; bits 8-11 source (as OP's left, scalar
+ *       index in bits 16-23); bits 24-25 the dtype. dst = source rounded
+ *       through the dtype (a CAST; F32 makes it a move).
+ *   STORE: bits 4-5 source R; bits 8-15 array operand; writes the value
+ *       converted to the operand's dtype.
  * m3_hip_launch_program checks the words on the host (magic, counts,
- * indices, operand kinds and alignment) before launching; device_words must
- * hold the same words in device memory. */
+ * indices, operand kinds, dtypes and alignment) before launching;
+ * device_words must hold the same words in device memory. */
 #define M3_HIP_PROGRAM_MAGIC 0x4d335031U /* "M3P1" */
 #define M3_HIP_PROGRAM_HEADER_WORDS 8U
 #define M3_HIP_PROGRAM_MAX_OPERANDS 255U
@@ -224,7 +234,8 @@ int m3_hip_launch_gated_silu(m3_hip_device *device, const m3_hip_view *gate,
 typedef enum {
     M3_HIP_PROGRAM_FETCH = 0,
     M3_HIP_PROGRAM_OP = 1,
-    M3_HIP_PROGRAM_STORE = 2
+    M3_HIP_PROGRAM_STORE = 2,
+    M3_HIP_PROGRAM_ROUND = 3
 } m3_hip_program_opcode;
 
 int m3_hip_launch_program(m3_hip_device *device, const uint32_t *words,

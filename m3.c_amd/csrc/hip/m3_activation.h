@@ -16,17 +16,6 @@
 #include "m3_libm.h"
 #include "m3_numeric.h"
 
-/* F32 bits rounded through a 16-bit float dtype and back (identity for
- * F32), with the converters of CAST. */
-M3_HD uint32_t m3_round_through_bits(uint32_t bits, uint32_t dtype)
-{
-    return dtype == M3N_F16
-               ? m3_f16_to_f32_bits(m3_f32_to_f16_bits(bits))
-           : dtype == M3N_BF16
-               ? m3_bf16_to_f32_bits(m3_f32_to_bf16_bits(bits))
-               : bits;
-}
-
 /* The unrounded activation gate / (1 + expf(-gate)). Its bits equal the
  * host's whenever they are not NaN. */
 M3_HD float m3_silu_quotient(float gate)

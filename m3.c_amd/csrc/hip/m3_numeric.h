@@ -162,6 +162,18 @@ M3_HD uint32_t m3_store_from_f32_bits(uint32_t bits, uint32_t dtype)
                                : (uint32_t)(int32_t)m3_bits_f32(bits);
 }
 
+/* F32 bits rounded through a 16-bit float dtype and back (identity for
+ * F32), with the converters of CAST: the value a store of `bits` to that
+ * dtype and a load back give (src/m3_op_numeric.c:210-222). */
+M3_HD uint32_t m3_round_through_bits(uint32_t bits, uint32_t dtype)
+{
+    return dtype == M3N_F16
+               ? m3_f16_to_f32_bits(m3_f32_to_f16_bits(bits))
+           : dtype == M3N_BF16
+               ? m3_bf16_to_f32_bits(m3_f32_to_bf16_bits(bits))
+               : bits;
+}
+
 /* One F32 operation, IEEE round-to-nearest-even, no contraction. */
 M3_HD uint32_t m3_binary_f32_bits(uint32_t op, uint32_t a, uint32_t b)
 {

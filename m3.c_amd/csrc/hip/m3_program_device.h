@@ -4,11 +4,14 @@
  * from program words at run time (compiled with hipRTC, which receives
  * this header and m3_numeric.h as in-memory headers).
  *
- * Element e of an array operand is the F32 at its address + 4e; a lane
- * handles the four elements 4g..4g+3. The last, partial group reads and
- * writes only the elements below `count`. Every operation is one F32
- * operation rounded to nearest even with the NaN results of
- * m3_binary_f32_bits.
+ * Element e of an array operand of dtype D (F32, F16 or BF16, bits 30-31
+ * of its high address word) is at its address + e * size(D); a lane
+ * handles the four elements 4g..4g+3 and holds them as F32. The last,
+ * partial group reads and writes only the elements below `count`. Loads
+ * convert to F32 and stores from F32 with the converters of CAST; an
+ * operation is one F32 operation rounded to nearest even with the NaN
+ * results of m3_binary_f32_bits, then rounded through its output dtype
+ * when that is F16 or BF16 (the value a store and a load back give).
  */
 #ifndef M3_PROGRAM_DEVICE_H
 #define M3_PROGRAM_DEVICE_H
@@ -16,32 +19,51 @@
 #include "m3_numeric.h"
 
 typedef float m3_program_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int m3_program_u32x2 __attribute__((ext_vector_type(2)));
 /* Operand memory is global memory: accesses through these types are
  * global (not flat) loads and stores, so a wait for scalar loads (operand
  * addresses) does not also wait for the lane's vector loads. */
 typedef float __attribute__((address_space(1))) m3_program_global_f32;
 typedef m3_program_f32x4
     __attribute__((address_space(1))) m3_program_global_f32x4;
+typedef unsigned short __attribute__((address_space(1))) m3_program_global_u16;
+typedef m3_program_u32x2
+    __attribute__((address_space(1))) m3_program_global_u32x2;
 
 __device__ __forceinline__ const unsigned char *m3_program_address(
     const unsigned int *operands, unsigned int index)
 {
     unsigned long long low = operands[2U * index];
-    unsigned long long high = operands[2U * index + 1U];
+    unsigned long long high = operands[2U * index + 1U] & 0x3fffffffU;
 
     return (const unsigned char *)(((high << 32U) | low) & ~1ULL);
 }
 
-/* A scalar operand: one F32 that no lane writes during the launch, read
- * through the constant address space so that it is a scalar load and does
- * not wait for the lane's outstanding vector loads. */
+/* Element type of operand `index` (M3N_F32, M3N_F16 or M3N_BF16). */
+__device__ __forceinline__ unsigned int m3_program_dtype(
+    const unsigned int *operands, unsigned int index)
+{
+    return operands[2U * index + 1U] >> 30U;
+}
+
+/* A scalar operand of dtype D: one element that no lane writes during the
+ * launch, read through the constant address space so that it is a scalar
+ * load and does not wait for the lane's outstanding vector loads. */
+template <unsigned int D>
 __device__ __forceinline__ float m3_program_scalar(
     const unsigned int *operands, unsigned int index)
 {
     typedef const float __attribute__((address_space(4))) *constant_f32;
+    typedef const unsigned short __attribute__((address_space(4))) *
+        constant_u16;
+    const unsigned long long address =
+        (unsigned long long)m3_program_address(operands, index);
 
-    return *(constant_f32)(unsigned long long)m3_program_address(operands,
-                                                                  index);
+    if (D == M3N_F32) {
+        return *(constant_f32)address;
+    }
+    return m3_bits_f32(
+        m3_load_as_f32_bits((unsigned int)*(constant_u16)address, D));
 }
 
 __device__ __forceinline__ m3_program_f32x4 m3_program_splat(float v)
@@ -51,63 +73,141 @@ __device__ __forceinline__ m3_program_f32x4 m3_program_splat(float v)
     return r;
 }
 
-template <bool FULL>
+template <bool FULL, unsigned int D>
 __device__ __forceinline__ m3_program_f32x4
 m3_program_load(const unsigned int *operands, unsigned int index,
                 unsigned long long g, unsigned long long count)
 {
-    const m3_program_global_f32 *p =
-        (const m3_program_global_f32 *)(unsigned long long)
+    const unsigned long long first = 4ULL * g;
+    m3_program_f32x4 v = {0.0F, 0.0F, 0.0F, 0.0F};
+
+    if (D == M3N_F32) {
+        const m3_program_global_f32 *p =
+            (const m3_program_global_f32 *)(unsigned long long)
+                m3_program_address(operands, index) +
+            first;
+
+        if (FULL) {
+            return *(const m3_program_global_f32x4 *)p;
+        }
+        v.x = p[0];
+        if (first + 1U < count) {
+            v.y = p[1];
+        }
+        if (first + 2U < count) {
+            v.z = p[2];
+        }
+        if (first + 3U < count) {
+            v.w = p[3];
+        }
+        return v;
+    }
+    const m3_program_global_u16 *p =
+        (const m3_program_global_u16 *)(unsigned long long)
             m3_program_address(operands, index) +
-        4ULL * g;
+        first;
+    unsigned int h[4] = {0U, 0U, 0U, 0U};
 
     if (FULL) {
-        return *(const m3_program_global_f32x4 *)p;
-    }
-    m3_program_f32x4 v = {0.0F, 0.0F, 0.0F, 0.0F};
-    const unsigned long long first = 4ULL * g;
+        const m3_program_u32x2 w = *(const m3_program_global_u32x2 *)p;
 
-    v.x = p[0];
-    if (first + 1U < count) {
-        v.y = p[1];
+        h[0] = w.x & 0xffffU;
+        h[1] = w.x >> 16U;
+        h[2] = w.y & 0xffffU;
+        h[3] = w.y >> 16U;
+    } else {
+        h[0] = p[0];
+        if (first + 1U < count) {
+            h[1] = p[1];
+        }
+        if (first + 2U < count) {
+            h[2] = p[2];
+        }
+        if (first + 3U < count) {
+            h[3] = p[3];
+        }
     }
-    if (first + 2U < count) {
-        v.z = p[2];
-    }
-    if (first + 3U < count) {
-        v.w = p[3];
-    }
+    v.x = m3_bits_f32(m3_load_as_f32_bits(h[0], D));
+    v.y = m3_bits_f32(m3_load_as_f32_bits(h[1], D));
+    v.z = m3_bits_f32(m3_load_as_f32_bits(h[2], D));
+    v.w = m3_bits_f32(m3_load_as_f32_bits(h[3], D));
     return v;
 }
 
 /* Stores are nontemporal for whole groups: program outputs are written
  * once and not read back by the launch. */
-template <bool FULL>
+template <bool FULL, unsigned int D>
 __device__ __forceinline__ void m3_program_store(
     const unsigned int *operands, unsigned int index, unsigned long long g,
     unsigned long long count, m3_program_f32x4 v)
 {
-    m3_program_global_f32 *p =
-        (m3_program_global_f32 *)(unsigned long long)m3_program_address(
-            operands, index) +
-        4ULL * g;
-
-    if (FULL) {
-        __builtin_nontemporal_store(v, (m3_program_global_f32x4 *)p);
-        return;
-    }
     const unsigned long long first = 4ULL * g;
 
-    p[0] = v.x;
+    if (D == M3N_F32) {
+        m3_program_global_f32 *p =
+            (m3_program_global_f32 *)(unsigned long long)m3_program_address(
+                operands, index) +
+            first;
+
+        if (FULL) {
+            __builtin_nontemporal_store(v, (m3_program_global_f32x4 *)p);
+            return;
+        }
+        p[0] = v.x;
+        if (first + 1U < count) {
+            p[1] = v.y;
+        }
+        if (first + 2U < count) {
+            p[2] = v.z;
+        }
+        if (first + 3U < count) {
+            p[3] = v.w;
+        }
+        return;
+    }
+    m3_program_global_u16 *p =
+        (m3_program_global_u16 *)(unsigned long long)m3_program_address(
+            operands, index) +
+        first;
+    const unsigned int h[4] = {m3_store_from_f32_bits(m3_f32_bits(v.x), D),
+                               m3_store_from_f32_bits(m3_f32_bits(v.y), D),
+                               m3_store_from_f32_bits(m3_f32_bits(v.z), D),
+                               m3_store_from_f32_bits(m3_f32_bits(v.w), D)};
+
+    if (FULL) {
+        const m3_program_u32x2 w = {h[0] | (h[1] << 16U),
+                                    h[2] | (h[3] << 16U)};
+
+        __builtin_nontemporal_store(w, (m3_program_global_u32x2 *)p);
+        return;
+    }
+    p[0] = (unsigned short)h[0];
     if (first + 1U < count) {
-        p[1] = v.y;
+        p[1] = (unsigned short)h[1];
     }
     if (first + 2U < count) {
-        p[2] = v.z;
+        p[2] = (unsigned short)h[2];
     }
     if (first + 3U < count) {
-        p[3] = v.w;
+        p[3] = (unsigned short)h[3];
     }
+}
+
+/* Four values rounded through dtype D (identity for F32). */
+template <unsigned int D>
+__device__ __forceinline__ m3_program_f32x4
+m3_program_round4(m3_program_f32x4 v)
+{
+    if (D == M3N_F32) {
+        return v;
+    }
+    m3_program_f32x4 r;
+
+    r.x = m3_bits_f32(m3_round_through_bits(m3_f32_bits(v.x), D));
+    r.y = m3_bits_f32(m3_round_through_bits(m3_f32_bits(v.y), D));
+    r.z = m3_bits_f32(m3_round_through_bits(m3_f32_bits(v.z), D));
+    r.w = m3_bits_f32(m3_round_through_bits(m3_f32_bits(v.w), D));
+    return r;
 }
 
 template <unsigned int OP>

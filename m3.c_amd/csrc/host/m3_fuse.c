@@ -4,8 +4,10 @@
  * Two passes over the nodes. The first decides group membership: a node
  * joins while the register state admits it (m3_fuse_step). The second
  * replays the same register state over each group and emits its program:
- * FETCH batches for operands produced before the group, one OP per node,
- * and a STORE for every value that must reach memory.
+ * FETCH batches for operands produced before the group, one OP (binary
+ * nodes) or ROUND (CAST, COPY) per node, and a STORE for every value that
+ * must reach memory. A unary node is described with right == left, so the
+ * register and fetch logic sees its one operand twice and counts it once.
  */
 #include "m3_fuse.h"
 
@@ -58,26 +60,49 @@ static bool m3_fuse_op_of(m3_op_kind kind, uint32_t *op)
     }
 }
 
+static bool m3_fuse_float(m3_dtype dtype)
+{
+    return dtype == M3_DTYPE_F32 || dtype == M3_DTYPE_F16 ||
+           dtype == M3_DTYPE_BF16;
+}
+
+static bool m3_fuse_unary(m3_op_kind kind)
+{
+    return kind == M3_OP_CAST || kind == M3_OP_COPY;
+}
+
 static bool m3_fuse_candidate(const m3_fuse_graph *g, size_t n)
 {
     const m3_fuse_node *node = &g->nodes[n];
     const uint32_t operands[2] = {node->left, node->right};
-    uint64_t count;
+    const m3_fuse_value *output = &g->values[node->output];
     uint32_t op;
     size_t k;
 
-    if (!node->eligible || !m3_fuse_op_of(node->kind, &op)) {
+    if (!node->eligible || output->element_count == 0U ||
+        !m3_fuse_float(output->dtype)) {
         return false;
     }
-    count = g->values[node->output].element_count;
-    if (g->values[node->output].dtype != M3_DTYPE_F32 || count == 0U) {
+    if (m3_fuse_unary(node->kind)) {
+        const m3_fuse_value *input = &g->values[node->left];
+
+        /* A 16-bit value kept in a register is F32; storing it again is
+         * not a byte copy for a signalling NaN, so a copy between equal
+         * dtypes fuses only for F32, whose register holds the raw bits. */
+        return node->right == node->left && m3_fuse_float(input->dtype) &&
+               input->element_count == output->element_count &&
+               (input->dtype != output->dtype ||
+                output->dtype == M3_DTYPE_F32);
+    }
+    if (!m3_fuse_op_of(node->kind, &op)) {
         return false;
     }
     for (k = 0U; k < 2U; ++k) {
         const m3_fuse_value *value = &g->values[operands[k]];
 
-        if (value->dtype != M3_DTYPE_F32 ||
-            (value->element_count != count && value->element_count != 1U)) {
+        if (!m3_fuse_float(value->dtype) ||
+            (value->element_count != output->element_count &&
+             value->element_count != 1U)) {
             return false;
         }
     }
@@ -361,14 +386,24 @@ static void m3_fuse_emit_group(const m3_fuse_graph *g, m3_fuse_writer *w,
                 sources[k] = M3_FUSE_FETCHES + slot;
             }
         }
-        (void)m3_fuse_op_of(node->kind, &op);
         if (!m3_fuse_step(g, &r, n, &destination)) {
             w->failed = true; /* the first pass admitted this node */
             break;
         }
-        m3_fuse_emit(w, (uint32_t)M3_HIP_PROGRAM_OP | (op << 2U) |
-                            (destination << 4U) | (sources[0] << 8U) |
-                            (sources[1] << 12U) | (scalar << 16U));
+        /* the register holds the value a store to the output's dtype and
+         * a load back give */
+        if (m3_fuse_unary(node->kind)) {
+            m3_fuse_emit(w, (uint32_t)M3_HIP_PROGRAM_ROUND |
+                                (destination << 4U) | (sources[0] << 8U) |
+                                (scalar << 16U) |
+                                ((uint32_t)output->dtype << 24U));
+        } else {
+            (void)m3_fuse_op_of(node->kind, &op);
+            m3_fuse_emit(w, (uint32_t)M3_HIP_PROGRAM_OP | (op << 2U) |
+                                (destination << 4U) | (sources[0] << 8U) |
+                                (sources[1] << 12U) | (scalar << 16U) |
+                                ((uint32_t)output->dtype << 24U));
+        }
         if (output->role != M3_GRAPH_TEMPORARY ||
             (g->last_use[node->output] != M3_FUSE_NO_NODE &&
              g->last_use[node->output] >= end)) {

@@ -2,17 +2,21 @@
  * m3_fuse.h - elementwise fusion planner of the session compiler.
  *
  * The planner sees the graph as values (role, dtype, element count) and
- * nodes in execution order, and groups consecutive F32 ADD/SUB/MUL/DIV
- * nodes of one element space into programs for m3_hip_launch_program
- * (word layout in m3_hip.h). It works on value indices only; the session
- * compiler resolves operands to device addresses. Nothing here touches a
- * device, so the planner is tested on the host.
+ * nodes in execution order, and groups consecutive ADD/SUB/MUL/DIV and
+ * CAST/COPY nodes over F32, F16 and BF16 values of one element space into
+ * programs for m3_hip_launch_program (word layout in m3_hip.h). It works
+ * on value indices only; the session compiler resolves operands to device
+ * addresses. Nothing here touches a device, so the planner is tested on
+ * the host.
  *
  * Rules, in the order nodes run:
  *   - a node may join a group when it is eligible (its provider executes
- *     programs), is ADD/SUB/MUL/DIV with F32 operands and output, and each
- *     operand has the output's element count (an array read at the same
- *     flat index) or one element (a scalar read by every element);
+ *     programs) and is either ADD/SUB/MUL/DIV whose operands and output
+ *     are F32, F16 or BF16 and whose operands have the output's element
+ *     count (an array read at the same flat index) or one element (a
+ *     scalar read by every element), or a CAST between two of those
+ *     dtypes, or a COPY of F32, described with right == left and an
+ *     input of the output's element count;
  *   - a group is a run of consecutive such nodes with the same element
  *     count; a value produced in the group lives in one of four registers
  *     from its producer to its last use, and a node joins only if a
@@ -22,7 +26,9 @@
  *   - operands produced before the group are fetched in batches of up to
  *     four arrays covering the next nodes, so their loads overlap.
  * Groups of one node are not formed. The per-element order of operations,
- * the operations themselves and every stored value are the unfused ones.
+ * the operations themselves and every stored value are the unfused ones: a
+ * value of a 16-bit dtype is kept in its register as the F32 a store and a
+ * load back give.
  */
 #ifndef M3_FUSE_H
 #define M3_FUSE_H

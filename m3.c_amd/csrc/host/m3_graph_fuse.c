@@ -3,8 +3,8 @@
  *
  * The run list is the session's commands in node order, except that each
  * group the fusion planner (m3_fuse.c) forms from consecutive ADD/SUB/
- * MUL/DIV nodes on the HIP provider becomes one elementwise-program
- * command. The planner works on value indices; here operands become device
+ * MUL/DIV and float CAST/COPY nodes on the HIP provider becomes one
+ * elementwise-program command. The planner works on value indices; here operands become device
  * addresses of the values' slots, and all programs of the session are
  * written once, at session creation, into one backend storage next to the
  * arena. Node providers, slots and allocated_bytes are those of the
@@ -49,21 +49,26 @@ static void m3_runs_unfused(m3_session *session)
     session->run_count = session->node_count;
 }
 
-/* Device address of value v's view, as two program words; false when the
- * address does not have the alignment its use needs. */
+/* Device address and dtype of value v's view, as two program words; false
+ * when the address does not have the alignment its use needs or does not
+ * fit beside the dtype bits. */
 static bool m3_operand_words(const m3_session *session, uint32_t value,
                              bool scalar, uint32_t *low, uint32_t *high)
 {
     const m3_tensor_view *view = &session->views[value];
+    const m3_dtype dtype = view->metadata.dtype;
     uint64_t address =
         (uint64_t)(uintptr_t)m3_storage_device_data(view->storage) +
         (uint64_t)view->byte_offset;
+    uint64_t alignment = scalar ? (dtype == M3_DTYPE_F32 ? 4U : 2U)
+                                : (dtype == M3_DTYPE_F32 ? 16U : 8U);
 
-    if (address == 0U || (address & (scalar ? 3U : 15U)) != 0U) {
+    if (address == 0U || (address & (alignment - 1U)) != 0U ||
+        (address >> 62U) != 0U) {
         return false;
     }
     *low = (uint32_t)address | (scalar ? 1U : 0U);
-    *high = (uint32_t)(address >> 32U);
+    *high = (uint32_t)(address >> 32U) | ((uint32_t)dtype << 30U);
     return true;
 }
 
@@ -192,6 +197,12 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
         if (m3_op_binary_of(&session->commands[n]) != NULL) {
             fuse_nodes[n].left = (uint32_t)node->inputs[0];
             fuse_nodes[n].right = (uint32_t)node->inputs[1];
+            fuse_nodes[n].output = (uint32_t)node->outputs[0];
+            fuse_nodes[n].eligible =
+                session->providers[n] == M3_PROVIDER_HIP;
+        } else if (node->kind == M3_OP_CAST || node->kind == M3_OP_COPY) {
+            fuse_nodes[n].left = (uint32_t)node->inputs[0];
+            fuse_nodes[n].right = (uint32_t)node->inputs[0];
             fuse_nodes[n].output = (uint32_t)node->outputs[0];
             fuse_nodes[n].eligible =
                 session->providers[n] == M3_PROVIDER_HIP;

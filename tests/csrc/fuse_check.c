@@ -5,8 +5,9 @@
  *
  * A graph is executed twice on the host: node by node, and with every
  * group the planner forms replaced by its program, interpreted per element
- * exactly as the kernel does (registers R0-R3 and F0-F3, FETCH, OP, STORE,
- * m3_binary_f32_bits for each operation). Each value gets its own buffer;
+ * exactly as the kernel does (registers R0-R3 and F0-F3, FETCH, OP, ROUND,
+ * STORE; m3_binary_f32_bits for each operation, m3_round_through_bits for
+ * the rounding dtype, conversions on load and store). Each value gets its own buffer;
  * buffers the node-by-node run writes start as a sentinel NaN in the fused
  * run, so a missing STORE or a read of an unwritten register shows. Every
  * value that must reach memory (OUTPUT values, values read outside their
@@ -15,12 +16,14 @@
  *
  * Modes (one JSON line on stdout; exit status 1 on any mismatch):
  *   fuse_check random <graphs> <seed> [planted]
- *       Random graphs of ADD/SUB/MUL/DIV over F32 and F16 values with
- *       array, scalar and differently sized operands, OUTPUT and TEMPORARY
- *       roles, COPY nodes and nodes on another provider between them.
+ *       Random graphs of ADD/SUB/MUL/DIV, CAST and COPY over F32, F16 and
+ *       BF16 values with array, scalar and differently sized operands,
+ *       OUTPUT and TEMPORARY roles, and nodes on another provider between
+ *       them.
  *       `planted` corrupts each plan before it runs (the first STORE is
- *       turned into a store of another register, and the sources of
- *       every SUB/DIV are swapped): the comparison must then fail.
+ *       turned into a store of another register, the sources of every
+ *       SUB/DIV are swapped, and OPs lose their rounding dtype): the
+ *       comparison must then fail.
  *   fuse_check euler <steps>
  *       The Euler CFG graph of the flow solver, 6 nodes per step; reports
  *       the plan's shape and checks its result.
@@ -137,7 +140,10 @@ static uint32_t op_of(m3_op_kind kind)
                                : M3N_DIV;
 }
 
-/* One node over all its elements, as the unfused provider runs it. */
+/* One node over all its elements, as the unfused provider runs it: COPY
+ * and a CAST between equal dtypes copy the raw element
+ * (src/m3_op_execute_basic.c:11-36), CAST converts through F32 (:37-59),
+ * ADD/SUB/MUL/DIV compute in F32 and store in the output's dtype. */
 static void run_node(graph_t *g, size_t n)
 {
     const m3_fuse_node *node = &g->nodes[n];
@@ -147,7 +153,12 @@ static void run_node(graph_t *g, size_t n)
     for (e = 0U; e < out->element_count; ++e) {
         uint32_t result;
 
-        if (node->kind == M3_OP_COPY) {
+        if ((node->kind == M3_OP_COPY || node->kind == M3_OP_CAST) &&
+            g->values[node->left].dtype == out->dtype) {
+            g->data[node->output][e] = g->data[node->left][e];
+            continue;
+        }
+        if (node->kind == M3_OP_CAST) {
             result = load_f32(g, node->left, e);
         } else {
             result = m3_binary_f32_bits(op_of(node->kind),
@@ -201,9 +212,25 @@ static size_t check_words(const m3_fuse_plan *plan, const m3_fuse_group *gr,
             uint32_t right = (w >> 12U) & 15U;
             uint32_t scalar = (w >> 16U) & 0xffU;
 
-            bad += (w & 0xc0U) != 0U || (w >> 24U) != 0U || left > 8U ||
-                   right > 8U;
+            bad += (w & 0xc0U) != 0U || (w >> 26U) != 0U ||
+                   ((w >> 24U) & 3U) > M3N_BF16 || left > 8U || right > 8U;
             if (left == 8U || right == 8U) {
+                bad += scalar >= gr->operand_count ||
+                       !plan->operands[gr->operand_first + scalar].scalar;
+            } else {
+                bad += scalar != 0U;
+            }
+            pc += 1U;
+            break;
+        }
+        case M3_HIP_PROGRAM_ROUND: {
+            uint32_t source = (w >> 8U) & 15U;
+            uint32_t scalar = (w >> 16U) & 0xffU;
+
+            bad += (w & 0xccU) != 0U || (w & 0xf000U) != 0U ||
+                   (w >> 26U) != 0U || ((w >> 24U) & 3U) > M3N_BF16 ||
+                   source > 8U;
+            if (source == 8U) {
                 bad += scalar >= gr->operand_count ||
                        !plan->operands[gr->operand_first + scalar].scalar;
             } else {
@@ -259,11 +286,13 @@ static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
                     f_set[k] = true;
                 }
                 pc += 2U;
-            } else if ((w & 3U) == M3_HIP_PROGRAM_OP) {
+            } else if ((w & 3U) == M3_HIP_PROGRAM_OP ||
+                       (w & 3U) == M3_HIP_PROGRAM_ROUND) {
+                bool binary = (w & 3U) == M3_HIP_PROGRAM_OP;
                 uint32_t kinds[2] = {(w >> 8U) & 15U, (w >> 12U) & 15U};
-                uint32_t x[2];
+                uint32_t x[2] = {0U, 0U};
 
-                for (int k = 0; k < 2; ++k) {
+                for (int k = 0; k < (binary ? 2 : 1); ++k) {
                     if (kinds[k] < 4U) {
                         x[k] = r[kinds[k]];
                         unwritten += !r_set[kinds[k]];
@@ -275,14 +304,18 @@ static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
                             g, operands[(w >> 16U) & 0xffU].value, 0U);
                     }
                 }
-                r[(w >> 4U) & 3U] =
-                    m3_binary_f32_bits((w >> 2U) & 3U, x[0], x[1]);
+                r[(w >> 4U) & 3U] = m3_round_through_bits(
+                    binary ? m3_binary_f32_bits((w >> 2U) & 3U, x[0], x[1])
+                           : x[0],
+                    (w >> 24U) & 3U);
                 r_set[(w >> 4U) & 3U] = true;
                 pc += 1U;
             } else {
                 uint32_t src = (w >> 4U) & 3U;
+                uint32_t target = operands[(w >> 8U) & 0xffU].value;
 
-                g->data[operands[(w >> 8U) & 0xffU].value][e] = r[src];
+                g->data[target][e] = m3_store_from_f32_bits(
+                    r[src], (uint32_t)g->values[target].dtype);
                 unwritten += !r_set[src];
                 pc += 1U;
             }
@@ -291,8 +324,9 @@ static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
     return unwritten;
 }
 
-/* Corrupts a plan: the first STORE stores another register, and the
- * sources of every SUB and DIV are swapped. */
+/* Corrupts a plan: the first STORE stores another register, the sources
+ * of every SUB and DIV are swapped, and no OP rounds through its output's
+ * 16-bit dtype. */
 static void plant(m3_fuse_plan *plan)
 {
     bool first = true;
@@ -316,6 +350,9 @@ static void plant(m3_fuse_plan *plan)
 
                 code[pc] = (w & ~0xff00U) | (right << 8U) | (left << 12U);
             }
+            if ((w & 3U) == M3_HIP_PROGRAM_OP) {
+                code[pc] &= ~(3U << 24U); /* drop the rounding dtype */
+            }
             if ((w & 3U) == M3_HIP_PROGRAM_STORE && first) {
                 code[pc] = w ^ (1U << 4U);
                 first = false;
@@ -334,6 +371,9 @@ typedef struct {
     size_t mismatches;
     size_t structure;
     size_t unwritten;
+    size_t rounds;         /* ROUND instructions (fused CAST/COPY) */
+    size_t rounding_ops;   /* OP instructions with a 16-bit rounding */
+    size_t narrow_operands; /* F16/BF16 operands of programs */
 } stats_t;
 
 static void allocate_data(graph_t *g, uint32_t **data)
@@ -371,6 +411,8 @@ static void check_graph(graph_t *g, bool planted, stats_t *st)
 
             if (val->dtype == M3_DTYPE_F16) {
                 bits = m3_f32_to_f16_bits(bits);
+            } else if (val->dtype == M3_DTYPE_BF16) {
+                bits = m3_f32_to_bf16_bits(bits);
             }
             reference[v][e] = given ? bits : SENTINEL;
             fused[v][e] = reference[v][e];
@@ -397,7 +439,15 @@ static void check_graph(graph_t *g, bool planted, stats_t *st)
             uint32_t w = plan.code[gr->code_first + pc];
 
             st->stores += (w & 3U) == M3_HIP_PROGRAM_STORE;
+            st->rounds += (w & 3U) == M3_HIP_PROGRAM_ROUND;
+            st->rounding_ops += (w & 3U) == M3_HIP_PROGRAM_OP &&
+                                ((w >> 24U) & 3U) != 0U;
             pc += (w & 3U) == M3_HIP_PROGRAM_FETCH ? 2U : 1U;
+        }
+        for (size_t p = 0U; p < gr->operand_count; ++p) {
+            st->narrow_operands +=
+                g->values[plan.operands[gr->operand_first + p].value].dtype !=
+                M3_DTYPE_F32;
         }
         for (n = gr->first_node; n < gr->first_node + gr->node_count; ++n) {
             group_of[n] = gi;
@@ -476,13 +526,17 @@ static void random_graph(graph_t *g)
     (void)add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32, 1U);
     (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_F32, counts[2]);
     (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_F16, counts[0]);
+    (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_BF16, counts[0]);
+    (void)add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_BF16, 1U);
     for (size_t n = 0U; n < nodes; ++n) {
+        static const m3_dtype floats[3] = {M3_DTYPE_F32, M3_DTYPE_F16,
+                                           M3_DTYPE_BF16};
         uint32_t left = below((uint32_t)g->value_count);
         uint64_t lc = g->values[left].element_count;
         uint32_t right;
         uint64_t rc;
         m3_dtype dtype = M3_DTYPE_F32;
-        bool copy = below(100U) < 10U;
+        uint32_t unary = below(100U);
         m3_graph_value_role role =
             n + 1U == nodes || below(100U) < 15U ? M3_GRAPH_OUTPUT
                                                  : M3_GRAPH_TEMPORARY;
@@ -491,14 +545,20 @@ static void random_graph(graph_t *g)
             right = below((uint32_t)g->value_count);
             rc = g->values[right].element_count;
         } while (!(rc == lc || rc == 1U || lc == 1U));
-        if (g->values[left].dtype == M3_DTYPE_F16 ||
-            g->values[right].dtype == M3_DTYPE_F16) {
-            dtype = below(2U) ? M3_DTYPE_F16 : M3_DTYPE_F32;
+        if (g->values[left].dtype != M3_DTYPE_F32 ||
+            g->values[right].dtype != M3_DTYPE_F32 || below(100U) < 20U) {
+            dtype = floats[below(3U)];
         }
-        if (copy) {
+        if (unary < 8U) {
             uint32_t out = add_value(g, role, g->values[left].dtype, lc);
 
-            add_node(g, M3_OP_COPY, left, left, out, false);
+            add_node(g, M3_OP_COPY, left, left, out, below(2U) != 0U);
+            continue;
+        }
+        if (unary < 20U) {
+            uint32_t out = add_value(g, role, floats[below(3U)], lc);
+
+            add_node(g, M3_OP_CAST, left, left, out, below(100U) >= 5U);
             continue;
         }
         add_node(g, kinds[below(4U)], left, right,
@@ -553,10 +613,12 @@ static void print_stats(const char *mode, size_t graphs, const stats_t *st)
     printf("{\"mode\": \"%s\", \"graphs\": %zu, \"groups\": %zu, "
            "\"fused_nodes\": %zu, \"stores\": %zu, \"internal_values\": %zu, "
            "\"compared_values\": %zu, \"mismatches\": %zu, "
-           "\"structure_errors\": %zu, \"unwritten_reads\": %zu",
+           "\"structure_errors\": %zu, \"unwritten_reads\": %zu, "
+           "\"rounds\": %zu, \"rounding_ops\": %zu, "
+           "\"narrow_operands\": %zu",
            mode, graphs, st->groups, st->fused_nodes, st->stores,
            st->internal, st->compared, st->mismatches, st->structure,
-           st->unwritten);
+           st->unwritten, st->rounds, st->rounding_ops, st->narrow_operands);
 }
 
 int main(int argc, char **argv)

@@ -163,14 +163,56 @@ static uint32_t oracle_op1(uint32_t op, uint32_t a, uint32_t b)
     return values[2];
 }
 
-static const uint32_t *operand_address(const uint32_t *operands,
-                                       uint32_t index)
+static uint8_t *operand_address(const uint32_t *operands, uint32_t index)
 {
     uint64_t low = operands[2U * index];
-    uint64_t high = operands[2U * index + 1U];
+    uint64_t high = operands[2U * index + 1U] & 0x3fffffffU;
 
-    return (const uint32_t *)(uintptr_t)(((high << 32U) | low) &
-                                         ~(uint64_t)1U);
+    return (uint8_t *)(uintptr_t)(((high << 32U) | low) & ~(uint64_t)1U);
+}
+
+/* Element e of operand `index` as F32 bits, converted from its dtype (bits
+ * 30-31 of the high word) with the oracle's converters. */
+static uint32_t operand_load(const uint32_t *operands, uint32_t index,
+                             uint64_t e)
+{
+    const uint8_t *base = operand_address(operands, index);
+    uint32_t dtype = operands[2U * index + 1U] >> 30U;
+    uint16_t half;
+    uint32_t bits;
+
+    if (dtype == ORACLE_F32) {
+        memcpy(&bits, base + 4U * e, sizeof(bits));
+        return bits;
+    }
+    memcpy(&half, base + 2U * e, sizeof(half));
+    return dtype == ORACLE_F16 ? oracle_f16_to_f32(half)
+                               : oracle_bf16_to_f32(half);
+}
+
+static void operand_store(const uint32_t *operands, uint32_t index,
+                          uint64_t e, uint32_t bits)
+{
+    uint8_t *base = operand_address(operands, index);
+    uint32_t dtype = operands[2U * index + 1U] >> 30U;
+    uint16_t half;
+
+    if (dtype == ORACLE_F32) {
+        memcpy(base + 4U * e, &bits, sizeof(bits));
+        return;
+    }
+    half = dtype == ORACLE_F16 ? oracle_f32_to_f16(bits)
+                               : oracle_f32_to_bf16(bits);
+    memcpy(base + 2U * e, &half, sizeof(half));
+}
+
+/* F32 bits stored to `dtype` and loaded back. */
+static uint32_t round_through(uint32_t bits, uint32_t dtype)
+{
+    return dtype == ORACLE_F16    ? oracle_f16_to_f32(oracle_f32_to_f16(bits))
+           : dtype == ORACLE_BF16 ? oracle_bf16_to_f32(
+                                        oracle_f32_to_bf16(bits))
+                                  : bits;
 }
 
 /* Runs an elementwise program (layout in m3_hip.h) element by element. */
@@ -205,29 +247,30 @@ static int run_program(const m3_op_elementwise_program *program)
                 uint32_t k;
 
                 for (k = 0U; k < n; ++k) {
-                    f[k] = operand_address(
-                        operands, (code[pc + 1U] >> (8U * k)) & 0xffU)[e];
+                    f[k] = operand_load(
+                        operands, (code[pc + 1U] >> (8U * k)) & 0xffU, e);
                 }
                 pc += 2U;
-            } else if ((w & 3U) == 1U) { /* OP */
+            } else if ((w & 3U) == 1U || (w & 3U) == 3U) { /* OP, ROUND */
+                int binary = (w & 3U) == 1U;
                 uint32_t kinds[2] = {(w >> 8U) & 15U, (w >> 12U) & 15U};
-                uint32_t x[2];
+                uint32_t x[2] = {0U, 0U};
                 int k;
 
-                for (k = 0; k < 2; ++k) {
+                for (k = 0; k < (binary ? 2 : 1); ++k) {
                     x[k] = kinds[k] < 4U   ? r[kinds[k]]
                            : kinds[k] < 8U ? f[kinds[k] - 4U]
-                                           : operand_address(
+                                           : operand_load(
                                                  operands,
-                                                 (w >> 16U) & 0xffU)[0];
+                                                 (w >> 16U) & 0xffU, 0U);
                 }
-                r[(w >> 4U) & 3U] = oracle_op1((w >> 2U) & 3U, x[0], x[1]);
+                r[(w >> 4U) & 3U] = round_through(
+                    binary ? oracle_op1((w >> 2U) & 3U, x[0], x[1]) : x[0],
+                    (w >> 24U) & 3U);
                 pc += 1U;
             } else { /* STORE */
-                uint32_t *out = (uint32_t *)(uintptr_t)operand_address(
-                    operands, (w >> 8U) & 0xffU);
-
-                out[e] = r[(w >> 4U) & 3U];
+                operand_store(operands, (w >> 8U) & 0xffU, e,
+                              r[(w >> 4U) & 3U]);
                 pc += 1U;
             }
         }

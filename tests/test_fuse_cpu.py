@@ -4,7 +4,8 @@ host.
 
 Each planned graph runs twice on the host: node by node with the
 reference's per-element operation (load as F32, one F32 operation, round to
-the output dtype; src/m3_op_execute_basic.c:61-77), and with every fused
+the output dtype; src/m3_op_execute_basic.c:61-77; CAST through F32 and
+COPY as a raw copy, :11-59), and with every fused
 group replaced by its program interpreted the way the kernel runs it. Every
 value that has to reach memory must agree bit for bit, NaN payloads
 included. A plan with planted mistakes (a STORE of the wrong register, SUB
@@ -57,6 +58,10 @@ def test_random_plans_match_node_by_node():
         assert r["groups"] > 5000
         assert r["internal_values"] > 5000
         assert r["compared_values"] > 50000
+        # float CASTs, F32 COPYs and 16-bit values are fused too
+        assert r["rounds"] > 1000
+        assert r["rounding_ops"] > 1000
+        assert r["narrow_operands"] > 1000
 
 
 def test_planted_plan_mistakes_are_detected():

@@ -42,6 +42,9 @@ class environment:
                 os.environ[key] = value
 
 
+NUMPY_OF = {m3.F32: np.float32, m3.F16: np.uint16, m3.BF16: np.uint16}
+
+
 def run_session(build, fusion, generated=True):
     with environment(M3_HIP_FUSION="1" if fusion else "0",
                      M3_HIP_PROGRAM_JIT="1" if generated else "0"):
@@ -62,14 +65,16 @@ def _run(session, g, feeds, outputs):
     session.run()
     kernels = session.timing_read()
     session.timing_enable(False)
-    results = [session.read(vid, np.zeros(shape, np.float32))
-               for vid, shape in outputs]
+    results = [session.read(vid, np.zeros(entry[0], entry[1] if len(entry)
+                                          > 1 else np.float32))
+               for vid, *entry in outputs]
     # a second run on the same inputs gives the same bits
     session.run()
-    again = [session.read(vid, np.zeros(shape, np.float32))
-             for vid, shape in outputs]
+    again = [session.read(vid, np.zeros(entry[0], entry[1] if len(entry)
+                                        > 1 else np.float32))
+             for vid, *entry in outputs]
     for a, b in zip(results, again):
-        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
     session.free()
     return results, (plan.storage_slot_count, plan.allocated_bytes), kernels
 
@@ -149,6 +154,90 @@ def test_fused_equals_unfused(gpu, seed, shape, generated):
         assert kernels_on.get(ran, (0, 0.0))[0] >= 1
 
 
+def narrow(rng, shape, dtype):
+    """Random 16-bit patterns: values near 1, NaN payloads (signalling and
+    quiet), infinities, zeros and subnormals."""
+    data = specials(rng, shape)
+    if dtype == m3.BF16:
+        return (data.view(np.uint32) >> np.uint32(16)).astype(np.uint16)
+    half = data.astype(np.float16).view(np.uint16)
+    pick = rng.random(shape)
+    half[pick < 0.05] = rng.integers(0x7c01, 0x8000, shape)[pick < 0.05]
+    half[(pick >= 0.05) & (pick < 0.07)] = 0x0001
+    return half
+
+
+def mixed_graph(seed, shape, nodes=40):
+    """Random elementwise DAG over F32, F16 and BF16 values: binary nodes
+    with any float output dtype, CASTs between float dtypes, COPYs, scalar
+    operands (F32 and BF16), OUTPUT values read again."""
+    def build():
+        rng = np.random.default_rng(seed)
+        floats = [m3.F32, m3.F16, m3.BF16]
+        g = m3.Graph()
+        values, feeds, outputs = [], [], []
+        for dtype in (m3.F32, m3.F16, m3.BF16, m3.F32):
+            vid = g.add_value(m3.INPUT, dtype, shape)
+            feeds.append((vid, specials(rng, shape) if dtype == m3.F32
+                          else narrow(rng, shape, dtype)))
+            values.append((vid, shape, dtype))
+        for dtype in (m3.F32, m3.BF16):
+            vid = g.add_value(m3.CONSTANT, dtype, (1,))
+            constant = (rng.standard_normal(1) + 2.0).astype(np.float32)
+            g.set_constant(vid, constant if dtype == m3.F32 else
+                           (constant.view(np.uint32) >> np.uint32(16))
+                           .astype(np.uint16))
+            values.append((vid, (1,), dtype))
+        kinds = [m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV]
+        for n in range(nodes):
+            role = m3.OUTPUT if n == nodes - 1 or rng.random() < 0.2 \
+                else m3.TEMPORARY
+            a = values[rng.integers(len(values))]
+            pick = rng.random()
+            if pick < 0.1:
+                vid = g.add_value(role, a[2], a[1])
+                g.add_node(m3.OP_COPY, [a[0]], [vid])
+                entry = (vid, a[1], a[2])
+            elif pick < 0.3:
+                dtype = floats[rng.integers(3)]
+                vid = g.add_value(role, dtype, a[1])
+                g.add_node(m3.OP_CAST, [a[0]], [vid])
+                entry = (vid, a[1], dtype)
+            else:
+                b = values[rng.integers(len(values))]
+                out_shape = shape if shape in (a[1], b[1]) else (1,)
+                dtype = floats[rng.integers(3)]
+                vid = g.add_value(role, dtype, out_shape)
+                g.add_node(kinds[rng.integers(4)], [a[0], b[0]], [vid])
+                entry = (vid, out_shape, dtype)
+            values.append(entry)
+            if role == m3.OUTPUT:
+                outputs.append((entry[0], entry[1], NUMPY_OF[entry[2]]))
+        return g, feeds, outputs
+    return build
+
+
+@pytest.mark.parametrize("generated", [True, False])
+@pytest.mark.parametrize("seed,shape", [(0, (3, 5, 7)), (1, (2, 33, 129)),
+                                        (2, (4, 1000, 37)), (3, (1, 4099)),
+                                        (4, (1,))])
+def test_fused_mixed_dtypes_equal_unfused(gpu, seed, shape, generated):
+    """F16/BF16 loads, stores and scalars, rounding through the output
+    dtype and fused CASTs: every OUTPUT byte for byte equal to the per-node
+    kernels, NaN payloads included."""
+    print("fusion mixed graph seed", seed, "shape", shape, "generated",
+          generated, flush=True)
+    build = mixed_graph(4000 + seed, shape)
+    fused, plan_on, kernels_on = run_session(build, True, generated)
+    plain, plan_off, kernels_off = run_session(build, False)
+    assert plan_on == plan_off
+    for a, b in zip(fused, plain):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    ran = "m3_program" if generated else "m3_program_interpreted"
+    if shape != (1,):
+        assert kernels_on.get(ran, (0, 0.0))[0] >= 1
+
+
 def euler_graph(steps, shape):
     def build():
         rng = m3.rng_new(0, 0)
@@ -215,44 +304,83 @@ def test_euler_graph_is_one_program(gpu, generated):
 def test_program_words_are_checked_before_launch(gpu):
     """m3_hip_launch_program rejects malformed words on the host (nothing
     is launched): bad magic, operand index out of range, a scalar fetched,
-    unknown opcode, and a word count that does not match the header."""
+    a rounding dtype out of range in OP and in ROUND, an operand dtype out
+    of range, a misaligned 16-bit array, and a word count that does not
+    match the header. Every address in the words, and the device copy of
+    the words, is real device memory, so a case the check missed would
+    still only touch memory of this test; the valid words run once."""
     _, lib = m3.load()
+    vp, sz, cp = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_char_p
+    lib.m3_hip_arena_reserve.argtypes = [vp, sz, ctypes.POINTER(vp), cp, sz]
+    lib.m3_hip_arena_release.argtypes = [vp, vp]
+    lib.m3_hip_fill_zero.argtypes = [vp, vp, sz, cp, sz]
+    lib.m3_hip_copy_h2d.argtypes = [vp, vp, vp, sz, cp, sz]
     handle = ctypes.c_void_p()
+    base = ctypes.c_void_p()
     msg = ctypes.create_string_buffer(256)
     assert lib.m3_hip_device_open(0, ctypes.byref(handle), msg, 256) == 0
     try:
+        assert lib.m3_hip_arena_reserve(handle, 65536, ctypes.byref(base),
+                                        msg, 256) == 0, msg.value
+        assert lib.m3_hip_fill_zero(handle, base, 65536, msg, 256) == 0
+        array = base.value + 4096      # 8 F32 elements
+        scalar = base.value + 8192     # one F32
+        device_words = ctypes.c_void_p(base.value + 16384)
+
         def words(operands, code, count=8):
             header = [0x4d335031, len(operands) // 2, len(code),
                       count, 0, 0, 0, 0]
             return np.array(header + operands + code, np.uint32)
 
-        # one array operand at a 16-byte aligned fake address, one scalar
-        operands = [0x10000, 0, 0x20001, 0]
+        def address(at, flags=0, dtype=0):
+            return [(at & 0xffffffff) | flags, (at >> 32) | (dtype << 30)]
+
+        # R0 = F0 * scalar, stored back to the array
+        operands = address(array) + address(scalar, flags=1)
         good = words(operands, [0x00000000 | (0 << 2), 0x00,
-                                0x1 | (0 << 2) | (0 << 4) | (4 << 8) |
+                                0x1 | (1 << 2) | (0 << 4) | (4 << 8) |
                                 (8 << 12) | (1 << 16),
                                 0x2 | (0 << 4) | (0 << 8)])
+        assert lib.m3_hip_copy_h2d(
+            handle, device_words, good.ctypes.data_as(ctypes.c_void_p),
+            good.nbytes, msg, 256) == 0
         bad = []
         b = good.copy()
         b[0] = 0
         bad.append(b)
         b = good.copy()
-        b[9 + 4] = 0x05  # FETCH operand 5 of 2
+        b[13] = 0x05  # FETCH operand 5 of 2
         bad.append(b)
         b = good.copy()
-        b[9 + 4] = 0x01  # FETCH the scalar
+        b[13] = 0x01  # FETCH the scalar
         bad.append(b)
         b = good.copy()
-        b[-1] = 0x3  # opcode 3
+        b[14] |= 3 << 24  # OP rounding dtype 3
         bad.append(b)
-        for w in bad:
+        b = good.copy()
+        b[15] = 0x3 | (3 << 24)  # ROUND with dtype 3
+        bad.append(b)
+        b = good.copy()
+        b[9] |= 3 << 30  # operand dtype 3
+        bad.append(b)
+        b = good.copy()
+        b[8:10] = address(array + 4, dtype=1)  # F16 array not 8-aligned
+        bad.append(b)
+        for index, w in enumerate(bad):
             code = lib.m3_hip_launch_program(
                 handle, w.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
-                ctypes.c_void_p(0x1000), w.size, msg, 256)
-            assert code == 1, msg.value  # M3_HIP_INVALID
+                device_words, w.size, msg, 256)
+            assert code == 1, (index, msg.value)  # M3_HIP_INVALID
         code = lib.m3_hip_launch_program(
             handle, good.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
-            ctypes.c_void_p(0x1000), good.size - 1, msg, 256)
+            device_words, good.size - 1, msg, 256)
         assert code == 1
+        code = lib.m3_hip_launch_program(
+            handle, good.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+            device_words, good.size, msg, 256)
+        assert code == 0, msg.value
+        assert lib.m3_hip_synchronize(handle, msg, 256) == 0, msg.value
     finally:
+        if base.value:
+            lib.m3_hip_arena_release(handle, base)
         lib.m3_hip_device_close(handle)

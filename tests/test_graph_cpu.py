@@ -395,8 +395,9 @@ def _session_outputs(graph_builder, fusion, fake):
     for vid, data in feeds:
         session.write(vid, data)
     session.run()
-    results = [session.read(vid, np.zeros(shape, np.float32))
-               for vid, shape in outputs]
+    results = [session.read(vid, np.zeros(entry[0], entry[1] if len(entry)
+                                          > 1 else np.float32))
+               for vid, *entry in outputs]
     programs = fake.oracle_backend_programs()
     kinds, _ = log_of(fake)
     session.free()
@@ -453,6 +454,102 @@ def _random_chain_graph(seed):
                 outputs.append((vid, out_shape))
         return g, feeds, outputs
     return build
+
+
+_NUMPY_OF = {m3.F32: np.float32, m3.F16: np.uint16, m3.BF16: np.uint16}
+
+
+def _narrow(rng, shape, dtype):
+    """Random 16-bit patterns of `dtype`: normal values near 1 with NaN
+    payloads (signalling and quiet), infinities, zeros and subnormals."""
+    data = _specials(rng, shape)
+    bits = data.view(np.uint32)
+    if dtype == m3.BF16:
+        return (bits >> np.uint32(16)).astype(np.uint16)
+    half = data.astype(np.float16).view(np.uint16)
+    pick = rng.random(shape)
+    half[pick < 0.05] = rng.integers(0x7c01, 0x8000, shape)[pick < 0.05]
+    half[(pick >= 0.05) & (pick < 0.07)] = 0x0001
+    return half
+
+
+def _mixed_chain_graph(seed):
+    """Elementwise DAGs over F32, F16 and BF16 values: binary nodes with
+    any float output dtype, CASTs between float dtypes, COPYs, scalar
+    operands, OUTPUT values read again."""
+    def build():
+        rng = np.random.default_rng(seed)
+        shape = (3, 5, 7)
+        floats = [m3.F32, m3.F16, m3.BF16]
+        g = m3.Graph()
+        values = []
+        feeds = []
+        outputs = []
+        for dtype in (m3.F32, m3.F16, m3.BF16, m3.F32):
+            vid = g.add_value(m3.INPUT, dtype, shape)
+            feeds.append((vid, _specials(rng, shape) if dtype == m3.F32
+                          else _narrow(rng, shape, dtype)))
+            values.append((vid, shape, dtype))
+        for dtype in (m3.F32, m3.BF16):
+            vid = g.add_value(m3.CONSTANT, dtype, (1,))
+            constant = (rng.standard_normal(1) + 2.0).astype(np.float32)
+            g.set_constant(vid, constant if dtype == m3.F32 else
+                           (constant.view(np.uint32) >> np.uint32(16))
+                           .astype(np.uint16))
+            values.append((vid, (1,), dtype))
+        kinds = [m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV]
+        for n in range(40):
+            role = m3.OUTPUT if n == 39 or rng.random() < 0.2 \
+                else m3.TEMPORARY
+            a = values[rng.integers(len(values))]
+            pick = rng.random()
+            if pick < 0.1:
+                vid = g.add_value(role, a[2], a[1])
+                g.add_node(m3.OP_COPY, [a[0]], [vid])
+                entry = (vid, a[1], a[2])
+            elif pick < 0.3:
+                dtype = floats[rng.integers(3)]
+                vid = g.add_value(role, dtype, a[1])
+                g.add_node(m3.OP_CAST, [a[0]], [vid])
+                entry = (vid, a[1], dtype)
+            else:
+                b = values[rng.integers(len(values))]
+                out_shape = shape if shape in (a[1], b[1]) else (1,)
+                dtype = floats[rng.integers(3)]
+                vid = g.add_value(role, dtype, out_shape)
+                g.add_node(kinds[rng.integers(4)], [a[0], b[0]], [vid])
+                entry = (vid, out_shape, dtype)
+            values.append(entry)
+            if role == m3.OUTPUT:
+                outputs.append((entry[0], entry[1], _NUMPY_OF[entry[2]]))
+        return g, feeds, outputs
+    return build
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_fused_mixed_dtype_runs_equal_unfused_runs(fake, seed):
+    """F16/BF16 values, CAST and COPY inside programs: every OUTPUT is
+    identical byte for byte with and without fusion."""
+    build = _mixed_chain_graph(3000 + seed)
+    fused, plan_on, programs_on, kinds_on = _session_outputs(build, True,
+                                                             fake)
+    plain, plan_off, programs_off, kinds_off = _session_outputs(build, False,
+                                                                fake)
+    assert plan_on == plan_off
+    assert programs_off == 0
+    assert kinds_on == kinds_off
+    for a, b in zip(fused, plain):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def test_mixed_dtype_graphs_fuse_casts(fake):
+    """The planner does fuse CAST nodes and 16-bit values (the backend logs
+    the constituents of every program it runs)."""
+    programs = 0
+    for seed in range(8):
+        build = _mixed_chain_graph(3000 + seed)
+        programs += _session_outputs(build, True, fake)[2]
+    assert programs >= 8
 
 
 @pytest.mark.parametrize("seed", range(8))
