@@ -144,7 +144,7 @@ def test_random_graphs_reuse_slots_on_device(gpu, seed):
 
 
 def test_mul_broadcast_config(gpu):
-    """C1 at reduced size: x ~ U(-1,1) times a constant c ~ N(0,1)
+    """Broadcast MUL x[8,1024,1536] * c[1536] at reduced size: x ~ U(-1,1) times a constant c ~ N(0,1)
     broadcast over the last axis."""
     shape = (2, 64, 1536)
     x = m3.rng_fill("uniform", int(np.prod(shape)), seed=0, a=-1.0,
@@ -171,7 +171,7 @@ def _oracle_unary(kind, src, src_dtype, dst_shape, dst_dtype, np_out):
 
 
 def test_softmax_causal_config(gpu):
-    """C2 at reduced size: causal logits ~ N(0,3), strict upper triangle
+    """Causal softmax of [16,1024,1024] scores at reduced size: logits ~ N(0,3), strict upper triangle
     -inf, bit-exact with the oracle (the C library's expf)."""
     n = 256
     s = m3.rng_fill("normal", 3 * n * n, seed=0, a=3.0).reshape(3, n, n)
@@ -220,7 +220,7 @@ def test_softmax_nan_input_is_rejected_until_rewritten(gpu):
 @pytest.mark.parametrize("pair", [(m3.F32, m3.F16), (m3.F16, m3.F32),
                                   (m3.F32, m3.BF16), (m3.BF16, m3.F32)])
 def test_cast_config(gpu, pair):
-    """C3 at reduced size: normals ~ N(0, 1e3) with 5% specials (subnormal,
+    """The F32<->F16/BF16 casts of [4096,4096] at reduced size: normals ~ N(0, 1e3) with 5% specials (subnormal,
     signed zeros, infinities, NaN payloads), bit-exact."""
     src_dtype, dst_dtype = pair
     n = 256 * 256
@@ -251,7 +251,7 @@ def test_cast_config(gpu, pair):
 
 
 def test_snake_config(gpu):
-    """C4 at reduced size: x ~ N(0,1), alpha ~ U(0.1, 2) per channel."""
+    """Snake1d of x[2,1536,65536] at reduced size: x ~ N(0,1), alpha ~ U(0.1, 2) per channel."""
     shape = (2, 48, 4096)
     x = m3.rng_fill("normal", int(np.prod(shape)), seed=0,
                     a=1.0).reshape(shape)
@@ -275,7 +275,7 @@ def test_snake_config(gpu):
 
 
 def test_euler_cfg_graph(gpu):
-    """C5 at reduced size: 4 Euler CFG steps in the reference's op order
+    """The 30-step Euler CFG graph at reduced size: 4 steps in the reference's op order
     (src/m3_flow_solver_math.c:36-135), constants per step, temporaries
     reusing slots; checked against the same float32 operations in numpy."""
     shape = (2, 64, 96)
