@@ -144,8 +144,8 @@ def test_random_graphs_reuse_slots_on_device(gpu, seed):
 
 
 def test_mul_broadcast_config(gpu):
-    """Broadcast MUL x[8,1024,1536] * c[1536] at reduced size: x ~ U(-1,1) times a constant c ~ N(0,1)
-    broadcast over the last axis."""
+    """Broadcast MUL x[8,1024,1536] * c[1536] at reduced size: x ~ U(-1,1)
+    times a constant c ~ N(0,1) broadcast over the last axis."""
     shape = (2, 64, 1536)
     x = m3.rng_fill("uniform", int(np.prod(shape)), seed=0, a=-1.0,
                     b=1.0).reshape(shape)
@@ -171,8 +171,9 @@ def _oracle_unary(kind, src, src_dtype, dst_shape, dst_dtype, np_out):
 
 
 def test_softmax_causal_config(gpu):
-    """Causal softmax of [16,1024,1024] scores at reduced size: logits ~ N(0,3), strict upper triangle
-    -inf, bit-exact with the oracle (the C library's expf)."""
+    """Causal softmax of [16,1024,1024] scores at reduced size: logits ~
+    N(0,3), strict upper triangle -inf, bit-exact with the oracle (the C
+    library's expf)."""
     n = 256
     s = m3.rng_fill("normal", 3 * n * n, seed=0, a=3.0).reshape(3, n, n)
     s[:, np.triu(np.ones((n, n), bool), k=1)] = -np.inf
@@ -220,8 +221,9 @@ def test_softmax_nan_input_is_rejected_until_rewritten(gpu):
 @pytest.mark.parametrize("pair", [(m3.F32, m3.F16), (m3.F16, m3.F32),
                                   (m3.F32, m3.BF16), (m3.BF16, m3.F32)])
 def test_cast_config(gpu, pair):
-    """The F32<->F16/BF16 casts of [4096,4096] at reduced size: normals ~ N(0, 1e3) with 5% specials (subnormal,
-    signed zeros, infinities, NaN payloads), bit-exact."""
+    """The F32<->F16/BF16 casts of [4096,4096] at reduced size: normals ~ N(0,
+    1e3) with 5% specials (subnormal, signed zeros, infinities, NaN payloads),
+    bit-exact."""
     src_dtype, dst_dtype = pair
     n = 256 * 256
     rng = np.random.default_rng(7)
@@ -251,7 +253,8 @@ def test_cast_config(gpu, pair):
 
 
 def test_snake_config(gpu):
-    """Snake1d of x[2,1536,65536] at reduced size: x ~ N(0,1), alpha ~ U(0.1, 2) per channel."""
+    """Snake1d of x[2,1536,65536] at reduced size: x ~ N(0,1), alpha ~ U(0.1,
+    2) per channel."""
     shape = (2, 48, 4096)
     x = m3.rng_fill("normal", int(np.prod(shape)), seed=0,
                     a=1.0).reshape(shape)
@@ -275,9 +278,10 @@ def test_snake_config(gpu):
 
 
 def test_euler_cfg_graph(gpu):
-    """The 30-step Euler CFG graph at reduced size: 4 steps in the reference's op order
-    (src/m3_flow_solver_math.c:36-135), constants per step, temporaries
-    reusing slots; checked against the same float32 operations in numpy."""
+    """The 30-step Euler CFG graph at reduced size: 4 steps in the reference's
+    op order (src/m3_flow_solver_math.c:36-135), constants per step,
+    temporaries reusing slots; checked against the same float32 operations in
+    numpy."""
     shape = (2, 64, 96)
     count = int(np.prod(shape))
     steps = 4
