@@ -45,6 +45,8 @@
  *                                   src/m3_op_data_preflight.c:8-64)
  *   m3_hip_synchronize           <- commit + waitUntilCompleted
  *                                   (src/m3_backend_metal.m:210-216)
+ *   m3_hip_prepare_program       no counterpart: compiles a program's
+ *                                   kernel ahead of its first launch
  *   m3_hip_launch_program        no counterpart: runs a run of ADD/SUB/
  *                                   MUL/DIV commands (per-element semantics
  *                                   of src/m3_op_execute_basic.c:61-77) that
@@ -238,6 +240,15 @@ typedef enum {
     M3_HIP_PROGRAM_ROUND = 3
 } m3_hip_program_opcode;
 
+/* Checks the words like m3_hip_launch_program and compiles the program's
+ * generated kernel into the device's cache without launching anything, so
+ * that the first launch does not pay for the compilation (session
+ * creation calls it for every program). Returns M3_HIP_OK also when
+ * runtime compilation is off or fails: the launch then runs the
+ * interpreter. */
+int m3_hip_prepare_program(m3_hip_device *device, const uint32_t *words,
+                           size_t word_count, char *message,
+                           size_t capacity);
 int m3_hip_launch_program(m3_hip_device *device, const uint32_t *words,
                           const void *device_words, size_t word_count,
                           char *message, size_t capacity);

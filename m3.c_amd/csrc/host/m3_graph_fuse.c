@@ -151,6 +151,26 @@ static void m3_runs_fused(m3_session *session, const m3_fuse_plan *plan,
     session->run_count = out;
 }
 
+/* Compiles every program's kernel now, so that the session's first run
+ * does not (a failure only leaves that program to the interpreter). */
+static void m3_prepare_programs(m3_session *session,
+                                const m3_fuse_plan *plan,
+                                const size_t *offsets)
+{
+    m3_hip_device *device = m3_backend_hip_device(session->backend);
+    size_t gi;
+
+    for (gi = 0U; device != NULL && gi < plan->group_count; ++gi) {
+        const m3_fuse_group *group = &plan->groups[gi];
+
+        (void)m3_hip_prepare_program(
+            device, session->program_words + offsets[gi],
+            M3_HIP_PROGRAM_HEADER_WORDS + 2U * group->operand_count +
+                group->code_count,
+            NULL, 0U);
+    }
+}
+
 m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
                                m3_error *error)
 {
@@ -247,6 +267,7 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
     }
     if (status == M3_STATUS_OK) {
         m3_runs_fused(session, &plan, offsets);
+        m3_prepare_programs(session, &plan, offsets);
     }
     free(offsets);
     m3_fuse_plan_free(&plan);
