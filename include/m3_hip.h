@@ -200,20 +200,26 @@ int m3_hip_launch_gated_silu(m3_hip_device *device, const m3_hip_view *gate,
  *   [1] P, operand count (at most M3_HIP_PROGRAM_MAX_OPERANDS)
  *   [2] I, instruction word count (at most M3_HIP_PROGRAM_MAX_WORDS)
  *   [3] count, low 32 bits     [4] count, high 32 bits
- *   [5..7] zero
+ *   [5] K, number of periodic operands (at most P)
+ *   [6..7] zero
  *   [8 .. 8+2P) operand p: device address, low word then high word. Bits
  *       30-31 of the high word: the element dtype (M3_HIP_F32, M3_HIP_F16
  *       or M3_HIP_BF16). Bit 0 of the low word set: a scalar, one element
  *       read by every element (aligned to its size). Clear: an array of
  *       `count` elements (16-byte aligned for F32, 8-byte for 16-bit),
- *       element e at address + e * size.
- *   [8+2P .. 8+2P+I) instructions.
+ *       element e at address + e * size, unless the operand is periodic.
+ *   [8+2P .. 8+2P+2K) periodic operands: pairs (operand index, period
+ *       M). Element e of that array operand is at index e mod M: a
+ *       trailing-axis broadcast of an M-element tensor. M is a multiple of
+ *       4 that divides `count` (so every group of 4 elements lies within
+ *       one period); operand indices increase strictly.
+ *   [8+2P+2K .. 8+2P+2K+I) instructions.
  * Registers per element: values R0..R3 and fetched operands F0..F3.
  * Instructions (bits 0-1 opcode):
  *   FETCH (two words): bits 2-3 n-1; the second word holds operand
- *       indices f0..f{n-1} in its bytes 0..n-1. Loads array operand fk,
- *       converted to F32, into Fk for k < n; all n loads are issued
- *       together.
+ *       indices f0..f{n-1} in its bytes 0..n-1. Loads array (or periodic)
+ *       operand fk, converted to F32, into Fk for k < n; all n loads are
+ *       issued together.
  *   OP: bits 2-3 the m3_hip_binary_op; bits 4-5 destination R; bits 8-11
  *       left source, bits 12-15 right source (0-3: R0-R3, 4-7: F0-F3,
  *       8: the scalar operand in bits 16-23); bits 24-25 a rounding dtype.
@@ -223,8 +229,8 @@ int m3_hip_launch_gated_silu(m3_hip_device *device, const m3_hip_view *gate,
  *   ROUND: bits 4-5 destination R; bits 8-11 source (as OP's left, scalar
  *       index in bits 16-23); bits 24-25 the dtype. dst = source rounded
  *       through the dtype (a CAST; F32 makes it a move).
- *   STORE: bits 4-5 source R; bits 8-15 array operand; writes the value
- *       converted to the operand's dtype.
+ *   STORE: bits 4-5 source R; bits 8-15 array operand (not periodic);
+ *       writes the value converted to the operand's dtype.
  * m3_hip_launch_program checks the words on the host (magic, counts,
  * indices, operand kinds, dtypes and alignment) before launching;
  * device_words must hold the same words in device memory. */

@@ -5,7 +5,9 @@
  * this header and m3_numeric.h as in-memory headers).
  *
  * Element e of an array operand of dtype D (F32, F16 or BF16, bits 30-31
- * of its high address word) is at its address + e * size(D); a lane
+ * of its high address word) is at its address + e * size(D), or at
+ * index e mod M for a periodic operand of period M (a multiple of 4, so
+ * the four elements of a group are consecutive there too); a lane
  * handles the four elements 4g..4g+3 and holds them as F32. The last,
  * partial group reads and writes only the elements below `count`. Loads
  * convert to F32 and stores from F32 with the converters of CAST; an
@@ -73,19 +75,23 @@ __device__ __forceinline__ m3_program_f32x4 m3_program_splat(float v)
     return r;
 }
 
+/* Loads elements 4g..4g+3 (those below `count`) of array operand `index`;
+ * `period` is its period, or 0 when it is not periodic. */
 template <bool FULL, unsigned int D>
 __device__ __forceinline__ m3_program_f32x4
 m3_program_load(const unsigned int *operands, unsigned int index,
-                unsigned long long g, unsigned long long count)
+                unsigned long long g, unsigned long long count,
+                unsigned long long period)
 {
     const unsigned long long first = 4ULL * g;
+    const unsigned long long at = period != 0ULL ? first % period : first;
     m3_program_f32x4 v = {0.0F, 0.0F, 0.0F, 0.0F};
 
     if (D == M3N_F32) {
         const m3_program_global_f32 *p =
             (const m3_program_global_f32 *)(unsigned long long)
                 m3_program_address(operands, index) +
-            first;
+            at;
 
         if (FULL) {
             return *(const m3_program_global_f32x4 *)p;
@@ -105,7 +111,7 @@ m3_program_load(const unsigned int *operands, unsigned int index,
     const m3_program_global_u16 *p =
         (const m3_program_global_u16 *)(unsigned long long)
             m3_program_address(operands, index) +
-        first;
+        at;
     unsigned int h[4] = {0U, 0U, 0U, 0U};
 
     if (FULL) {

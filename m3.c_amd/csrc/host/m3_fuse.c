@@ -71,6 +71,16 @@ static bool m3_fuse_unary(m3_op_kind kind)
     return kind == M3_OP_CAST || kind == M3_OP_COPY;
 }
 
+/* An operand of `element_count` elements read periodically by a group of
+ * `count`: every group of four elements lies within one period, and the
+ * period fits its program word. */
+static bool m3_fuse_periodic(uint64_t element_count, uint64_t count)
+{
+    return element_count > 1U && element_count < count &&
+           element_count <= UINT32_MAX && element_count % 4U == 0U &&
+           count % element_count == 0U;
+}
+
 static bool m3_fuse_candidate(const m3_fuse_graph *g, size_t n)
 {
     const m3_fuse_node *node = &g->nodes[n];
@@ -99,10 +109,14 @@ static bool m3_fuse_candidate(const m3_fuse_graph *g, size_t n)
     }
     for (k = 0U; k < 2U; ++k) {
         const m3_fuse_value *value = &g->values[operands[k]];
+        const bool trailing =
+            k == 0U ? node->left_trailing : node->right_trailing;
 
         if (!m3_fuse_float(value->dtype) ||
             (value->element_count != output->element_count &&
-             value->element_count != 1U)) {
+             value->element_count != 1U &&
+             !(trailing && m3_fuse_periodic(value->element_count,
+                                            output->element_count)))) {
             return false;
         }
     }
@@ -227,12 +241,16 @@ static void m3_fuse_emit(m3_fuse_writer *w, uint32_t word)
     plan->code[plan->code_count++] = word;
 }
 
-/* Index of (value, scalar) among the group's operands, added if new. */
-static uint32_t m3_fuse_operand_index(m3_fuse_writer *w,
+/* Index of (value, scalar) among the group's operands, added if new. An
+ * array with fewer elements than the group is periodic (the candidate
+ * rule admits no other). */
+static uint32_t m3_fuse_operand_index(const m3_fuse_graph *g,
+                                      m3_fuse_writer *w,
                                       const m3_fuse_group *group,
                                       uint32_t value, bool scalar)
 {
     m3_fuse_plan *plan = w->plan;
+    const uint64_t element_count = g->values[value].element_count;
     size_t i;
 
     for (i = group->operand_first; i < plan->operand_count; ++i) {
@@ -249,6 +267,9 @@ static uint32_t m3_fuse_operand_index(m3_fuse_writer *w,
     }
     plan->operands[plan->operand_count].value = value;
     plan->operands[plan->operand_count].scalar = scalar;
+    plan->operands[plan->operand_count].period =
+        !scalar && element_count != group->element_count ? element_count
+                                                          : 0U;
     plan->operand_count += 1U;
     return (uint32_t)(i - group->operand_first);
 }
@@ -366,7 +387,7 @@ static void m3_fuse_emit_group(const m3_fuse_graph *g, m3_fuse_writer *w,
                 }
             }
             for (m = 0U; m < batch_size; ++m) {
-                list |= m3_fuse_operand_index(w, &group, batch[m], false)
+                list |= m3_fuse_operand_index(g, w, &group, batch[m], false)
                         << (8U * m);
             }
             m3_fuse_emit(w, (uint32_t)M3_HIP_PROGRAM_FETCH |
@@ -379,7 +400,7 @@ static void m3_fuse_emit_group(const m3_fuse_graph *g, m3_fuse_writer *w,
             if (m3_fuse_in_group(g, value, first, n)) {
                 sources[k] = m3_fuse_holder_of(&r, value);
             } else if (m3_fuse_scalar(g, value, group.element_count)) {
-                scalar = m3_fuse_operand_index(w, &group, value, true);
+                scalar = m3_fuse_operand_index(g, w, &group, value, true);
                 sources[k] = M3_FUSE_SCALAR_SOURCE;
             } else {
                 (void)m3_fuse_batch_has(batch, batch_size, value, &slot);
@@ -409,7 +430,7 @@ static void m3_fuse_emit_group(const m3_fuse_graph *g, m3_fuse_writer *w,
              g->last_use[node->output] >= end)) {
             m3_fuse_emit(w, (uint32_t)M3_HIP_PROGRAM_STORE |
                                 (destination << 4U) |
-                                (m3_fuse_operand_index(w, &group,
+                                (m3_fuse_operand_index(g, w, &group,
                                                        node->output, false)
                                  << 8U));
         }
@@ -418,6 +439,10 @@ static void m3_fuse_emit_group(const m3_fuse_graph *g, m3_fuse_writer *w,
         return;
     }
     group.operand_count = plan->operand_count - group.operand_first;
+    for (i = 0U; i < group.operand_count; ++i) {
+        group.period_count +=
+            plan->operands[group.operand_first + i].period != 0U ? 1U : 0U;
+    }
     group.code_count = plan->code_count - group.code_first;
     if (!m3_fuse_grow((void **)&plan->groups, &w->group_capacity,
                       plan->group_count + 1U, sizeof(*plan->groups))) {

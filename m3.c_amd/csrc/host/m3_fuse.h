@@ -13,8 +13,12 @@
  *   - a node may join a group when it is eligible (its provider executes
  *     programs) and is either ADD/SUB/MUL/DIV whose operands and output
  *     are F32, F16 or BF16 and whose operands have the output's element
- *     count (an array read at the same flat index) or one element (a
- *     scalar read by every element), or a CAST between two of those
+ *     count (an array read at the same flat index), one element (a
+ *     scalar read by every element) or, when the node marks the operand
+ *     trailing, M elements with M a multiple of 4 that divides the
+ *     output's count (a periodic operand: element e reads e mod M, the
+ *     right-aligned broadcast of a tensor whose shape, leading ones
+ *     removed, is the output's trailing dimensions), or a CAST between two of those
  *     dtypes, or a COPY of F32, described with right == left and an
  *     input of the output's element count;
  *   - a group is a run of consecutive such nodes with the same element
@@ -45,19 +49,26 @@ typedef struct {
     uint64_t element_count;
 } m3_fuse_value;
 
+/* left_trailing / right_trailing: the operand's shape, leading ones
+ * removed, equals the output's trailing dimensions, so a smaller operand
+ * is a right-aligned broadcast read at e mod its element count. */
 typedef struct {
     m3_op_kind kind;
     uint32_t left;
     uint32_t right;
     uint32_t output;
     bool eligible;
+    bool left_trailing;
+    bool right_trailing;
 } m3_fuse_node;
 
-/* An operand of a group's program: value index and whether it is read as
- * a scalar. Operand i of the group is entry operand_first + i. */
+/* An operand of a group's program: value index, whether it is read as a
+ * scalar, and its period (0 unless it is a periodic array). Operand i of
+ * the group is entry operand_first + i. */
 typedef struct {
     uint32_t value;
     bool scalar;
+    uint64_t period;
 } m3_fuse_operand;
 
 typedef struct {
@@ -66,6 +77,7 @@ typedef struct {
     uint64_t element_count;
     size_t operand_first;
     size_t operand_count;
+    size_t period_count; /* operands with a period */
     size_t code_first;
     size_t code_count;
 } m3_fuse_group;

@@ -72,6 +72,41 @@ static bool m3_operand_words(const m3_session *session, uint32_t value,
     return true;
 }
 
+/* Words of a group's program: header, operand table, period table and
+ * instructions. */
+static size_t m3_program_word_count(const m3_fuse_group *group)
+{
+    return M3_HIP_PROGRAM_HEADER_WORDS + 2U * group->operand_count +
+           2U * group->period_count + group->code_count;
+}
+
+/* True when the operand's shape, leading ones removed, is the output's
+ * trailing dimensions: under the right-aligned broadcast of the binary
+ * operations, output element e then reads operand element e mod its
+ * element count. */
+static bool m3_trailing_broadcast(const m3_tensor_metadata *operand,
+                                  const m3_tensor_metadata *output)
+{
+    size_t first = 0U;
+    size_t kept;
+    size_t i;
+
+    while (first < operand->rank && operand->shape[first] == 1U) {
+        first += 1U;
+    }
+    kept = operand->rank - first;
+    if (kept > output->rank) {
+        return false;
+    }
+    for (i = 0U; i < kept; ++i) {
+        if (operand->shape[first + i] !=
+            output->shape[output->rank - kept + i]) {
+            return false;
+        }
+    }
+    return true;
+}
+
 /* Writes the programs of all groups into session->program_words; false
  * when an operand address is unusable (the session then runs unfused). */
 static bool m3_write_programs(m3_session *session, const m3_fuse_plan *plan,
@@ -83,6 +118,8 @@ static bool m3_write_programs(m3_session *session, const m3_fuse_plan *plan,
     for (gi = 0U; gi < plan->group_count; ++gi) {
         const m3_fuse_group *group = &plan->groups[gi];
         uint32_t *words = session->program_words + at;
+        uint32_t *periods = words + M3_HIP_PROGRAM_HEADER_WORDS +
+                            2U * group->operand_count;
         size_t p;
 
         offsets[gi] = at;
@@ -92,6 +129,7 @@ static bool m3_write_programs(m3_session *session, const m3_fuse_plan *plan,
         words[2] = (uint32_t)group->code_count;
         words[3] = (uint32_t)group->element_count;
         words[4] = (uint32_t)(group->element_count >> 32U);
+        words[5] = (uint32_t)group->period_count;
         for (p = 0U; p < group->operand_count; ++p) {
             const m3_fuse_operand *operand =
                 &plan->operands[group->operand_first + p];
@@ -102,13 +140,15 @@ static bool m3_write_programs(m3_session *session, const m3_fuse_plan *plan,
                     &words[M3_HIP_PROGRAM_HEADER_WORDS + 2U * p + 1U])) {
                 return false;
             }
+            if (operand->period != 0U) {
+                periods[0] = (uint32_t)p;
+                periods[1] = (uint32_t)operand->period;
+                periods += 2U;
+            }
         }
-        (void)memcpy(words + M3_HIP_PROGRAM_HEADER_WORDS +
-                         2U * group->operand_count,
-                     plan->code + group->code_first,
+        (void)memcpy(periods, plan->code + group->code_first,
                      group->code_count * sizeof(*words));
-        at += M3_HIP_PROGRAM_HEADER_WORDS + 2U * group->operand_count +
-              group->code_count;
+        at += m3_program_word_count(group);
     }
     return true;
 }
@@ -132,9 +172,7 @@ static void m3_runs_fused(m3_session *session, const m3_fuse_plan *plan,
             program->commands = &session->commands[n];
             program->command_count = group->node_count;
             program->words = session->program_words + offsets[gi];
-            program->word_count = M3_HIP_PROGRAM_HEADER_WORDS +
-                                  2U * group->operand_count +
-                                  group->code_count;
+            program->word_count = m3_program_word_count(group);
             program->storage = session->program_storage;
             program->byte_offset = offsets[gi] * sizeof(uint32_t);
             session->run_providers[out] = session->providers[n];
@@ -163,11 +201,9 @@ static void m3_prepare_programs(m3_session *session,
     for (gi = 0U; device != NULL && gi < plan->group_count; ++gi) {
         const m3_fuse_group *group = &plan->groups[gi];
 
-        (void)m3_hip_prepare_program(
-            device, session->program_words + offsets[gi],
-            M3_HIP_PROGRAM_HEADER_WORDS + 2U * group->operand_count +
-                group->code_count,
-            NULL, 0U);
+        (void)m3_hip_prepare_program(device,
+                                     session->program_words + offsets[gi],
+                                     m3_program_word_count(group), NULL, 0U);
     }
 }
 
@@ -215,11 +251,18 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
 
         fuse_nodes[n].kind = node->kind;
         if (m3_op_binary_of(&session->commands[n]) != NULL) {
+            const m3_tensor_metadata *output =
+                &session->values[node->outputs[0]].metadata;
+
             fuse_nodes[n].left = (uint32_t)node->inputs[0];
             fuse_nodes[n].right = (uint32_t)node->inputs[1];
             fuse_nodes[n].output = (uint32_t)node->outputs[0];
             fuse_nodes[n].eligible =
                 session->providers[n] == M3_PROVIDER_HIP;
+            fuse_nodes[n].left_trailing = m3_trailing_broadcast(
+                &session->values[node->inputs[0]].metadata, output);
+            fuse_nodes[n].right_trailing = m3_trailing_broadcast(
+                &session->values[node->inputs[1]].metadata, output);
         } else if (node->kind == M3_OP_CAST || node->kind == M3_OP_COPY) {
             fuse_nodes[n].left = (uint32_t)node->inputs[0];
             fuse_nodes[n].right = (uint32_t)node->inputs[0];
@@ -238,9 +281,7 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
         return status;
     }
     for (n = 0U; n < plan.group_count; ++n) {
-        total += M3_HIP_PROGRAM_HEADER_WORDS +
-                 2U * plan.groups[n].operand_count +
-                 plan.groups[n].code_count;
+        total += m3_program_word_count(&plan.groups[n]);
     }
     session->program_words = malloc(total * sizeof(uint32_t));
     offsets = malloc(plan.group_count * sizeof(*offsets));

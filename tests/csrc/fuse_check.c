@@ -19,11 +19,14 @@
  *       Random graphs of ADD/SUB/MUL/DIV, CAST and COPY over F32, F16 and
  *       BF16 values with array, scalar and differently sized operands,
  *       OUTPUT and TEMPORARY roles, and nodes on another provider between
- *       them.
+ *       them. An operand smaller than the output (its count divides the
+ *       output's) is a trailing broadcast, read at e mod its count, or,
+ *       when the node does not mark it trailing, a leading one, read at
+ *       e / (output count / its count); only the first kind may fuse.
  *       `planted` corrupts each plan before it runs (the first STORE is
  *       turned into a store of another register, the sources of every
- *       SUB/DIV are swapped, and OPs lose their rounding dtype): the
- *       comparison must then fail.
+ *       SUB/DIV are swapped, OPs lose their rounding dtype and periodic
+ *       operands their period): the comparison must then fail.
  *   fuse_check euler <steps>
  *       The Euler CFG graph of the flow solver, 6 nodes per step; reports
  *       the plan's shape and checks its result.
@@ -99,6 +102,8 @@ static void add_node(graph_t *g, m3_op_kind kind, uint32_t left,
     g->nodes[g->node_count].right = right;
     g->nodes[g->node_count].output = output;
     g->nodes[g->node_count].eligible = eligible;
+    g->nodes[g->node_count].left_trailing = false;
+    g->nodes[g->node_count].right_trailing = false;
     g->node_count += 1U;
 }
 
@@ -124,12 +129,23 @@ static uint32_t random_f32(void)
     return (bits & 0x807fffffU) | ((120U + below(14U)) << 23U);
 }
 
-static uint32_t load_f32(const graph_t *g, uint32_t value, uint64_t e)
+/* Element `index` of a value, as F32 bits. */
+static uint32_t load_f32(const graph_t *g, uint32_t value, uint64_t index)
 {
-    const m3_fuse_value *v = &g->values[value];
-    uint32_t raw = g->data[value][v->element_count == 1U ? 0U : e];
+    return m3_load_as_f32_bits(g->data[value][index],
+                               (uint32_t)g->values[value].dtype);
+}
 
-    return m3_load_as_f32_bits(raw, (uint32_t)v->dtype);
+/* Index of an operand of `count` elements read for output element e of
+ * `out` elements: the same element, the one scalar, a trailing broadcast
+ * (e mod count) or a leading one (e / (out / count)). */
+static uint64_t broadcast_index(uint64_t count, uint64_t out, bool trailing,
+                                uint64_t e)
+{
+    return count == out  ? e
+           : count == 1U ? 0U
+           : trailing    ? e % count
+                         : e / (out / count);
 }
 
 static uint32_t op_of(m3_op_kind kind)
@@ -161,9 +177,17 @@ static void run_node(graph_t *g, size_t n)
         if (node->kind == M3_OP_CAST) {
             result = load_f32(g, node->left, e);
         } else {
-            result = m3_binary_f32_bits(op_of(node->kind),
-                                        load_f32(g, node->left, e),
-                                        load_f32(g, node->right, e));
+            const uint64_t lc = g->values[node->left].element_count;
+            const uint64_t rc = g->values[node->right].element_count;
+
+            result = m3_binary_f32_bits(
+                op_of(node->kind),
+                load_f32(g, node->left,
+                         broadcast_index(lc, out->element_count,
+                                         node->left_trailing, e)),
+                load_f32(g, node->right,
+                         broadcast_index(rc, out->element_count,
+                                         node->right_trailing, e)));
         }
         g->data[node->output][e] =
             m3_store_from_f32_bits(result, (uint32_t)out->dtype);
@@ -178,6 +202,7 @@ static size_t check_words(const m3_fuse_plan *plan, const m3_fuse_group *gr,
     const uint32_t *code = plan->code + gr->code_first;
     size_t bad = 0U;
     size_t pc = 0U;
+    size_t periodic = 0U;
 
     if (gr->operand_count > M3_HIP_PROGRAM_MAX_OPERANDS ||
         gr->code_count > M3_HIP_PROGRAM_MAX_WORDS) {
@@ -185,11 +210,24 @@ static size_t check_words(const m3_fuse_plan *plan, const m3_fuse_group *gr,
     }
     for (size_t p = 0U; p < gr->operand_count; ++p) {
         const m3_fuse_operand *o = &plan->operands[gr->operand_first + p];
+        uint64_t count;
 
-        bad += o->value >= g->value_count;
-        bad += o->scalar != (g->values[o->value].element_count == 1U &&
-                             gr->element_count > 1U);
+        if (o->value >= g->value_count) {
+            bad += 1U;
+            continue;
+        }
+        count = g->values[o->value].element_count;
+        bad += o->scalar != (count == 1U && gr->element_count > 1U);
+        /* an array smaller than the group is read with its period, a
+         * multiple of 4 dividing the group's count (the launcher's rule) */
+        bad += o->period != (!o->scalar && count != gr->element_count
+                                 ? count
+                                 : 0U);
+        bad += o->period != 0U && (o->period % 4U != 0U ||
+                                   gr->element_count % o->period != 0U);
+        periodic += o->period != 0U;
     }
+    bad += periodic != gr->period_count;
     while (pc < gr->code_count) {
         uint32_t w = code[pc];
 
@@ -244,7 +282,8 @@ static size_t check_words(const m3_fuse_plan *plan, const m3_fuse_group *gr,
 
             bad += (w & 0xccU) != 0U || (w >> 16U) != 0U ||
                    index >= gr->operand_count ||
-                   plan->operands[gr->operand_first + index].scalar;
+                   plan->operands[gr->operand_first + index].scalar ||
+                   plan->operands[gr->operand_first + index].period != 0U;
             pc += 1U;
             break;
         }
@@ -280,10 +319,19 @@ static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
                 uint32_t n = ((w >> 2U) & 3U) + 1U;
 
                 for (uint32_t k = 0U; k < n; ++k) {
-                    uint32_t index = (code[pc + 1U] >> (8U * k)) & 0xffU;
+                    const m3_fuse_operand *o =
+                        &operands[(code[pc + 1U] >> (8U * k)) & 0xffU];
+                    uint64_t at = o->period != 0U ? e % o->period : e;
 
-                    f[k] = load_f32(g, operands[index].value, e);
-                    f_set[k] = true;
+                    /* a read past the value (a lost period) counts as
+                     * unwritten and yields the sentinel */
+                    if (at < g->values[o->value].element_count) {
+                        f[k] = load_f32(g, o->value, at);
+                        f_set[k] = true;
+                    } else {
+                        f[k] = SENTINEL;
+                        f_set[k] = false;
+                    }
                 }
                 pc += 2U;
             } else if ((w & 3U) == M3_HIP_PROGRAM_OP ||
@@ -325,12 +373,15 @@ static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
 }
 
 /* Corrupts a plan: the first STORE stores another register, the sources
- * of every SUB and DIV are swapped, and no OP rounds through its output's
- * 16-bit dtype. */
+ * of every SUB and DIV are swapped, no OP rounds through its output's
+ * 16-bit dtype, and periodic operands lose their period. */
 static void plant(m3_fuse_plan *plan)
 {
     bool first = true;
 
+    for (size_t p = 0U; p < plan->operand_count; ++p) {
+        plan->operands[p].period = 0U;
+    }
     for (size_t gi = 0U; gi < plan->group_count; ++gi) {
         const m3_fuse_group *gr = &plan->groups[gi];
         uint32_t *code = plan->code + gr->code_first;
@@ -374,6 +425,7 @@ typedef struct {
     size_t rounds;         /* ROUND instructions (fused CAST/COPY) */
     size_t rounding_ops;   /* OP instructions with a 16-bit rounding */
     size_t narrow_operands; /* F16/BF16 operands of programs */
+    size_t periodic_operands; /* operands read with a period */
 } stats_t;
 
 static void allocate_data(graph_t *g, uint32_t **data)
@@ -445,9 +497,11 @@ static void check_graph(graph_t *g, bool planted, stats_t *st)
             pc += (w & 3U) == M3_HIP_PROGRAM_FETCH ? 2U : 1U;
         }
         for (size_t p = 0U; p < gr->operand_count; ++p) {
+            const m3_fuse_operand *o = &plan.operands[gr->operand_first + p];
+
             st->narrow_operands +=
-                g->values[plan.operands[gr->operand_first + p].value].dtype !=
-                M3_DTYPE_F32;
+                g->values[o->value].dtype != M3_DTYPE_F32;
+            st->periodic_operands += o->period != 0U;
         }
         for (n = gr->first_node; n < gr->first_node + gr->node_count; ++n) {
             group_of[n] = gi;
@@ -514,9 +568,21 @@ static void random_graph(graph_t *g)
 {
     static const m3_op_kind kinds[] = {M3_OP_ADD, M3_OP_MUL, M3_OP_SUB,
                                        M3_OP_DIV};
-    const uint64_t counts[3] = {1U + below(40U), 1U, 1U + below(12U)};
+    /* half of the graphs have a count that is a multiple of 4, with a
+     * period (a multiple of 4 dividing it) for trailing operands; a value
+     * of half the count (not always a multiple of 4) is read with either
+     * broadcast */
+    const uint64_t quads = 1U + below(10U);
+    const uint64_t base = below(2U) ? 4U * quads : 1U + below(40U);
+    uint64_t period = 4U;
+    const uint64_t counts[3] = {base, 1U, 1U + below(12U)};
     size_t nodes = 2U + below(40U);
 
+    if (base % 4U == 0U) {
+        do {
+            period = 4U * (1U + below((uint32_t)quads));
+        } while (base % period != 0U);
+    }
     memset(g, 0, sizeof(*g));
     for (int k = 0; k < 3; ++k) {
         (void)add_value(g, below(2U) ? M3_GRAPH_INPUT : M3_GRAPH_CONSTANT,
@@ -528,6 +594,10 @@ static void random_graph(graph_t *g)
     (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_F16, counts[0]);
     (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_BF16, counts[0]);
     (void)add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_BF16, 1U);
+    (void)add_value(g, M3_GRAPH_INPUT, M3_DTYPE_F32, period);
+    (void)add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_BF16, period);
+    (void)add_value(g, M3_GRAPH_CONSTANT, M3_DTYPE_F32,
+                    base % 2U == 0U ? base / 2U : base);
     for (size_t n = 0U; n < nodes; ++n) {
         static const m3_dtype floats[3] = {M3_DTYPE_F32, M3_DTYPE_F16,
                                            M3_DTYPE_BF16};
@@ -544,7 +614,7 @@ static void random_graph(graph_t *g)
         do {
             right = below((uint32_t)g->value_count);
             rc = g->values[right].element_count;
-        } while (!(rc == lc || rc == 1U || lc == 1U));
+        } while (lc % rc != 0U && rc % lc != 0U);
         if (g->values[left].dtype != M3_DTYPE_F32 ||
             g->values[right].dtype != M3_DTYPE_F32 || below(100U) < 20U) {
             dtype = floats[below(3U)];
@@ -564,6 +634,8 @@ static void random_graph(graph_t *g)
         add_node(g, kinds[below(4U)], left, right,
                  add_value(g, role, dtype, lc > rc ? lc : rc),
                  below(100U) >= 5U);
+        g->nodes[g->node_count - 1U].left_trailing = below(100U) < 75U;
+        g->nodes[g->node_count - 1U].right_trailing = below(100U) < 75U;
     }
 }
 
@@ -615,10 +687,11 @@ static void print_stats(const char *mode, size_t graphs, const stats_t *st)
            "\"compared_values\": %zu, \"mismatches\": %zu, "
            "\"structure_errors\": %zu, \"unwritten_reads\": %zu, "
            "\"rounds\": %zu, \"rounding_ops\": %zu, "
-           "\"narrow_operands\": %zu",
+           "\"narrow_operands\": %zu, \"periodic_operands\": %zu",
            mode, graphs, st->groups, st->fused_nodes, st->stores,
            st->internal, st->compared, st->mismatches, st->structure,
-           st->unwritten, st->rounds, st->rounding_ops, st->narrow_operands);
+           st->unwritten, st->rounds, st->rounding_ops, st->narrow_operands,
+           st->periodic_operands);
 }
 
 int main(int argc, char **argv)

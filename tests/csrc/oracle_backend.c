@@ -32,6 +32,7 @@ static size_t g_allocations;
 static size_t g_fail_allocation_at; /* 0: never */
 static size_t g_reserved;
 static size_t g_programs;
+static size_t g_periodic; /* periodic operands of the programs run */
 
 void oracle_backend_reset(void);
 size_t oracle_backend_log(int *kinds, int *lists, size_t capacity);
@@ -39,6 +40,7 @@ size_t oracle_backend_lists(void);
 size_t oracle_backend_reserved(void);
 void oracle_backend_fail_allocation_at(size_t index);
 size_t oracle_backend_programs(void);
+size_t oracle_backend_periodic(void);
 m3_status oracle_backend_create(m3_backend **backend, m3_error *error);
 
 void oracle_backend_reset(void)
@@ -49,11 +51,17 @@ void oracle_backend_reset(void)
     g_fail_allocation_at = 0U;
     g_reserved = 0U;
     g_programs = 0U;
+    g_periodic = 0U;
 }
 
 size_t oracle_backend_programs(void)
 {
     return g_programs;
+}
+
+size_t oracle_backend_periodic(void)
+{
+    return g_periodic;
 }
 
 size_t oracle_backend_log(int *kinds, int *lists, size_t capacity)
@@ -171,16 +179,35 @@ static uint8_t *operand_address(const uint32_t *operands, uint32_t index)
     return (uint8_t *)(uintptr_t)(((high << 32U) | low) & ~(uint64_t)1U);
 }
 
+/* Period of operand `index` from the period table (pairs of operand index
+ * and period), 0 when it is not periodic. */
+static uint64_t operand_period(const uint32_t *periods, uint32_t period_count,
+                               uint32_t index)
+{
+    uint32_t k;
+
+    for (k = 0U; k < period_count; ++k) {
+        if (periods[2U * k] == index) {
+            return periods[2U * k + 1U];
+        }
+    }
+    return 0U;
+}
+
 /* Element e of operand `index` as F32 bits, converted from its dtype (bits
- * 30-31 of the high word) with the oracle's converters. */
-static uint32_t operand_load(const uint32_t *operands, uint32_t index,
+ * 30-31 of the high word) with the oracle's converters; a periodic operand
+ * is read at e mod its period. */
+static uint32_t operand_load(const uint32_t *operands, const uint32_t *periods,
+                             uint32_t period_count, uint32_t index,
                              uint64_t e)
 {
     const uint8_t *base = operand_address(operands, index);
+    const uint64_t period = operand_period(periods, period_count, index);
     uint32_t dtype = operands[2U * index + 1U] >> 30U;
     uint16_t half;
     uint32_t bits;
 
+    e = period != 0U ? e % period : e;
     if (dtype == ORACLE_F32) {
         memcpy(&bits, base + 4U * e, sizeof(bits));
         return bits;
@@ -222,8 +249,10 @@ static int run_program(const m3_op_elementwise_program *program)
     const uint32_t operand_count = words[1];
     const uint32_t code_words = words[2];
     const uint64_t count = (uint64_t)words[3] | ((uint64_t)words[4] << 32U);
+    const uint32_t period_count = words[5];
     const uint32_t *operands = words + 8;
-    const uint32_t *code = operands + 2U * operand_count;
+    const uint32_t *periods = operands + 2U * operand_count;
+    const uint32_t *code = periods + 2U * period_count;
     const uint8_t *stored =
         (const uint8_t *)m3_storage_data(program->storage);
     uint64_t e;
@@ -231,7 +260,8 @@ static int run_program(const m3_op_elementwise_program *program)
     if (stored == NULL ||
         memcmp(stored + program->byte_offset, words,
                program->word_count * sizeof(uint32_t)) != 0 ||
-        program->word_count != 8U + 2U * operand_count + code_words) {
+        program->word_count !=
+            8U + 2U * operand_count + 2U * period_count + code_words) {
         return (int)M3_STATUS_INTERNAL;
     }
     for (e = 0U; e < count; ++e) {
@@ -247,8 +277,9 @@ static int run_program(const m3_op_elementwise_program *program)
                 uint32_t k;
 
                 for (k = 0U; k < n; ++k) {
-                    f[k] = operand_load(
-                        operands, (code[pc + 1U] >> (8U * k)) & 0xffU, e);
+                    f[k] = operand_load(operands, periods, period_count,
+                                        (code[pc + 1U] >> (8U * k)) & 0xffU,
+                                        e);
                 }
                 pc += 2U;
             } else if ((w & 3U) == 1U || (w & 3U) == 3U) { /* OP, ROUND */
@@ -261,7 +292,8 @@ static int run_program(const m3_op_elementwise_program *program)
                     x[k] = kinds[k] < 4U   ? r[kinds[k]]
                            : kinds[k] < 8U ? f[kinds[k] - 4U]
                                            : operand_load(
-                                                 operands,
+                                                 operands, periods,
+                                                 period_count,
                                                  (w >> 16U) & 0xffU, 0U);
                 }
                 r[(w >> 4U) & 3U] = round_through(
@@ -276,6 +308,7 @@ static int run_program(const m3_op_elementwise_program *program)
         }
     }
     g_programs += 1U;
+    g_periodic += period_count;
     return 0;
 }
 

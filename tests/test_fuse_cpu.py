@@ -8,8 +8,11 @@ the output dtype; src/m3_op_execute_basic.c:61-77; CAST through F32 and
 COPY as a raw copy, :11-59), and with every fused
 group replaced by its program interpreted the way the kernel runs it. Every
 value that has to reach memory must agree bit for bit, NaN payloads
-included. A plan with planted mistakes (a STORE of the wrong register, SUB
-and DIV with swapped operands) must be caught by the same comparison.
+included. Operands smaller than the output are broadcast along trailing
+axes (read at e mod their count, the only kind that may fuse) or leading
+ones. A plan with planted mistakes (a STORE of the wrong register, SUB and
+DIV with swapped operands, periodic operands read without their period)
+must be caught by the same comparison.
 """
 import json
 import os
@@ -62,11 +65,15 @@ def test_random_plans_match_node_by_node():
         assert r["rounds"] > 1000
         assert r["rounding_ops"] > 1000
         assert r["narrow_operands"] > 1000
+        # smaller operands broadcast along trailing axes are fused too
+        assert r["periodic_operands"] > 1000
 
 
 def test_planted_plan_mistakes_are_detected():
     r = run("random", "500", "3", "planted", expect_ok=False)
     assert r["mismatches"] > 100
+    # a periodic operand without its period breaks the launcher's rules
+    assert r["structure_errors"] > 100
 
 
 def test_euler_graph_is_one_program():

@@ -238,6 +238,132 @@ def test_fused_mixed_dtypes_equal_unfused(gpu, seed, shape, generated):
         assert kernels_on.get(ran, (0, 0.0))[0] >= 1
 
 
+def broadcast_graph(seed, full, nodes=40):
+    """Random elementwise DAG over `full` = (A, B, C) whose operands are
+    broadcast from smaller tensors: along trailing axes ((C,), (1, C),
+    (B, C), (1, B, C)), which programs read periodically, and along others
+    ((A, 1, C), (A, B, 1), (B, 1)), which stay per-node kernels; F16 and
+    BF16 values and scalars among them."""
+    a_, b_, c_ = full
+    shapes = [full, (c_,), (1, c_), (b_, c_), (1, b_, c_), (a_, 1, c_),
+              (a_, b_, 1), (b_, 1), (1,)]
+
+    def build():
+        rng = np.random.default_rng(seed)
+        floats = [m3.F32, m3.F16, m3.BF16]
+        g = m3.Graph()
+        values, feeds, outputs = [], [], []
+        for shape in shapes:
+            for dtype in (m3.F32, floats[1 + rng.integers(2)]):
+                vid = g.add_value(m3.INPUT, dtype, shape)
+                feeds.append((vid, specials(rng, shape) if dtype == m3.F32
+                              else narrow(rng, shape, dtype)))
+                values.append((vid, shape, dtype))
+        kinds = [m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV]
+        for n in range(nodes):
+            role = m3.OUTPUT if n == nodes - 1 or rng.random() < 0.2 \
+                else m3.TEMPORARY
+            produced = [v for v in values[2 * len(shapes):] if v[1] == full]
+            pool = produced if produced and rng.random() < 0.7 else values
+            a = pool[rng.integers(len(pool))]
+            b = values[rng.integers(len(values))]
+            if rng.random() < 0.5:
+                a, b = b, a
+            out_shape = tuple(np.broadcast_shapes(a[1], b[1]))
+            dtype = floats[rng.integers(3)] if rng.random() < 0.3 \
+                else m3.F32
+            vid = g.add_value(role, dtype, out_shape)
+            g.add_node(kinds[rng.integers(4)], [a[0], b[0]], [vid])
+            entry = (vid, out_shape, dtype)
+            values.append(entry)
+            if role == m3.OUTPUT:
+                outputs.append((vid, out_shape, NUMPY_OF[dtype]))
+        return g, feeds, outputs
+    return build
+
+
+@pytest.mark.parametrize("generated", [True, False])
+@pytest.mark.parametrize("seed,full", [(0, (3, 4, 8)), (1, (2, 33, 132)),
+                                       (2, (4, 96, 1536))])
+def test_fused_broadcasts_equal_unfused(gpu, seed, full, generated):
+    """Operands broadcast along trailing axes, read periodically inside
+    programs, give every OUTPUT byte for byte equal to the per-node
+    kernels, NaN payloads included."""
+    print("fusion broadcast graph seed", seed, "shape", full, "generated",
+          generated, flush=True)
+    build = broadcast_graph(6000 + seed, full)
+    fused, plan_on, kernels_on = run_session(build, True, generated)
+    plain, plan_off, _ = run_session(build, False)
+    assert plan_on == plan_off
+    for a, b in zip(fused, plain):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+    ran = "m3_program" if generated else "m3_program_interpreted"
+    assert kernels_on.get(ran, (0, 0.0))[0] >= 1
+
+
+def scale_shift_graph(shape):
+    """y = bf16((x * scale + shift) * gate) with per-channel scale and
+    shift [C] and a per-position gate [L, C] over x [N, L, C]."""
+    def build():
+        rng = np.random.default_rng(11)
+        n, length, channels = shape
+        x = specials(rng, shape)
+        scale = rng.standard_normal(channels).astype(np.float32)
+        shift = rng.standard_normal((1, channels)).astype(np.float32)
+        gate = rng.standard_normal((length, channels)).astype(np.float32)
+        g = m3.Graph()
+        vx = g.add_value(m3.INPUT, m3.F32, shape)
+        vs = g.add_value(m3.CONSTANT, m3.F32, (channels,))
+        vb = g.add_value(m3.CONSTANT, m3.F32, (1, channels))
+        vg = g.add_value(m3.INPUT, m3.F32, (length, channels))
+        g.set_constant(vs, scale)
+        g.set_constant(vb, shift)
+        t0 = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        t1 = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        t2 = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        vy = g.add_value(m3.OUTPUT, m3.BF16, shape)
+        g.add_node(m3.OP_MUL, [vx, vs], [t0])
+        g.add_node(m3.OP_ADD, [t0, vb], [t1])
+        g.add_node(m3.OP_MUL, [t1, vg], [t2])
+        g.add_node(m3.OP_CAST, [t2], [vy])
+        f = np.float32
+        with np.errstate(invalid="ignore", over="ignore"):
+            y = ((x * scale).astype(f) + shift).astype(f)
+            y = (y * gate).astype(f)
+        scale_shift_graph.expected = y
+        return g, [(vx, x), (vg, gate)], [(vy, shape, np.uint16)]
+    return build
+
+
+def bf16_bits(values):
+    """float32 -> bfloat16 bits, round to nearest even, NaNs quieted (the
+    CAST's conversion)."""
+    bits = values.view(np.uint32).astype(np.uint64)
+    rounded = ((bits + 0x7fff + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(values)
+    rounded[nan] = ((bits[nan] >> 16) | 0x40).astype(np.uint16)
+    return rounded
+
+
+@pytest.mark.parametrize("generated", [True, False])
+def test_scale_shift_gate_is_one_program(gpu, generated):
+    """A per-channel scale and shift and a per-position gate read
+    periodically: the four nodes run as one program launch whose output
+    equals the float32 numpy operations rounded to bfloat16."""
+    shape = (4, 256, 1536)
+    print("fusion scale/shift/gate", shape, "generated", generated,
+          flush=True)
+    build = scale_shift_graph(shape)
+    fused, plan_on, kernels = run_session(build, True, generated)
+    plain, plan_off, _ = run_session(build, False)
+    name = "m3_program" if generated else "m3_program_interpreted"
+    assert plan_on == plan_off
+    assert kernels[name][0] == 1 and set(kernels) == {name}
+    expected = bf16_bits(scale_shift_graph.expected)
+    assert np.array_equal(fused[0], expected)
+    assert np.array_equal(plain[0], expected)
+
+
 def euler_graph(steps, shape):
     def build():
         rng = m3.rng_new(0, 0)
@@ -305,8 +431,11 @@ def test_program_words_are_checked_before_launch(gpu):
     """m3_hip_launch_program rejects malformed words on the host (nothing
     is launched): bad magic, operand index out of range, a scalar fetched,
     a rounding dtype out of range in OP and in ROUND, an operand dtype out
-    of range, a misaligned 16-bit array, and a word count that does not
-    match the header. Every address in the words, and the device copy of
+    of range, a misaligned 16-bit array, a word count that does not match
+    the header, and period tables that break the rules (more entries than
+    operands, a period that is zero, not a multiple of 4 or does not
+    divide the count, an index out of range, a scalar or STORE target made
+    periodic, indices not increasing). Every address in the words, and the device copy of
     the words, is real device memory, so a case the check missed would
     still only touch memory of this test; the valid words run once."""
     _, lib = m3.load()
@@ -327,10 +456,11 @@ def test_program_words_are_checked_before_launch(gpu):
         scalar = base.value + 8192     # one F32
         device_words = ctypes.c_void_p(base.value + 16384)
 
-        def words(operands, code, count=8):
+        def words(operands, code, count=8, periods=()):
             header = [0x4d335031, len(operands) // 2, len(code),
-                      count, 0, 0, 0, 0]
-            return np.array(header + operands + code, np.uint32)
+                      count, 0, len(periods) // 2, 0, 0]
+            return np.array(header + operands + list(periods) + code,
+                            np.uint32)
 
         def address(at, flags=0, dtype=0):
             return [(at & 0xffffffff) | flags, (at >> 32) | (dtype << 30)]
@@ -380,6 +510,56 @@ def test_program_words_are_checked_before_launch(gpu):
             device_words, good.size, msg, 256)
         assert code == 0, msg.value
         assert lib.m3_hip_synchronize(handle, msg, 256) == 0, msg.value
+
+        # periodic operand: array[e] = array[e] * period4[e mod 4]
+        period4 = base.value + 6144    # 4 F32 elements
+        operands = address(array) + address(period4)
+        periodic = words(operands, [0x0 | (1 << 2), 0x0100,
+                                    0x1 | (1 << 2) | (0 << 4) | (4 << 8) |
+                                    (5 << 12),
+                                    0x2 | (0 << 4) | (0 << 8)],
+                         periods=[1, 4])
+        assert lib.m3_hip_copy_h2d(
+            handle, device_words, periodic.ctypes.data_as(ctypes.c_void_p),
+            periodic.nbytes, msg, 256) == 0
+        bad = []
+        for at, value in ((5, 3),          # more periodic operands than P
+                          (13, 6),         # period not a multiple of 4
+                          (13, 16),        # period does not divide count
+                          (13, 0),         # period zero
+                          (12, 2),         # operand index out of range
+                          (17, 0x2 | (1 << 8))):  # STORE to the periodic
+            b = periodic.copy()
+            b[at] = value
+            bad.append(b)
+        b = periodic.copy()
+        b[10] |= 1  # the periodic operand flagged scalar
+        bad.append(b)
+        bad.append(words(operands + address(period4),
+                         [0x0 | (1 << 2), 0x0100, 0x1 | (4 << 8) | (5 << 12),
+                          0x2], periods=[2, 4, 1, 4]))  # not increasing
+        for index, w in enumerate(bad):
+            code = lib.m3_hip_launch_program(
+                handle, w.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                device_words, w.size, msg, 256)
+            assert code == 1, ("periodic", index, msg.value)
+        x = np.arange(1, 9, dtype=np.float32)
+        p = np.array([2.0, -1.0, 0.5, 3.0], np.float32)
+        for data, at in ((x, array), (p, period4)):
+            assert lib.m3_hip_copy_h2d(
+                handle, ctypes.c_void_p(at),
+                data.ctypes.data_as(ctypes.c_void_p), data.nbytes, msg,
+                256) == 0
+        code = lib.m3_hip_launch_program(
+            handle, periodic.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+            device_words, periodic.size, msg, 256)
+        assert code == 0, msg.value
+        got = np.zeros(8, np.float32)
+        lib.m3_hip_copy_d2h.argtypes = [vp, vp, vp, sz, cp, sz]
+        assert lib.m3_hip_copy_d2h(
+            handle, got.ctypes.data_as(ctypes.c_void_p),
+            ctypes.c_void_p(array), got.nbytes, msg, 256) == 0, msg.value
+        assert np.array_equal(got, x * np.tile(p, 2))
     finally:
         if base.value:
             lib.m3_hip_arena_release(handle, base)

@@ -46,6 +46,7 @@ def backend_lib():
     fake.oracle_backend_reserved.restype = ctypes.c_size_t
     fake.oracle_backend_fail_allocation_at.argtypes = [ctypes.c_size_t]
     fake.oracle_backend_programs.restype = ctypes.c_size_t
+    fake.oracle_backend_periodic.restype = ctypes.c_size_t
     factory = ctypes.cast(fake.oracle_backend_create, ctypes.c_void_p)
     lib.m3_provider_set_gpu_factory.argtypes = [ctypes.c_void_p]
     lib.m3_provider_set_gpu_factory(factory)
@@ -574,6 +575,79 @@ def test_fusion_happens_on_random_graphs(fake):
         build = _random_chain_graph(1000 + seed)
         total += _session_outputs(build, True, fake)[2]
     assert total >= 8
+
+
+def _broadcast_chain_graph(seed):
+    """Elementwise DAGs over [3, 4, 8] whose operands are broadcast from
+    smaller tensors: trailing ones ([8], [1, 8], [4, 8], [1, 4, 8], which
+    programs read periodically), others ([3, 1, 8], [3, 4, 1], [4, 1],
+    which stay unfused nodes), scalars, F16 and BF16 values among them."""
+    full = (3, 4, 8)
+    shapes = [full, (8,), (1, 8), (4, 8), (1, 4, 8), (3, 1, 8), (3, 4, 1),
+              (4, 1), (1,)]
+
+    def build():
+        rng = np.random.default_rng(seed)
+        floats = [m3.F32, m3.F16, m3.BF16]
+        g = m3.Graph()
+        values = []
+        feeds = []
+        outputs = []
+        for shape in shapes:
+            for dtype in (m3.F32, floats[1 + rng.integers(2)]):
+                vid = g.add_value(m3.INPUT, dtype, shape)
+                feeds.append((vid, _specials(rng, shape) if dtype == m3.F32
+                              else _narrow(rng, shape, dtype)))
+                values.append((vid, shape, dtype))
+        kinds = [m3.OP_ADD, m3.OP_MUL, m3.OP_SUB, m3.OP_DIV]
+        for n in range(40):
+            role = m3.OUTPUT if n == 39 or rng.random() < 0.2 \
+                else m3.TEMPORARY
+            # mostly a full-size operand beside a broadcast one
+            produced = [v for v in values[2 * len(shapes):]
+                        if v[1] == full]
+            pool = produced if produced and rng.random() < 0.7 else values
+            a = pool[rng.integers(len(pool))]
+            b = values[rng.integers(len(values))]
+            if rng.random() < 0.5:
+                a, b = b, a
+            out_shape = tuple(np.broadcast_shapes(a[1], b[1]))
+            dtype = floats[rng.integers(3)] if rng.random() < 0.3 \
+                else m3.F32
+            vid = g.add_value(role, dtype, out_shape)
+            g.add_node(kinds[rng.integers(4)], [a[0], b[0]], [vid])
+            entry = (vid, out_shape, dtype)
+            values.append(entry)
+            if role == m3.OUTPUT:
+                outputs.append((vid, out_shape, _NUMPY_OF[dtype]))
+        return g, feeds, outputs
+    return build
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_fused_broadcast_runs_equal_unfused_runs(fake, seed):
+    """Operands broadcast along trailing axes are read periodically inside
+    programs; every OUTPUT is identical byte for byte with and without
+    fusion."""
+    build = _broadcast_chain_graph(5000 + seed)
+    fused, plan_on, _, kinds_on = _session_outputs(build, True, fake)
+    plain, plan_off, programs_off, kinds_off = _session_outputs(build, False,
+                                                                fake)
+    assert plan_on == plan_off
+    assert programs_off == 0
+    assert kinds_on == kinds_off
+    for a, b in zip(fused, plain):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+def test_broadcast_graphs_fuse_periodic_operands(fake):
+    """The planner does read trailing-broadcast operands inside programs
+    (the backend counts the periodic operands of the programs it runs)."""
+    periodic = 0
+    for seed in range(8):
+        _session_outputs(_broadcast_chain_graph(5000 + seed), True, fake)
+        periodic += fake.oracle_backend_periodic()
+    assert periodic >= 40
 
 
 def _euler_graph(steps, shape):
