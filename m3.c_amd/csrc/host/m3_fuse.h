@@ -18,9 +18,9 @@
  *     trailing, M elements with M a multiple of 4 that divides the
  *     output's count (a periodic operand: element e reads e mod M, the
  *     right-aligned broadcast of a tensor whose shape, leading ones
- *     removed, is the output's trailing dimensions), or a CAST between two of those
- *     dtypes, or a COPY of F32, described with right == left and an
- *     input of the output's element count;
+ *     removed, is the output's trailing dimensions); or a CAST between
+ *     two of those dtypes, or a COPY of F32, described with
+ *     right == left and an input of the output's element count;
  *   - a group is a run of consecutive such nodes with the same element
  *     count; a value produced in the group lives in one of four registers
  *     from its producer to its last use, and a node joins only if a
