@@ -14,7 +14,9 @@ For every class:
                   scan, launches and the closing stream synchronize);
   * kernel_us     average duration of the dominant kernel from the HIP
                   events the library attaches to each of its dispatches
-                  (hipExtLaunchKernelGGL on the session's own stream);
+                  (hipExtLaunchKernelGGL on the session's own stream), with
+                  the median over runs and the fastest and slowest run
+                  beside it (VALU-bound kernels vary with the GPU clock);
   * GB/s          algorithmic bytes (unique tensor bytes read + written)
                   divided by those times; peak HBM is 8.0 TB/s.
 Sessions rotate so that the inputs read between two runs of one session
@@ -183,22 +185,30 @@ class Workload:
         for i in range(steps):
             self.sessions[i % len(self.sessions)].run()
         wall = (time.perf_counter() - start) / steps
-        for session in self.sessions:
-            session.timing_enable(True)
-        for i in range(steps):
-            self.sessions[i % len(self.sessions)].run()
+        # the timed pass reads the events run by run, so that the median of
+        # the dominant kernel's per-run average can be reported beside the
+        # mean (VALU-bound kernels vary with the clock from run to run)
         launches = 0
         total_ms = 0.0
         per_kernel = {}
-        for session in self.sessions:
-            for name, (count, ms) in session.timing_read().items():
+        self.run_kernel_us = []
+        for i in range(steps):
+            session = self.sessions[i % len(self.sessions)]
+            session.timing_reset()
+            session.timing_enable(True)
+            session.run()
+            times = session.timing_read()
+            session.timing_enable(False)
+            run_count, run_ms = 0, 0.0
+            for name, (count, ms) in times.items():
                 previous = per_kernel.get(name, (0, 0.0))
                 per_kernel[name] = (previous[0] + count, previous[1] + ms)
-                session.timing_enable(False)
-        for name in self.kernel:
-            count, ms = per_kernel.get(name, (0, 0.0))
-            launches += count
-            total_ms += ms
+                if name in self.kernel:
+                    run_count += count
+                    run_ms += ms
+            launches += run_count
+            total_ms += run_ms
+            self.run_kernel_us.append(1000.0 * run_ms / max(run_count, 1))
         kernel_us = 1000.0 * total_ms / max(launches, 1)
         runs_kernel_ms = sum(ms for _, ms in per_kernel.values()) / steps
         return wall * 1000.0, kernel_us, launches // steps, per_kernel, \
@@ -480,6 +490,14 @@ def result_entry(name, workload, wall_ms, kernel_us, launches, bytes_total,
         "kernel_frac_of_peak": round(kernel_gbps / PEAK_GBPS, 4),
         "parity": parity,
     }
+    runs = getattr(workload, "run_kernel_us", None)
+    if runs:
+        median_us = float(np.median(runs))
+        entry["kernel_us_median"] = round(median_us, 3)
+        entry["kernel_frac_of_peak_median"] = round(
+            kernel_bytes / (median_us * 1e-6) / 1e9 / PEAK_GBPS, 4)
+        entry["kernel_us_min_max"] = [round(min(runs), 3),
+                                      round(max(runs), 3)]
     if cpu_seconds is not None:
         entry["cpu_GBps"] = round(cpu_bytes / cpu_seconds / 1e9, 4)
     return entry
@@ -646,8 +664,7 @@ def main():
         nbytes = 2 * x.nbytes + alpha.nbytes
         w = Workload("snake", build_snake(x, alpha), [x, alpha], nbytes,
                      ["m3_snake1d"], 1, cpu)
-        wall, kus, launches, _, _ = w.measure(max(args.steps // 4, 3),
-                                              args.warmup)
+        wall, kus, launches, _, _ = w.measure(args.steps, args.warmup)
         parity = None
         cpu_seconds = None
         if cpu is not None:
@@ -680,8 +697,7 @@ def main():
         nbytes = 2 * x.nbytes
         w = Workload("tanh", build_tanh(x), [x], nbytes, ["m3_tanh"], 1,
                      cpu)
-        wall, kus, launches, _, _ = w.measure(max(args.steps // 4, 3),
-                                              args.warmup)
+        wall, kus, launches, _, _ = w.measure(args.steps, args.warmup)
         parity = None
         cpu_seconds = None
         if cpu is not None:
@@ -724,8 +740,7 @@ def main():
             nbytes = 3 * g.nbytes
             w = Workload(name, build_gated_silu(g, u, dtype, out_np), [g, u],
                          nbytes, [kernel], 1, cpu)
-            wall, kus, launches, _, _ = w.measure(max(args.steps // 4, 3),
-                                                  args.warmup)
+            wall, kus, launches, _, _ = w.measure(args.steps, args.warmup)
             parity = None
             cpu_seconds = None
             if cpu is not None:
@@ -773,7 +788,7 @@ def main():
                      nbytes, ["m3_program", "m3_program_interpreted",
                               "m3_binary_add", "m3_binary_mul"], 1, cpu)
         wall, kus, launches, kernels, run_kernel_ms = w.measure(
-            max(args.steps // 4, 3), args.warmup)
+            args.steps, args.warmup)
         parity = None
         cpu_seconds = None
         if cpu is not None:
