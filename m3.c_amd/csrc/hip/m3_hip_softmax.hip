@@ -636,8 +636,10 @@ struct m3_rows_variant {
 };
 
 /* Wave-independent variants; the first whose width class fits is used.
- * Rows per wave and sum prefetch depth keep each variant within 128 VGPRs
- * (four waves per SIMD). */
+ * Rows per wave and sum prefetch depth are chosen for four waves per SIMD
+ * (88, 98 and 120 VGPRs for the F32 instances up to width 1024); the
+ * width-2048 instance and the 16-bit-IO instances from width 1024 take
+ * 133-157 VGPRs, three waves per SIMD. */
 const m3_rows_variant m3_rows_variants[] = {
     {1U, 8U, &m3_launch_rows<1, 8, 8, true>,
      &m3_launch_rows<1, 8, 8, false>},
