@@ -79,14 +79,14 @@ def measured_traffic(kernel):
     return None if entry is None else entry.get("traffic_bytes")
 
 
-# ---- CPU baseline (checker side: oracle/_ref or oracle) -------------------
+# ---- CPU baseline (oracle/_ref or the oracle) ------------------------------
 
 class CpuBaseline:
     """The reference CPU provider (kind "reference") or the oracle ("port")."""
 
     def __init__(self):
         sys.path.insert(0, os.path.join(ROOT, "tests"))
-        import harness  # noqa: E402  (checker, loaded only for this leg)
+        import harness  # noqa: E402  (test harness, loaded only for this leg)
         self.harness = harness
         self.kind = "reference" if harness.ref_available() else "port"
 

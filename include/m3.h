@@ -11,7 +11,7 @@
  *   - M3_PROVIDER_HIP (the AMD GPU execution provider; the reference lists
  *     NEURAL_ENGINE, METAL and CPU, include/m3.h:80-84).
  * m3_session_options.allow_metal keeps its name and means "allow the
- * platform GPU provider"; on this build that provider is HIP on gfx950.
+ * platform GPU provider"; in this library that provider is HIP on gfx950.
  *
  * The Music3 model engine (include/m3.h:155-291) is a model adapter and is
  * not part of this library.
@@ -227,14 +227,14 @@ m3_status m3_graph_add_node(m3_graph *graph,
                             const m3_graph_node_desc *description,
                             m3_error *error);
 
-/* Core ML partitions need Apple frameworks. On this build the call records
- * nothing and returns M3_STATUS_UNSUPPORTED. */
+/* Core ML partitions need Apple frameworks. In this library the call
+ * records nothing and returns M3_STATUS_UNSUPPORTED. */
 m3_status m3_graph_add_coreml_partition(
     m3_graph *graph, const m3_coreml_partition_desc *description,
     m3_error *error);
 
 /* A session owns its storage backend and compiled plan; the graph may be
- * freed after creation. On this build a session runs its regular nodes on
+ * freed after creation. In this library a session runs its regular nodes on
  * the HIP provider and needs allow_metal; a session that allows only the
  * CPU provider is rejected with M3_STATUS_UNSUPPORTED. Sessions are not
  * thread-safe. Reference: include/m3.h:240-259. */

@@ -75,7 +75,7 @@ typedef enum {
     M3_HIP_NO_DEVICE = 2,    /* no usable HIP device */
     M3_HIP_OUT_OF_MEMORY = 3,
     M3_HIP_RUNTIME = 4,      /* the HIP runtime reported an error */
-    M3_HIP_UNSUPPORTED = 5   /* valid request this build cannot run */
+    M3_HIP_UNSUPPORTED = 5   /* valid request this library cannot run */
 } m3_hip_code;
 
 /* Element types; values equal m3_dtype. */

@@ -2,8 +2,8 @@
  * m3_graph_internal.h - graph and session state shared by the graph files.
  *
  * The shapes of these records follow src/m3_graph_internal.h:10-88 of the
- * reference; Core ML nodes do not exist on this build, so every node is a
- * regular node.
+ * reference; Core ML nodes do not exist in this library, so every node is
+ * a regular node.
  */
 #ifndef M3_GRAPH_INTERNAL_H
 #define M3_GRAPH_INTERNAL_H

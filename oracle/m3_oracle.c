@@ -1,8 +1,8 @@
 /*
  * m3_oracle.c - CPU restatement of the reference's host tensor ops.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP provider; never part
- * of the product. Built with -ffp-contract=off and without -ffast-math, as
+ * TEST INFRASTRUCTURE ONLY: what the tests compare the HIP provider with;
+ * never part of the product. Built with -ffp-contract=off and without -ffast-math, as
  * the reference asks for (Makefile:7 builds with clang -O3 and no fast-math;
  * src/m3_op_execute_basic.c:182 turns contraction off for Snake1d).
  * Transcendentals are the platform libm's expf/sinf, which is what the

@@ -2,7 +2,8 @@
  * m3_oracle.h - CPU restatement of the reference's host tensor ops.
  *
  * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this code, and only as the checker.
+ * cpu_baseline leg of bench.py may load this code, and only to check or
+ * time results.
  * The product (libm3.so / libm3_hip.so) never links or calls it.
  *
  * Every function restates the reference CPU provider of

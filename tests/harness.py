@@ -5,7 +5,7 @@ A case is a list of host storages (numpy uint8 buffers) and views over them
 (ViewSpec: storage index, dtype, shape, byte strides, byte offset). Views
 that name the same storage alias exactly as they do in the reference.
 
-* ``run_oracle``  - oracle/liboracle.so (CPU restatement, the checker)
+* ``run_oracle``  - oracle/liboracle.so (CPU restatement of the reference)
 * ``run_ref``     - oracle/_ref/libm3ref.so (the reference's own host code),
                     when it was built in this container
 * ``HipFixture``  - the product: storages on the HIP backend, commands
