@@ -344,6 +344,20 @@ def test_snake1d_layouts(hip, shape):
     compare(hip, m3.OP_SNAKE1D, storages, views, "snake %s" % (shape,))
 
 
+def test_snake1d_large_grid(hip):
+    """x[2,64,262144]: 8,192 workgroups of one tile each, every element
+    compared with the oracle."""
+    shape = (2, 64, 262144)
+    rng = np.random.default_rng(10077)
+    count = int(np.prod(shape))
+    x = random_f32(rng, count, scale=3.0, specials=0.001)
+    alpha = rng.uniform(0.1, 2.0, shape[1]).astype(np.float32)
+    views = [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, (1, shape[1], 1)),
+             ViewSpec(2, m3.F32, shape)]
+    storages = [as_bytes(x), as_bytes(alpha), np.zeros(x.nbytes, np.uint8)]
+    compare(hip, m3.OP_SNAKE1D, storages, views, "snake %s" % (shape,))
+
+
 def test_snake1d_strided_input_and_alias(hip):
     rng = np.random.default_rng(11)
     x = random_f32(rng, 2 * 8 * 64, scale=2.0, specials=0.0)
