@@ -14,11 +14,8 @@
  *   - e_j uses m3_expf (the libm algorithm restated bit for bit);
  *   - the sum keeps the reference's left-to-right F32 order: one lane per
  *     row walks the row's e_j in LDS;
- *   - p_j = RN_f32(e_j * RN_f64(1/sum)) equals the IEEE F32 quotient
- *     e_j / sum for all floats e_j and sum >= 1 (a quotient of two floats
- *     lies at least 2^-49 relative from any F32 rounding midpoint unless it
- *     is one, which needs sum = 2^k where 1/sum is exact; the double
- *     product errs by under 2^-52).
+ *   - p_j is the IEEE F32 quotient e_j / sum, formed as
+ *     RN_f32(e_j * RN_f64(1/sum)) where that is exact (m3_softmax_scale4).
  *
  * Kernels, chosen by layout and width (rows contiguous along the last axis
  * with a uniform row stride and width a multiple of 4 use the first two):
@@ -159,9 +156,62 @@ __device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint64_t c,
     m3_stream_store((uint2 *)(row + c * 2U), packed);
 }
 
+/* p = e / sum, the IEEE F32 quotient, for e >= 0 and sum >= 1 given
+ * inverse = RN_f64(1/sum).
+ *
+ * q = RN_f64(e * inverse) is within 2^-52 (relative) of e / sum, so
+ * RN_f32(q) is the quotient unless e / sum lies within 2^-52 of an F32
+ * rounding midpoint:
+ *   - for a normal result the midpoints have 25 significant bits; e / sum
+ *     equals one only when sum = 2^k (1/sum then exact, and q too), and
+ *     otherwise stays at least 2^-49 away from it;
+ *   - below 2^-126 the midpoints are (2k+1) * 2^-150, numbers with few
+ *     significant bits, so e = sum * midpoint holds for ordinary sums
+ *     (147 * 2^-149 / 98 = 3 * 2^-150) and q falls on either side of the
+ *     tie. Such a quotient rounds to a positive subnormal, or to +0 only
+ *     from the tie 2^-150, whose correct rounding is +0 (a non-tie
+ *     quotient near 2^-150 is at least 2^-24 relative from it).
+ * So RN_f32(q) is the quotient whenever it is +0 or normal, and a lane
+ * whose result is a positive subnormal takes the F32 division instead,
+ * behind a wave-uniform test (sum is recovered exactly as
+ * RN_f32(1 / inverse)). The test is one v_cmp_class per element. */
 __device__ __forceinline__ float m3_softmax_scale(float e, double inverse)
 {
-    return (float)((double)e * inverse);
+    constexpr int kPositiveSubnormal = 1 << 7;
+    const float p = (float)((double)e * inverse);
+    const bool tiny = __builtin_amdgcn_classf(p, kPositiveSubnormal);
+
+    if (__any(tiny)) {
+        if (tiny) {
+            return e / (float)(1.0 / inverse);
+        }
+    }
+    return p;
+}
+
+__device__ __forceinline__ float4 m3_softmax_scale4(float4 e, double inverse)
+{
+    constexpr int kPositiveSubnormal = 1 << 7;
+    float4 p;
+
+    p.x = (float)((double)e.x * inverse);
+    p.y = (float)((double)e.y * inverse);
+    p.z = (float)((double)e.z * inverse);
+    p.w = (float)((double)e.w * inverse);
+    const bool tx = __builtin_amdgcn_classf(p.x, kPositiveSubnormal);
+    const bool ty = __builtin_amdgcn_classf(p.y, kPositiveSubnormal);
+    const bool tz = __builtin_amdgcn_classf(p.z, kPositiveSubnormal);
+    const bool tw = __builtin_amdgcn_classf(p.w, kPositiveSubnormal);
+
+    if (__any(tx | ty | tz | tw)) {
+        const float sum = (float)(1.0 / inverse);
+
+        p.x = tx ? e.x / sum : p.x;
+        p.y = ty ? e.y / sum : p.y;
+        p.z = tz ? e.z / sum : p.z;
+        p.w = tw ? e.w / sum : p.w;
+    }
+    return p;
 }
 
 /* The reference's left-to-right F32 sum of `width` values (a multiple of
@@ -320,10 +370,7 @@ __global__ __launch_bounds__(256) void m3_softmax_tiled_kernel(
                     p.z = v.z == INFINITY ? s.one_over_count : 0.0F;
                     p.w = v.w == INFINITY ? s.one_over_count : 0.0F;
                 } else {
-                    p.x = m3_softmax_scale(v.x, s.inverse);
-                    p.y = m3_softmax_scale(v.y, s.inverse);
-                    p.z = m3_softmax_scale(v.z, s.inverse);
-                    p.w = m3_softmax_scale(v.w, s.inverse);
+                    p = m3_softmax_scale4(v, s.inverse);
                 }
                 m3_softmax_store4<F32IO>(out, c, out_dtype, p);
             }
@@ -557,10 +604,7 @@ __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
                     if (lane * 4U + kChunk * j >= width) {
                         continue;
                     }
-                    p.x = m3_softmax_scale(e.x, inverse);
-                    p.y = m3_softmax_scale(e.y, inverse);
-                    p.z = m3_softmax_scale(e.z, inverse);
-                    p.w = m3_softmax_scale(e.w, inverse);
+                    p = m3_softmax_scale4(e, inverse);
                     m3_softmax_store4<F32IO>(out, (uint64_t)kChunk * j,
                                              out_dtype, p);
                 }

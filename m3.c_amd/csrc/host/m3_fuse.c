@@ -8,6 +8,8 @@
  * nodes) or ROUND (CAST, COPY) per node, and a STORE for every value that
  * must reach memory. A unary node is described with right == left, so the
  * register and fetch logic sees its one operand twice and counts it once.
+ * Between the passes, a group whose stores could land on memory another
+ * lane still reads is shortened (m3_fuse_group_races).
  */
 #include "m3_fuse.h"
 
@@ -196,6 +198,73 @@ static bool m3_fuse_step(const m3_fuse_graph *g, m3_fuse_registers *r,
     *r = next;
     *output_register = chosen;
     return true;
+}
+
+static uint64_t m3_fuse_element_size(m3_dtype dtype)
+{
+    return dtype == M3_DTYPE_F32 ? 4U : 2U;
+}
+
+static bool m3_fuse_overlap(const m3_fuse_value *a, const m3_fuse_value *b)
+{
+    return a->byte_count != 0U && b->byte_count != 0U &&
+           a->address < b->address + b->byte_count &&
+           b->address < a->address + a->byte_count;
+}
+
+/* A value produced in [first, end) that the group's program stores. */
+static bool m3_fuse_stored(const m3_fuse_graph *g, uint32_t value,
+                           size_t first, size_t end)
+{
+    const size_t producer = g->producer[value];
+    const size_t last = g->last_use[value];
+
+    return producer != M3_FUSE_NO_NODE && producer >= first &&
+           producer < end &&
+           (g->values[value].role != M3_GRAPH_TEMPORARY ||
+            (last != M3_FUSE_NO_NODE && last >= end));
+}
+
+/* True when the program of nodes [first, end) would store over memory
+ * that a lane other than the storing one may still read: a stored value
+ * overlapping an operand read from memory, unless both are arrays of the
+ * group's element count at one base address with one element size. */
+static bool m3_fuse_group_races(const m3_fuse_graph *g, size_t first,
+                                size_t end)
+{
+    const uint64_t count = g->values[g->nodes[first].output].element_count;
+    size_t m;
+    size_t p;
+    size_t k;
+
+    for (m = first; m < end; ++m) {
+        const uint32_t operands[2] = {g->nodes[m].left, g->nodes[m].right};
+
+        for (k = 0U; k < 2U; ++k) {
+            const m3_fuse_value *read = &g->values[operands[k]];
+
+            if (m3_fuse_in_group(g, operands[k], first, m)) {
+                continue;
+            }
+            for (p = first; p < end; ++p) {
+                const uint32_t output = g->nodes[p].output;
+                const m3_fuse_value *stored = &g->values[output];
+
+                if (!m3_fuse_stored(g, output, first, end) ||
+                    !m3_fuse_overlap(read, stored)) {
+                    continue;
+                }
+                if (read->element_count == count &&
+                    read->address == stored->address &&
+                    m3_fuse_element_size(read->dtype) ==
+                        m3_fuse_element_size(stored->dtype)) {
+                    continue;
+                }
+                return true;
+            }
+        }
+    }
+    return false;
 }
 
 static bool m3_fuse_grow(void **array, size_t *capacity, size_t needed,
@@ -479,10 +548,32 @@ m3_status m3_fuse_plan_build(const m3_fuse_value *values, size_t value_count,
     }
     (void)memset(plan, 0, sizeof(*plan));
     for (n = 0U; n < node_count; ++n) {
-        if (nodes[n].left >= value_count || nodes[n].right >= value_count ||
-            nodes[n].output >= value_count) {
+        const m3_fuse_node *node = &nodes[n];
+        bool left_read = !node->eligible;
+        bool right_read = !node->eligible;
+        uint32_t k;
+
+        if (node->read_count > M3_FUSE_MAX_READS ||
+            node->left >= value_count || node->right >= value_count ||
+            node->output >= value_count) {
             return m3_error_set(error, M3_STATUS_OUT_OF_RANGE,
                                 "fusion node %zu names a value out of range",
+                                n);
+        }
+        for (k = 0U; k < node->read_count; ++k) {
+            if (node->reads[k] >= value_count) {
+                return m3_error_set(error, M3_STATUS_OUT_OF_RANGE,
+                                    "fusion node %zu reads a value out of "
+                                    "range",
+                                    n);
+            }
+            left_read = left_read || node->reads[k] == node->left;
+            right_read = right_read || node->reads[k] == node->right;
+        }
+        if (!left_read || !right_read) {
+            return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
+                                "fusion node %zu does not list its operands "
+                                "among its reads",
                                 n);
         }
     }
@@ -506,8 +597,11 @@ m3_status m3_fuse_plan_build(const m3_fuse_value *values, size_t value_count,
         g.last_use[v] = M3_FUSE_NO_NODE;
     }
     for (n = 0U; n < node_count; ++n) {
-        g.last_use[nodes[n].left] = n;
-        g.last_use[nodes[n].right] = n;
+        uint32_t k;
+
+        for (k = 0U; k < nodes[n].read_count; ++k) {
+            g.last_use[nodes[n].reads[k]] = n;
+        }
         if (g.producer[nodes[n].output] == M3_FUSE_NO_NODE) {
             g.producer[nodes[n].output] = n;
         }
@@ -582,6 +676,9 @@ m3_status m3_fuse_plan_build(const m3_fuse_value *values, size_t value_count,
                         : 0U;
             budget_words += M3_FUSE_NODE_WORDS;
             end += 1U;
+        }
+        while (end - n >= 2U && m3_fuse_group_races(&g, n, end)) {
+            end -= 1U;
         }
         if (end - n >= 2U) {
             m3_fuse_emit_group(&g, &w, n, end);

@@ -28,7 +28,20 @@
  *   - a value produced in the group is stored unless it is a TEMPORARY
  *     whose every use is inside the group (those never reach memory);
  *   - operands produced before the group are fetched in batches of up to
- *     four arrays covering the next nodes, so their loads overlap.
+ *     four arrays covering the next nodes, so their loads overlap;
+ *   - the lanes of a program run in no particular order, so a group may
+ *     not store a value over memory that another lane may still read: a
+ *     stored value's bytes may overlap an operand the group reads from
+ *     memory only when both are arrays of the group's element count with
+ *     the same base address and element size (each lane then reads its
+ *     element before it writes the same bytes). Slots come from the
+ *     unfused liveness plan, which lets a value produced late take the
+ *     slot of one whose last reader ran earlier; a group that would store
+ *     over a periodic or scalar operand, or over an array of another
+ *     element size, is cut short before the node that makes it so.
+ * Liveness counts every value a node reads (`reads`), whatever its kind,
+ * so a value produced in a group and read later by a node that is not
+ * fused (SOFTMAX, TANH, SNAKE1D, GATED_SILU, ...) is stored.
  * Groups of one node are not formed. The per-element order of operations,
  * the operations themselves and every stored value are the unfused ones: a
  * value of a 16-bit dtype is kept in its register as the F32 a store and a
@@ -43,17 +56,28 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/* address/byte_count: where the value lives; byte_count 0 when it has no
+ * memory of its own (it then overlaps nothing). */
 typedef struct {
     m3_graph_value_role role;
     m3_dtype dtype;
     uint64_t element_count;
+    uint64_t address;
+    uint64_t byte_count;
 } m3_fuse_value;
 
-/* left_trailing / right_trailing: the operand's shape, leading ones
+#define M3_FUSE_MAX_READS 5U
+
+/* reads: every value the node reads, whatever its kind (liveness).
+ * left/right/output: the operands of a node that may fuse (a unary node
+ * has right == left); output is also the value the node writes.
+ * left_trailing / right_trailing: the operand's shape, leading ones
  * removed, equals the output's trailing dimensions, so a smaller operand
  * is a right-aligned broadcast read at e mod its element count. */
 typedef struct {
     m3_op_kind kind;
+    uint32_t reads[M3_FUSE_MAX_READS];
+    uint32_t read_count;
     uint32_t left;
     uint32_t right;
     uint32_t output;
@@ -92,7 +116,8 @@ typedef struct {
 } m3_fuse_plan;
 
 /* Plans the groups of `nodes` (execution order). Values are referenced by
- * index; every node's operands and output must be < value_count. On
+ * index; every node's reads, operands and output must be < value_count,
+ * and an eligible node's left and right must be among its reads. On
  * success *plan owns its arrays (free with m3_fuse_plan_free); a plan
  * with no groups is valid. */
 m3_status m3_fuse_plan_build(const m3_fuse_value *values, size_t value_count,

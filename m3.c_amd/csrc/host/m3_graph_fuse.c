@@ -241,15 +241,34 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
                             "cannot allocate fusion planner input");
     }
     for (v = 0U; v < session->value_count; ++v) {
+        const m3_tensor_view *view = &session->views[v];
+
         fuse_values[v].role = session->values[v].description.role;
         fuse_values[v].dtype = session->values[v].metadata.dtype;
         fuse_values[v].element_count =
             (uint64_t)session->values[v].metadata.element_count;
+        fuse_values[v].address =
+            (uint64_t)(uintptr_t)m3_storage_device_data(view->storage) +
+            (uint64_t)view->byte_offset;
+        fuse_values[v].byte_count =
+            (uint64_t)session->values[v].metadata.byte_count;
     }
     for (n = 0U; n < session->node_count; ++n) {
         const m3_graph_node_desc *node = &graph->nodes[n];
+        size_t i;
 
         fuse_nodes[n].kind = node->kind;
+        /* every value the node reads counts for liveness, fused or not */
+        for (i = 0U; i < M3_GRAPH_NODE_INPUT_CAPACITY &&
+                     i < M3_FUSE_MAX_READS &&
+                     node->inputs[i] != M3_GRAPH_VALUE_NONE;
+             ++i) {
+            fuse_nodes[n].reads[i] = (uint32_t)node->inputs[i];
+        }
+        fuse_nodes[n].read_count = (uint32_t)i;
+        fuse_nodes[n].output = (uint32_t)node->outputs[0];
+        fuse_nodes[n].left = fuse_nodes[n].output;
+        fuse_nodes[n].right = fuse_nodes[n].output;
         if (m3_op_binary_of(&session->commands[n]) != NULL) {
             const m3_tensor_metadata *output =
                 &session->values[node->outputs[0]].metadata;

@@ -3,16 +3,25 @@
  * planner (m3.c_amd/csrc/host/m3_fuse.c) and of the program format it
  * emits (m3_hip_launch_program in include/m3_hip.h).
  *
- * A graph is executed twice on the host: node by node, and with every
- * group the planner forms replaced by its program, interpreted per element
- * exactly as the kernel does (registers R0-R3 and F0-F3, FETCH, OP, ROUND,
- * STORE; m3_binary_f32_bits for each operation, m3_round_through_bits for
- * the rounding dtype, conversions on load and store). Each value gets its own buffer;
- * buffers the node-by-node run writes start as a sentinel NaN in the fused
- * run, so a missing STORE or a read of an unwritten register shows. Every
- * value that must reach memory (OUTPUT values, values read outside their
- * producer's group, INPUT and CONSTANT values) is compared bit for bit.
- * The words are also checked structurally (the rules of the launcher).
+ * A graph is executed node by node with one buffer per value (the
+ * expected values), and then with every group the planner forms replaced
+ * by its program, interpreted per element exactly as the kernel does
+ * (registers R0-R3 and F0-F3, FETCH, OP, ROUND, STORE; m3_binary_f32_bits
+ * for each operation, m3_round_through_bits for the rounding dtype,
+ * conversions on load and store). The fused run works on one byte memory
+ * in which every value sits in the slot the session compiler's liveness
+ * plan gives it (INPUT, CONSTANT and OUTPUT values own a slot; a TEMPORARY
+ * takes the smallest slot free before its producer that is large enough),
+ * so values whose lives do not overlap share bytes as on the device. A
+ * program's lanes run in no fixed order, so the fused run is made twice,
+ * once over the elements in increasing and once in decreasing order: a
+ * store that lands on bytes another element still reads changes the
+ * result in one of the two. Before every node or program the values it
+ * reads from memory must hold their expected bits; after it, every value
+ * it stored that must reach memory (OUTPUT values, values read outside
+ * their producer's group) must too, and so must every OUTPUT value at the
+ * end. The words are also checked structurally (the rules of the
+ * launcher).
  *
  * Modes (one JSON line on stdout; exit status 1 on any mismatch):
  *   fuse_check random <graphs> <seed> [planted]
@@ -23,10 +32,18 @@
  *       output's) is a trailing broadcast, read at e mod its count, or,
  *       when the node does not mark it trailing, a leading one, read at
  *       e / (output count / its count); only the first kind may fuse.
- *       `planted` corrupts each plan before it runs (the first STORE is
- *       turned into a store of another register, the sources of every
- *       SUB/DIV are swapped, OPs lose their rounding dtype and periodic
- *       operands their period): the comparison must then fail.
+ *       Nodes of kinds that never fuse (SOFTMAX with one input,
+ *       GATED_SILU with two) read values between the groups.
+ *       The last argument plants a mistake, and the comparison must then
+ *       fail:
+ *         `planted` corrupts each plan before it runs (the first STORE is
+ *         turned into a store of another register, the sources of every
+ *         SUB/DIV are swapped, OPs lose their rounding dtype and periodic
+ *         operands their period);
+ *         `unaware` hides where values live from the planner (no address
+ *         ranges), so it cannot see a store landing on an operand's bytes;
+ *         `blind` hides the reads of the nodes that never fuse from the
+ *         planner, so it keeps values they read in registers only.
  *   fuse_check euler <steps>
  *       The Euler CFG graph of the flow solver, 6 nodes per step; reports
  *       the plan's shape and checks its result.
@@ -50,7 +67,15 @@ typedef struct {
     size_t node_count;
     size_t node_capacity;
     uint32_t **data; /* per value: element_count raw elements */
+    uint8_t *memory; /* when set, values live here, at their address */
 } graph_t;
+
+typedef enum {
+    PLANT_NONE,
+    PLANT_CODE,
+    PLANT_UNAWARE,
+    PLANT_BLIND
+} plant_t;
 
 static uint64_t rng_state;
 
@@ -97,7 +122,11 @@ static void add_node(graph_t *g, m3_op_kind kind, uint32_t left,
 {
     g->nodes = grow(g->nodes, &g->node_capacity, g->node_count + 1U,
                     sizeof(*g->nodes));
+    memset(&g->nodes[g->node_count], 0, sizeof(*g->nodes));
     g->nodes[g->node_count].kind = kind;
+    g->nodes[g->node_count].reads[0] = left;
+    g->nodes[g->node_count].reads[1] = right;
+    g->nodes[g->node_count].read_count = left == right ? 1U : 2U;
     g->nodes[g->node_count].left = left;
     g->nodes[g->node_count].right = right;
     g->nodes[g->node_count].output = output;
@@ -105,6 +134,129 @@ static void add_node(graph_t *g, m3_op_kind kind, uint32_t left,
     g->nodes[g->node_count].left_trailing = false;
     g->nodes[g->node_count].right_trailing = false;
     g->node_count += 1U;
+}
+
+/* A node of a kind that never fuses, reading `left` and `right` (one value
+ * when they are equal). */
+static bool opaque(const m3_fuse_node *node)
+{
+    return node->kind == M3_OP_SOFTMAX || node->kind == M3_OP_GATED_SILU;
+}
+
+static uint64_t element_size(m3_dtype dtype)
+{
+    return dtype == M3_DTYPE_F32 ? 4U : 2U;
+}
+
+/* Raw element `index` of a value: from its buffer, or from the memory at
+ * the value's address during the fused run. */
+static uint32_t load_raw(const graph_t *g, uint32_t value, uint64_t index)
+{
+    const m3_fuse_value *v = &g->values[value];
+    const uint8_t *at;
+
+    if (g->memory == NULL) {
+        return g->data[value][index];
+    }
+    at = g->memory + v->address + index * element_size(v->dtype);
+    return element_size(v->dtype) == 4U
+               ? (uint32_t)at[0] | ((uint32_t)at[1] << 8U) |
+                     ((uint32_t)at[2] << 16U) | ((uint32_t)at[3] << 24U)
+               : (uint32_t)at[0] | ((uint32_t)at[1] << 8U);
+}
+
+static void store_raw(graph_t *g, uint32_t value, uint64_t index,
+                      uint32_t bits)
+{
+    const m3_fuse_value *v = &g->values[value];
+    uint8_t *at;
+
+    if (g->memory == NULL) {
+        g->data[value][index] = bits;
+        return;
+    }
+    at = g->memory + v->address + index * element_size(v->dtype);
+    for (uint64_t b = 0U; b < element_size(v->dtype); ++b) {
+        at[b] = (uint8_t)(bits >> (8U * b));
+    }
+}
+
+/* Slots as the session compiler plans them (src/m3_graph_compile.c:
+ * 260-324 of the reference): INPUT, CONSTANT and OUTPUT values own one;
+ * a TEMPORARY produced by node n takes the smallest slot whose last user
+ * ran before n and that is large enough, else a new one. Slots are laid
+ * out 64-byte aligned from address 4096. Returns the memory size. */
+static uint64_t plan_memory(graph_t *g)
+{
+    const size_t count = g->value_count;
+    uint64_t *slot_bytes = calloc(count, sizeof(*slot_bytes));
+    uint64_t *slot_at = calloc(count, sizeof(*slot_at));
+    size_t *busy = calloc(count, sizeof(*busy));
+    size_t *slot_of = calloc(count, sizeof(*slot_of));
+    size_t *last = calloc(count, sizeof(*last));
+    size_t *producer = calloc(count, sizeof(*producer));
+    size_t slots = 0U;
+    uint64_t end = 4096U;
+
+    if (slot_bytes == NULL || slot_at == NULL || busy == NULL ||
+        slot_of == NULL || last == NULL || producer == NULL) {
+        fprintf(stderr, "out of memory\n");
+        exit(2);
+    }
+    for (size_t v = 0U; v < count; ++v) {
+        producer[v] = SIZE_MAX;
+        last[v] = 0U;
+    }
+    for (size_t n = 0U; n < g->node_count; ++n) {
+        for (uint32_t k = 0U; k < g->nodes[n].read_count; ++k) {
+            last[g->nodes[n].reads[k]] = n;
+        }
+        producer[g->nodes[n].output] = n;
+        last[g->nodes[n].output] = n;
+    }
+    for (size_t v = 0U; v < count; ++v) {
+        g->values[v].byte_count = g->values[v].element_count *
+                                  element_size(g->values[v].dtype);
+        if (g->values[v].role != M3_GRAPH_TEMPORARY) {
+            slot_bytes[slots] = g->values[v].byte_count;
+            busy[slots] = SIZE_MAX;
+            slot_of[v] = slots++;
+        }
+    }
+    for (size_t n = 0U; n < g->node_count; ++n) {
+        const uint32_t v = g->nodes[n].output;
+        size_t best = SIZE_MAX;
+
+        if (g->values[v].role != M3_GRAPH_TEMPORARY || producer[v] != n) {
+            continue;
+        }
+        for (size_t s = 0U; s < slots; ++s) {
+            if (busy[s] < n && slot_bytes[s] >= g->values[v].byte_count &&
+                (best == SIZE_MAX || slot_bytes[s] < slot_bytes[best])) {
+                best = s;
+            }
+        }
+        if (best == SIZE_MAX) {
+            slot_bytes[slots] = g->values[v].byte_count;
+            best = slots++;
+        }
+        slot_of[v] = best;
+        busy[best] = last[v];
+    }
+    for (size_t s = 0U; s < slots; ++s) {
+        slot_at[s] = end;
+        end += (slot_bytes[s] + 63U) & ~(uint64_t)63U;
+    }
+    for (size_t v = 0U; v < count; ++v) {
+        g->values[v].address = slot_at[slot_of[v]];
+    }
+    free(slot_bytes);
+    free(slot_at);
+    free(busy);
+    free(slot_of);
+    free(last);
+    free(producer);
+    return end;
 }
 
 /* Random F32 bits: mostly normal values near 1, with zeros, infinities,
@@ -132,7 +284,7 @@ static uint32_t random_f32(void)
 /* Element `index` of a value, as F32 bits. */
 static uint32_t load_f32(const graph_t *g, uint32_t value, uint64_t index)
 {
-    return m3_load_as_f32_bits(g->data[value][index],
+    return m3_load_as_f32_bits(load_raw(g, value, index),
                                (uint32_t)g->values[value].dtype);
 }
 
@@ -171,10 +323,27 @@ static void run_node(graph_t *g, size_t n)
 
         if ((node->kind == M3_OP_COPY || node->kind == M3_OP_CAST) &&
             g->values[node->left].dtype == out->dtype) {
-            g->data[node->output][e] = g->data[node->left][e];
+            store_raw(g, node->output, e, load_raw(g, node->left, e));
             continue;
         }
-        if (node->kind == M3_OP_CAST) {
+        if (opaque(node)) {
+            /* any fixed function of the inputs: x*x, or x*x + y */
+            const uint32_t a = node->reads[0];
+            const uint32_t b = node->reads[node->read_count - 1U];
+            const uint32_t x = load_f32(
+                g, a,
+                broadcast_index(g->values[a].element_count,
+                                out->element_count, false, e));
+            const uint32_t y = load_f32(
+                g, b,
+                broadcast_index(g->values[b].element_count,
+                                out->element_count, false, e));
+
+            result = m3_binary_f32_bits(M3N_MUL, x, x);
+            if (node->read_count == 2U) {
+                result = m3_binary_f32_bits(M3N_ADD, result, y);
+            }
+        } else if (node->kind == M3_OP_CAST) {
             result = load_f32(g, node->left, e);
         } else {
             const uint64_t lc = g->values[node->left].element_count;
@@ -189,8 +358,8 @@ static void run_node(graph_t *g, size_t n)
                          broadcast_index(rc, out->element_count,
                                          node->right_trailing, e)));
         }
-        g->data[node->output][e] =
-            m3_store_from_f32_bits(result, (uint32_t)out->dtype);
+        store_raw(g, node->output, e,
+                  m3_store_from_f32_bits(result, (uint32_t)out->dtype));
     }
 }
 
@@ -296,16 +465,18 @@ static size_t check_words(const m3_fuse_plan *plan, const m3_fuse_group *gr,
     return bad;
 }
 
-/* The group's program over every element, as the kernel runs it. */
+/* The group's program over every element, as the kernel runs it, the
+ * elements taken in increasing or in decreasing order. */
 static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
-                          const m3_fuse_group *gr)
+                          const m3_fuse_group *gr, bool decreasing)
 {
     const uint32_t *code = plan->code + gr->code_first;
     const m3_fuse_operand *operands = plan->operands + gr->operand_first;
     size_t unwritten = 0U;
-    uint64_t e;
+    uint64_t i;
 
-    for (e = 0U; e < gr->element_count; ++e) {
+    for (i = 0U; i < gr->element_count; ++i) {
+        const uint64_t e = decreasing ? gr->element_count - 1U - i : i;
         uint32_t r[4] = {SENTINEL, SENTINEL, SENTINEL, SENTINEL};
         uint32_t f[4] = {SENTINEL, SENTINEL, SENTINEL, SENTINEL};
         bool r_set[4] = {false, false, false, false};
@@ -362,8 +533,9 @@ static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
                 uint32_t src = (w >> 4U) & 3U;
                 uint32_t target = operands[(w >> 8U) & 0xffU].value;
 
-                g->data[target][e] = m3_store_from_f32_bits(
-                    r[src], (uint32_t)g->values[target].dtype);
+                store_raw(g, target, e,
+                          m3_store_from_f32_bits(
+                              r[src], (uint32_t)g->values[target].dtype));
                 unwritten += !r_set[src];
                 pc += 1U;
             }
@@ -375,7 +547,7 @@ static size_t run_program(graph_t *g, const m3_fuse_plan *plan,
 /* Corrupts a plan: the first STORE stores another register, the sources
  * of every SUB and DIV are swapped, no OP rounds through its output's
  * 16-bit dtype, and periodic operands lose their period. */
-static void plant(m3_fuse_plan *plan)
+static void plant_code(m3_fuse_plan *plan)
 {
     bool first = true;
 
@@ -420,19 +592,21 @@ typedef struct {
     size_t internal;
     size_t compared;
     size_t mismatches;
+    size_t stale;     /* a node or program read bytes not holding its operand */
     size_t structure;
     size_t unwritten;
     size_t rounds;         /* ROUND instructions (fused CAST/COPY) */
     size_t rounding_ops;   /* OP instructions with a 16-bit rounding */
     size_t narrow_operands; /* F16/BF16 operands of programs */
     size_t periodic_operands; /* operands read with a period */
+    size_t shared_slots;   /* program operands whose slot a store reuses */
 } stats_t;
 
 static void allocate_data(graph_t *g, uint32_t **data)
 {
     for (size_t v = 0U; v < g->value_count; ++v) {
         data[v] = malloc((size_t)g->values[v].element_count *
-                         sizeof(uint32_t));
+                         sizeof(uint32_t) + sizeof(uint32_t));
         if (data[v] == NULL) {
             fprintf(stderr, "out of memory\n");
             exit(2);
@@ -440,24 +614,73 @@ static void allocate_data(graph_t *g, uint32_t **data)
     }
 }
 
-/* Plans g, runs it both ways and compares. */
-static void check_graph(graph_t *g, bool planted, stats_t *st)
+/* The fused run's memory holds value v's expected bits. */
+static bool holds(const graph_t *g, uint32_t **expected, uint32_t v)
 {
-    uint32_t **reference = calloc(g->value_count, sizeof(*reference));
-    uint32_t **fused = calloc(g->value_count, sizeof(*fused));
+    for (uint64_t e = 0U; e < g->values[v].element_count; ++e) {
+        if (load_raw(g, v, e) != expected[v][e]) {
+            return false;
+        }
+    }
+    return true;
+}
+
+static bool node_reads(const m3_fuse_node *node, uint32_t v)
+{
+    for (uint32_t k = 0U; k < node->read_count; ++k) {
+        if (node->reads[k] == v) {
+            return true;
+        }
+    }
+    return false;
+}
+
+/* What the planner is told: the graph, or the graph with a mistake of the
+ * caller planted (no address ranges; no reads for nodes that never fuse,
+ * whose records are then all zero). */
+static void describe(const graph_t *g, plant_t plant, m3_fuse_value *values,
+                     m3_fuse_node *nodes)
+{
+    memcpy(values, g->values, g->value_count * sizeof(*values));
+    memcpy(nodes, g->nodes, g->node_count * sizeof(*nodes));
+    for (size_t v = 0U; plant == PLANT_UNAWARE && v < g->value_count; ++v) {
+        values[v].address = 0U;
+        values[v].byte_count = 0U;
+    }
+    for (size_t n = 0U; plant == PLANT_BLIND && n < g->node_count; ++n) {
+        if (opaque(&nodes[n])) {
+            memset(&nodes[n], 0, sizeof(nodes[n]));
+            nodes[n].kind = g->nodes[n].kind;
+        }
+    }
+}
+
+/* Plans g, runs it node by node and fused, and compares. */
+static void check_graph(graph_t *g, plant_t plant, stats_t *st)
+{
+    const uint64_t memory_bytes = plan_memory(g);
+    uint32_t **expected = calloc(g->value_count, sizeof(*expected));
     size_t *group_of = malloc(g->node_count * sizeof(*group_of));
+    size_t *producer = malloc(g->value_count * sizeof(*producer));
+    m3_fuse_value *told_values = malloc(g->value_count * sizeof(*told_values));
+    m3_fuse_node *told_nodes = malloc(g->node_count * sizeof(*told_nodes));
     m3_fuse_plan plan;
     m3_error error;
     size_t v;
     size_t n;
 
-    allocate_data(g, reference);
-    allocate_data(g, fused);
+    if (expected == NULL || group_of == NULL || producer == NULL ||
+        told_values == NULL || told_nodes == NULL) {
+        fprintf(stderr, "out of memory\n");
+        exit(2);
+    }
+    allocate_data(g, expected);
     for (v = 0U; v < g->value_count; ++v) {
         const m3_fuse_value *val = &g->values[v];
         bool given = val->role == M3_GRAPH_INPUT ||
                      val->role == M3_GRAPH_CONSTANT;
 
+        producer[v] = SIZE_MAX;
         for (uint64_t e = 0U; e < val->element_count; ++e) {
             uint32_t bits = random_f32();
 
@@ -466,17 +689,20 @@ static void check_graph(graph_t *g, bool planted, stats_t *st)
             } else if (val->dtype == M3_DTYPE_BF16) {
                 bits = m3_f32_to_bf16_bits(bits);
             }
-            reference[v][e] = given ? bits : SENTINEL;
-            fused[v][e] = reference[v][e];
+            expected[v][e] = given ? bits : SENTINEL;
         }
     }
-    if (m3_fuse_plan_build(g->values, g->value_count, g->nodes,
+    for (n = 0U; n < g->node_count; ++n) {
+        producer[g->nodes[n].output] = n;
+    }
+    describe(g, plant, told_values, told_nodes);
+    if (m3_fuse_plan_build(told_values, g->value_count, told_nodes,
                            g->node_count, &plan, &error) != M3_STATUS_OK) {
         fprintf(stderr, "plan failed: %s\n", error.message);
         exit(2);
     }
-    if (planted) {
-        plant(&plan);
+    if (plant == PLANT_CODE) {
+        plant_code(&plan);
     }
     for (n = 0U; n < g->node_count; ++n) {
         group_of[n] = NO_GROUP;
@@ -502,65 +728,99 @@ static void check_graph(graph_t *g, bool planted, stats_t *st)
             st->narrow_operands +=
                 g->values[o->value].dtype != M3_DTYPE_F32;
             st->periodic_operands += o->period != 0U;
+            for (size_t q = 0U; q < gr->operand_count; ++q) {
+                const m3_fuse_operand *w =
+                    &plan.operands[gr->operand_first + q];
+
+                st->shared_slots +=
+                    q != p &&
+                    g->values[o->value].address ==
+                        g->values[w->value].address;
+            }
         }
         for (n = gr->first_node; n < gr->first_node + gr->node_count; ++n) {
             group_of[n] = gi;
         }
     }
-    g->data = reference;
+    g->data = expected;
+    g->memory = NULL;
     for (n = 0U; n < g->node_count; ++n) {
         run_node(g, n);
     }
-    g->data = fused;
-    n = 0U;
-    while (n < g->node_count) {
-        if (group_of[n] != NO_GROUP) {
-            const m3_fuse_group *gr = &plan.groups[group_of[n]];
-
-            st->unwritten += run_program(g, &plan, gr);
-            n = gr->first_node + gr->node_count;
-        } else {
-            run_node(g, n);
-            n += 1U;
+    for (int pass = 0; pass < 2; ++pass) {
+        g->memory = malloc(memory_bytes);
+        if (g->memory == NULL) {
+            fprintf(stderr, "out of memory\n");
+            exit(2);
         }
-    }
-    for (v = 0U; v < g->value_count; ++v) {
-        const m3_fuse_value *val = &g->values[v];
-        size_t producer = SIZE_MAX;
-        bool needed = val->role != M3_GRAPH_TEMPORARY;
-
-        for (n = 0U; n < g->node_count; ++n) {
-            if (g->nodes[n].output == v) {
-                producer = n;
+        memset(g->memory, 0xa5, memory_bytes);
+        for (v = 0U; v < g->value_count; ++v) {
+            if (g->values[v].role == M3_GRAPH_INPUT ||
+                g->values[v].role == M3_GRAPH_CONSTANT) {
+                for (uint64_t e = 0U; e < g->values[v].element_count; ++e) {
+                    store_raw(g, (uint32_t)v, e, expected[v][e]);
+                }
             }
         }
-        for (n = 0U; n < g->node_count && !needed; ++n) {
-            const m3_fuse_node *node = &g->nodes[n];
+        n = 0U;
+        while (n < g->node_count) {
+            size_t first = n;
+            size_t end = n + 1U;
 
-            if ((node->left == v || node->right == v) &&
-                (producer == SIZE_MAX || group_of[n] == NO_GROUP ||
-                 group_of[n] != group_of[producer])) {
-                needed = true;
+            if (group_of[n] != NO_GROUP) {
+                const m3_fuse_group *gr = &plan.groups[group_of[n]];
+
+                end = gr->first_node + gr->node_count;
+                for (size_t p = 0U; p < gr->operand_count; ++p) {
+                    uint32_t o = plan.operands[gr->operand_first + p].value;
+
+                    if ((producer[o] == SIZE_MAX || producer[o] < first ||
+                         producer[o] >= end) &&
+                        !holds(g, expected, o)) {
+                        st->stale += 1U;
+                    }
+                }
+                st->unwritten += run_program(g, &plan, gr, pass == 1);
+            } else {
+                for (uint32_t k = 0U; k < g->nodes[n].read_count; ++k) {
+                    st->stale += !holds(g, expected, g->nodes[n].reads[k]);
+                }
+                run_node(g, n);
+            }
+            /* every value produced here that must reach memory */
+            for (size_t m = first; m < end; ++m) {
+                const uint32_t out = g->nodes[m].output;
+                bool needed = g->values[out].role != M3_GRAPH_TEMPORARY;
+
+                for (size_t r = end; r < g->node_count && !needed; ++r) {
+                    needed = node_reads(&g->nodes[r], out);
+                }
+                if (!needed) {
+                    st->internal += pass == 0 && group_of[m] != NO_GROUP;
+                    continue;
+                }
+                st->compared += 1U;
+                st->mismatches += !holds(g, expected, out);
+            }
+            n = end;
+        }
+        for (v = 0U; v < g->value_count; ++v) {
+            if (g->values[v].role == M3_GRAPH_OUTPUT) {
+                st->compared += 1U;
+                st->mismatches += !holds(g, expected, (uint32_t)v);
             }
         }
-        if (!needed) {
-            st->internal += producer != SIZE_MAX &&
-                            group_of[producer] != NO_GROUP;
-            continue;
-        }
-        st->compared += 1U;
-        if (memcmp(reference[v], fused[v],
-                   (size_t)val->element_count * sizeof(uint32_t)) != 0) {
-            st->mismatches += 1U;
-        }
+        free(g->memory);
+        g->memory = NULL;
     }
     for (v = 0U; v < g->value_count; ++v) {
-        free(reference[v]);
-        free(fused[v]);
+        free(expected[v]);
     }
-    free(reference);
-    free(fused);
+    free(expected);
     free(group_of);
+    free(producer);
+    free(told_values);
+    free(told_nodes);
     m3_fuse_plan_free(&plan);
 }
 
@@ -631,6 +891,16 @@ static void random_graph(graph_t *g)
             add_node(g, M3_OP_CAST, left, left, out, below(100U) >= 5U);
             continue;
         }
+        if (unary < 28U) {
+            /* a node that never fuses, reading one or two values */
+            const bool two = below(2U) != 0U;
+            uint32_t out = add_value(g, role, floats[below(3U)],
+                                     two && rc > lc ? rc : lc);
+
+            add_node(g, two ? M3_OP_GATED_SILU : M3_OP_SOFTMAX, left,
+                     two ? right : left, out, below(2U) != 0U);
+            continue;
+        }
         add_node(g, kinds[below(4U)], left, right,
                  add_value(g, role, dtype, lc > rc ? lc : rc),
                  below(100U) >= 5U);
@@ -687,11 +957,12 @@ static void print_stats(const char *mode, size_t graphs, const stats_t *st)
            "\"compared_values\": %zu, \"mismatches\": %zu, "
            "\"structure_errors\": %zu, \"unwritten_reads\": %zu, "
            "\"rounds\": %zu, \"rounding_ops\": %zu, "
-           "\"narrow_operands\": %zu, \"periodic_operands\": %zu",
+           "\"narrow_operands\": %zu, \"periodic_operands\": %zu, "
+           "\"stale_reads\": %zu, \"shared_slots\": %zu",
            mode, graphs, st->groups, st->fused_nodes, st->stores,
            st->internal, st->compared, st->mismatches, st->structure,
            st->unwritten, st->rounds, st->rounding_ops, st->narrow_operands,
-           st->periodic_operands);
+           st->periodic_operands, st->stale, st->shared_slots);
 }
 
 int main(int argc, char **argv)
@@ -701,20 +972,24 @@ int main(int argc, char **argv)
     memset(&st, 0, sizeof(st));
     if (argc >= 4 && strcmp(argv[1], "random") == 0) {
         size_t graphs = strtoull(argv[2], NULL, 10);
-        bool planted = argc >= 5 && strcmp(argv[4], "planted") == 0;
+        const char *mode = argc >= 5 ? argv[4] : "random";
+        plant_t plant = strcmp(mode, "planted") == 0   ? PLANT_CODE
+                        : strcmp(mode, "unaware") == 0 ? PLANT_UNAWARE
+                        : strcmp(mode, "blind") == 0   ? PLANT_BLIND
+                                                       : PLANT_NONE;
 
         rng_state = strtoull(argv[3], NULL, 10);
         for (size_t i = 0U; i < graphs; ++i) {
             graph_t g;
 
             random_graph(&g);
-            check_graph(&g, planted, &st);
+            check_graph(&g, plant, &st);
             free_graph(&g);
         }
-        print_stats(planted ? "planted" : "random", graphs, &st);
+        print_stats(plant == PLANT_NONE ? "random" : mode, graphs, &st);
         printf("}\n");
-        return st.mismatches == 0U && st.structure == 0U &&
-                       st.unwritten == 0U
+        return st.mismatches == 0U && st.stale == 0U &&
+                       st.structure == 0U && st.unwritten == 0U
                    ? 0
                    : 1;
     }
@@ -747,7 +1022,7 @@ int main(int argc, char **argv)
                 }
             }
         }
-        check_graph(&g, false, &st);
+        check_graph(&g, PLANT_NONE, &st);
         print_stats("euler", 1U, &st);
         printf(", \"first_group_nodes\": %zu, \"first_group_operands\": %zu, "
                "\"first_group_words\": %zu, \"fetched_arrays\": %zu}\n",
@@ -757,12 +1032,13 @@ int main(int argc, char **argv)
                fetch_loads);
         m3_fuse_plan_free(&plan);
         free_graph(&g);
-        return st.mismatches == 0U && st.structure == 0U &&
-                       st.unwritten == 0U
+        return st.mismatches == 0U && st.stale == 0U &&
+                       st.structure == 0U && st.unwritten == 0U
                    ? 0
                    : 1;
     }
-    fprintf(stderr, "usage: fuse_check random <graphs> <seed> [planted] | "
+    fprintf(stderr, "usage: fuse_check random <graphs> <seed> "
+                    "[planted|unaware|blind] | "
                     "euler <steps>\n");
     return 2;
 }

@@ -33,6 +33,11 @@ static size_t g_fail_allocation_at; /* 0: never */
 static size_t g_reserved;
 static size_t g_programs;
 static size_t g_periodic; /* periodic operands of the programs run */
+/* Programs run their elements in increasing order, or in decreasing order
+ * when set: a device runs a program's lanes in no fixed order, and a
+ * store that lands on bytes another element still reads changes the
+ * result in one of the two. */
+static int g_decreasing;
 
 void oracle_backend_reset(void);
 size_t oracle_backend_log(int *kinds, int *lists, size_t capacity);
@@ -41,6 +46,7 @@ size_t oracle_backend_reserved(void);
 void oracle_backend_fail_allocation_at(size_t index);
 size_t oracle_backend_programs(void);
 size_t oracle_backend_periodic(void);
+void oracle_backend_set_program_order(int decreasing);
 m3_status oracle_backend_create(m3_backend **backend, m3_error *error);
 
 void oracle_backend_reset(void)
@@ -52,6 +58,11 @@ void oracle_backend_reset(void)
     g_reserved = 0U;
     g_programs = 0U;
     g_periodic = 0U;
+}
+
+void oracle_backend_set_program_order(int decreasing)
+{
+    g_decreasing = decreasing;
 }
 
 size_t oracle_backend_programs(void)
@@ -242,7 +253,8 @@ static uint32_t round_through(uint32_t bits, uint32_t dtype)
                                   : bits;
 }
 
-/* Runs an elementwise program (layout in m3_hip.h) element by element. */
+/* Runs an elementwise program (layout in m3_hip.h) element by element, in
+ * the order g_decreasing selects. */
 static int run_program(const m3_op_elementwise_program *program)
 {
     const uint32_t *words = program->words;
@@ -255,7 +267,7 @@ static int run_program(const m3_op_elementwise_program *program)
     const uint32_t *code = periods + 2U * period_count;
     const uint8_t *stored =
         (const uint8_t *)m3_storage_data(program->storage);
-    uint64_t e;
+    uint64_t i;
 
     if (stored == NULL ||
         memcmp(stored + program->byte_offset, words,
@@ -264,7 +276,8 @@ static int run_program(const m3_op_elementwise_program *program)
             8U + 2U * operand_count + 2U * period_count + code_words) {
         return (int)M3_STATUS_INTERNAL;
     }
-    for (e = 0U; e < count; ++e) {
+    for (i = 0U; i < count; ++i) {
+        const uint64_t e = g_decreasing ? count - 1U - i : i;
         uint32_t r[4] = {0U, 0U, 0U, 0U};
         uint32_t f[4] = {0U, 0U, 0U, 0U};
         uint32_t pc = 0U;

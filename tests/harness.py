@@ -272,3 +272,63 @@ def f32_bits(values):
 
 def bits_f32(bits):
     return np.asarray(bits, dtype=np.uint32).view(np.float32)
+
+
+# Row sums z (a count of zero logits, each e = 1) for which RN_f64(1/z) is
+# far enough from 1/z that RN_f32(e * RN_f64(1/z)) misses the tie of some
+# subnormal quotients e / z = (2k+1) * 2^-150 (found by enumerating every
+# even z below 300; smaller ones round back onto the tie).
+TIE_SUMS = (98, 150, 154, 182, 186, 198)
+
+
+def _tie_logits(rng, z, count):
+    """Up to `count` logits v with expf(v) = e subnormal and e / z an exact
+    rounding midpoint that the product with the reciprocal rounds the wrong
+    way."""
+    import ctypes
+    import ctypes.util
+
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    m = z // 2
+    k = rng.integers(0, (1 << 16) // m, 8 * count + 64).astype(np.int64)
+    a = m * (2 * k + 1)
+    product = (a * 2.0 ** -149 * (1.0 / np.float64(z))).astype(np.float32)
+    correct = np.where(k % 2 == 0, k, k + 1)  # the even neighbour
+    wrong = a[product.view(np.uint32).astype(np.int64) != correct]
+    found = []
+    for target in wrong:
+        guess = np.float32(np.log(float(target) * 2.0 ** -149))
+        for step in range(-6, 7):
+            v = np.uint32(int(guess.view(np.uint32)) + step).view(np.float32)
+            e = np.float32(libm.expf(float(v)))
+            if int(e.view(np.uint32)) == int(target):
+                found.append(v)
+                break
+        if len(found) == count:
+            break
+    return np.array(found, np.float32)
+
+
+def subnormal_tie_rows(rng, rows, width):
+    """Softmax rows whose quotients e_j / sum fall exactly on rounding
+    midpoints of the F32 subnormal range: z zeros (each e = 1, so sum = z
+    exactly, z from TIE_SUMS) followed by logits whose e_j = expf(v) is a
+    subnormal with e_j / z = (2k+1) * 2^-150, chosen where a product with
+    the reciprocal in double rounds the other way, then -inf. Row 0 is
+    [98 zeros, -0x1.892ae8p+6, -inf...] (147 * 2^-149 / 98 = 3 * 2^-150).
+    Needs width >= 100."""
+    sums = [z for z in TIE_SUMS if z + 2 <= width]
+    assert sums, "tie rows need width >= 100"
+    logits = np.full((rows, width), -np.inf, np.float32)
+    for r in range(rows):
+        z = sums[r % len(sums)]
+        logits[r, :z] = 0.0
+        ties = _tie_logits(rng, z, min(64, (width - z) * 3 // 4))
+        logits[r, z:z + ties.size] = ties
+        rng.shuffle(logits[r, :z + ties.size])
+    logits[0, :] = -np.inf
+    logits[0, :98] = 0.0
+    logits[0, 98] = np.float32(float.fromhex("-0x1.892ae8p+6"))
+    return logits

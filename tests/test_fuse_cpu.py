@@ -10,9 +10,16 @@ group replaced by its program interpreted the way the kernel runs it. Every
 value that has to reach memory must agree bit for bit, NaN payloads
 included. Operands smaller than the output are broadcast along trailing
 axes (read at e mod their count, the only kind that may fuse) or leading
-ones. A plan with planted mistakes (a STORE of the wrong register, SUB and
-DIV with swapped operands, periodic operands read without their period)
-must be caught by the same comparison.
+ones. Values live in the slots of the session compiler's liveness plan, so
+values whose lives do not overlap share bytes, and each program runs over
+its elements in increasing and then decreasing order (a device's lanes run
+in no fixed order). Nodes that never fuse (SOFTMAX, GATED_SILU) read values
+between the groups. A plan with planted mistakes (a STORE of the wrong
+register, SUB and DIV with swapped operands, periodic operands read without
+their period) must be caught by the same comparison, and so must a planner
+that is not told where values live (it would store over an operand other
+elements still read) or what the non-fusing nodes read (it would keep
+their inputs in registers only).
 """
 import json
 import os
@@ -55,8 +62,12 @@ def test_random_plans_match_node_by_node():
     for seed in (1, 2):
         r = run("random", "3000", str(seed))
         assert r["mismatches"] == 0
+        assert r["stale_reads"] == 0
         assert r["structure_errors"] == 0
         assert r["unwritten_reads"] == 0
+        # programs do read and write arrays that share a slot (same base,
+        # same element size: each element is read before it is written)
+        assert r["shared_slots"] > 500
         # the graphs do fuse, and fused temporaries stay out of memory
         assert r["groups"] > 5000
         assert r["internal_values"] > 5000
@@ -74,6 +85,22 @@ def test_planted_plan_mistakes_are_detected():
     assert r["mismatches"] > 100
     # a periodic operand without its period breaks the launcher's rules
     assert r["structure_errors"] > 100
+
+
+def test_planner_that_ignores_shared_slots_is_detected():
+    """Without address ranges the planner fuses runs whose stores land on
+    a periodic or scalar operand, or on an operand of another element
+    size, in a slot the liveness plan shares: one of the two element
+    orders then reads overwritten bytes."""
+    r = run("random", "3000", "1", "unaware", expect_ok=False)
+    assert r["mismatches"] + r["stale_reads"] > 100
+
+
+def test_planner_that_ignores_unfused_readers_is_detected():
+    """A planner that does not see the inputs of SOFTMAX and GATED_SILU
+    nodes keeps values they read in registers and never stores them."""
+    r = run("random", "3000", "1", "blind", expect_ok=False)
+    assert r["stale_reads"] > 100
 
 
 def test_euler_graph_is_one_program():

@@ -564,3 +564,127 @@ def test_program_words_are_checked_before_launch(gpu):
         if base.value:
             lib.m3_hip_arena_release(handle, base)
         lib.m3_hip_device_close(handle)
+
+
+def consumer_graph(consumer, shape):
+    """x * scale + bias feeding a node that never fuses (the scale + mask
+    -> softmax and x * w + b -> tanh patterns; Snake1d and GATED_SILU read
+    two values)."""
+    def build():
+        rng = np.random.default_rng(17)
+        g = m3.Graph()
+        x = g.add_value(m3.INPUT, m3.F32, shape)
+        x_data = rng.standard_normal(shape).astype(np.float32)
+        scale = g.add_value(m3.CONSTANT, m3.F32, (1,))
+        g.set_constant(scale, np.array([0.125], np.float32))
+        bias = g.add_value(m3.CONSTANT, m3.F32, shape[-1:])
+        g.set_constant(bias, rng.standard_normal(shape[-1:])
+                       .astype(np.float32))
+        t0 = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        t1 = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        g.add_node(m3.OP_MUL, [x, scale], [t0])
+        g.add_node(m3.OP_ADD, [t0, bias], [t1])
+        y = g.add_value(m3.OUTPUT, m3.F32, shape)
+        if consumer == m3.OP_SNAKE1D:
+            alpha = g.add_value(m3.CONSTANT, m3.F32, (1, shape[1], 1))
+            g.set_constant(alpha, rng.uniform(0.1, 2.0, (1, shape[1], 1))
+                           .astype(np.float32))
+            g.add_node(m3.OP_SNAKE1D, [t1, alpha], [y])
+        elif consumer == m3.OP_GATED_SILU:
+            g.add_node(m3.OP_GATED_SILU, [t1, x], [y])
+        else:
+            g.add_node(consumer, [t1], [y])
+        return g, [(x, x_data)], [(y, shape)]
+    return build
+
+
+@pytest.mark.parametrize("generated", [True, False])
+@pytest.mark.parametrize("consumer", ["SOFTMAX", "TANH", "SNAKE1D",
+                                      "GATED_SILU"])
+def test_value_read_by_an_unfused_kind_is_stored(gpu, consumer, generated):
+    """The fused MUL + ADD program stores the temporary that its
+    non-fusing reader needs: fused equals unfused bit for bit, as one
+    program launch plus the reader's kernel."""
+    kind = getattr(m3, "OP_" + consumer)
+    shape = (4, 96, 1024) if kind == m3.OP_SNAKE1D else (384, 1024)
+    build = consumer_graph(kind, shape)
+    fused, plan_on, kernels = run_session(build, True, generated)
+    plain, plan_off, _ = run_session(build, False)
+    assert plan_on == plan_off
+    assert sum(launches for name, (launches, _) in kernels.items()
+               if name.startswith("m3_program")) == 1, kernels
+    assert np.array_equal(fused[0].view(np.uint32),
+                          plain[0].view(np.uint32))
+
+
+def periodic_slot_graph(rows):
+    """x = c + d ([4]) takes the 16 * rows-byte slot a finished [rows, 4]
+    value left; z = y + x reads x as a trailing broadcast and t = z * a is
+    planned into the same slot once x is dead. A program storing t there
+    would overwrite x while other lanes still read x[e mod 4]."""
+    def build():
+        rng = np.random.default_rng(3)
+        shape = (rows, 4)
+        g = m3.Graph()
+        a, b, y = (g.add_value(m3.INPUT, m3.F32, shape) for _ in range(3))
+        c = g.add_value(m3.CONSTANT, m3.F32, (4,))
+        d = g.add_value(m3.CONSTANT, m3.F32, (4,))
+        g.set_constant(c, rng.standard_normal(4).astype(np.float32))
+        g.set_constant(d, rng.standard_normal(4).astype(np.float32))
+        p = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        q = g.add_value(m3.OUTPUT, m3.F32, shape)
+        x = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+        z = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        t = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        out = g.add_value(m3.OUTPUT, m3.F32, shape)
+        g.add_node(m3.OP_MUL, [a, b], [p])
+        g.add_node(m3.OP_SOFTMAX, [p], [q])
+        g.add_node(m3.OP_ADD, [c, d], [x])
+        g.add_node(m3.OP_ADD, [y, x], [z])
+        g.add_node(m3.OP_MUL, [z, a], [t])
+        g.add_node(m3.OP_TANH, [t], [out])
+        feeds = [(v, rng.standard_normal(shape).astype(np.float32))
+                 for v in (a, b, y)]
+        return g, feeds, [(q, shape), (out, shape)]
+    return build
+
+
+def narrow_slot_graph(rows, width):
+    """A softmax output s (F32) is read by a fused MUL + CAST whose F16
+    result h is planned into s's slot once s is dead: lane e's store of h
+    covers bytes of s[e / 2], which another lane reads."""
+    def build():
+        rng = np.random.default_rng(4)
+        shape = (rows, width)
+        g = m3.Graph()
+        x = g.add_value(m3.INPUT, m3.F32, shape)
+        w = g.add_value(m3.INPUT, m3.F32, shape)
+        s = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        u = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        h = g.add_value(m3.TEMPORARY, m3.F16, shape)
+        out = g.add_value(m3.OUTPUT, m3.F32, shape)
+        g.add_node(m3.OP_SOFTMAX, [x], [s])
+        g.add_node(m3.OP_MUL, [s, w], [u])
+        g.add_node(m3.OP_CAST, [u], [h])
+        g.add_node(m3.OP_SOFTMAX, [h], [out])
+        feeds = [(x, rng.standard_normal(shape).astype(np.float32)),
+                 (w, rng.standard_normal(shape).astype(np.float32))]
+        return g, feeds, [(out, shape)]
+    return build
+
+
+@pytest.mark.parametrize("generated", [True, False])
+@pytest.mark.parametrize("graph", ["periodic", "narrow"])
+def test_fused_stores_never_land_on_operands_other_lanes_read(gpu, graph,
+                                                              generated):
+    """Slots shared by liveness never put a program's store on an operand
+    that other lanes still read: such runs stay unfused, and the results
+    equal the unfused run's bit for bit."""
+    build = periodic_slot_graph(1 << 16) if graph == "periodic" \
+        else narrow_slot_graph(512, 1024)
+    fused, plan_on, kernels = run_session(build, True, generated)
+    plain, plan_off, _ = run_session(build, False)
+    assert plan_on == plan_off
+    assert not any(k.startswith("m3_program") for k in kernels), kernels
+    for a, b in zip(fused, plain):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 
 from conftest import m3
-from harness import HipFixture, ViewSpec, as_bytes, run_oracle
+from harness import (HipFixture, ViewSpec, as_bytes, run_oracle,
+                     subnormal_tie_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -300,6 +301,23 @@ def test_softmax_zero_tails(hip, width):
              ViewSpec(1, m3.F32, (rows, width))]
     storages = [as_bytes(logits), np.zeros(logits.nbytes, np.uint8)]
     compare(hip, m3.OP_SOFTMAX, storages, views, "softmax tails w=%d" % width)
+
+
+@pytest.mark.parametrize("width", [100, 102, 128, 1024, 2048, 4096, 10000])
+def test_softmax_subnormal_ties(hip, width):
+    """Quotients that land exactly on a rounding midpoint of the F32
+    subnormal range (e_j = sum * (2k+1) * 2^-150) round to even, as the
+    reference's F32 division does, in every softmax kernel (widths 100,
+    102 and 10000 run the general kernel, 128 to 2048 the rows kernel,
+    4096 the tiled one)."""
+    rng = np.random.default_rng(13000 + width)
+    rows = 96
+    logits = subnormal_tie_rows(rng, rows, width)
+    views = [ViewSpec(0, m3.F32, (rows, width)),
+             ViewSpec(1, m3.F32, (rows, width))]
+    storages = [as_bytes(logits), np.zeros(logits.nbytes, np.uint8)]
+    compare(hip, m3.OP_SOFTMAX, storages, views,
+            "softmax subnormal ties w=%d" % width)
 
 
 def test_softmax_strided_and_in_place(hip):

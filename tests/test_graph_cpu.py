@@ -47,6 +47,7 @@ def backend_lib():
     fake.oracle_backend_fail_allocation_at.argtypes = [ctypes.c_size_t]
     fake.oracle_backend_programs.restype = ctypes.c_size_t
     fake.oracle_backend_periodic.restype = ctypes.c_size_t
+    fake.oracle_backend_set_program_order.argtypes = [ctypes.c_int]
     factory = ctypes.cast(fake.oracle_backend_create, ctypes.c_void_p)
     lib.m3_provider_set_gpu_factory.argtypes = [ctypes.c_void_p]
     lib.m3_provider_set_gpu_factory(factory)
@@ -695,3 +696,138 @@ def test_euler_graph_runs_as_one_program(fake):
     assert kinds == kinds_off and len(kinds) == 36
     assert plan_on == plan_off
     assert np.array_equal(fused[0].view(np.uint32), plain[0].view(np.uint32))
+
+
+# ---- fused runs next to nodes that never fuse, and shared slots ------------
+
+def _both_orders(fake, build):
+    """Fused outputs with programs run over increasing and decreasing
+    elements, and the unfused outputs."""
+    results = []
+    try:
+        for decreasing in (0, 1):
+            fake.oracle_backend_set_program_order(decreasing)
+            results.append(_session_outputs(build, True, fake))
+    finally:
+        fake.oracle_backend_set_program_order(0)
+    return results, _session_outputs(build, False, fake)
+
+
+def _consumer_graph(consumer):
+    """A fused run whose last temporary is read only by a node that never
+    fuses (the scale + mask -> softmax and x * w + b -> tanh patterns, and
+    the two-input Snake1d and GATED_SILU)."""
+    def build():
+        rng = np.random.default_rng(17)
+        shape = (4, 8, 64) if consumer == m3.OP_SNAKE1D else (4, 64)
+        g = m3.Graph()
+        x = g.add_value(m3.INPUT, m3.F32, shape)
+        x_data = rng.standard_normal(shape).astype(np.float32)
+        scale = g.add_value(m3.CONSTANT, m3.F32, (1,))
+        g.set_constant(scale, np.array([0.125], np.float32))
+        bias = g.add_value(m3.CONSTANT, m3.F32, shape[-1:])
+        g.set_constant(bias, rng.standard_normal(shape[-1:])
+                       .astype(np.float32))
+        t0 = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        t1 = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        g.add_node(m3.OP_MUL, [x, scale], [t0])
+        g.add_node(m3.OP_ADD, [t0, bias], [t1])
+        y = g.add_value(m3.OUTPUT, m3.F32, shape)
+        if consumer == m3.OP_SNAKE1D:
+            alpha = g.add_value(m3.CONSTANT, m3.F32, (1, shape[1], 1))
+            g.set_constant(alpha, rng.uniform(0.1, 2.0, (1, shape[1], 1))
+                           .astype(np.float32))
+            g.add_node(m3.OP_SNAKE1D, [t1, alpha], [y])
+        elif consumer == m3.OP_GATED_SILU:
+            g.add_node(m3.OP_GATED_SILU, [t1, x], [y])
+        else:
+            g.add_node(consumer, [t1], [y])
+        return g, [(x, x_data)], [(y, shape)]
+    return build
+
+
+@pytest.mark.parametrize("consumer", ["SOFTMAX", "TANH", "SNAKE1D",
+                                      "GATED_SILU"])
+def test_value_read_by_an_unfused_kind_is_stored(fake, consumer):
+    """The fused MUL + ADD run stores the temporary its non-fusing reader
+    needs; the result equals the unfused run's, and the run is fused."""
+    build = _consumer_graph(getattr(m3, "OP_" + consumer))
+    fused_runs, plain = _both_orders(fake, build)
+    for fused in fused_runs:
+        assert fused[2] == 1
+        assert fused[1] == plain[1]
+        assert np.array_equal(fused[0][0].view(np.uint32),
+                              plain[0][0].view(np.uint32))
+
+
+def _periodic_slot_graph():
+    """x = c + d ([4]) takes the free 128-byte slot a finished [8, 4] value
+    left; z = y + x reads x periodically (a trailing broadcast) and
+    t = z * a is planned into the same slot once x is dead. Fused, t's
+    stores would overwrite x while other elements still read x[e mod 4]."""
+    def build():
+        rng = np.random.default_rng(3)
+        shape = (8, 4)
+        g = m3.Graph()
+        a = g.add_value(m3.INPUT, m3.F32, shape)
+        b = g.add_value(m3.INPUT, m3.F32, shape)
+        y = g.add_value(m3.INPUT, m3.F32, shape)
+        c = g.add_value(m3.CONSTANT, m3.F32, (4,))
+        d = g.add_value(m3.CONSTANT, m3.F32, (4,))
+        g.set_constant(c, rng.standard_normal(4).astype(np.float32))
+        g.set_constant(d, rng.standard_normal(4).astype(np.float32))
+        p = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        q = g.add_value(m3.OUTPUT, m3.F32, shape)
+        x = g.add_value(m3.TEMPORARY, m3.F32, (4,))
+        z = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        t = g.add_value(m3.TEMPORARY, m3.F32, shape)
+        out = g.add_value(m3.OUTPUT, m3.F32, shape)
+        g.add_node(m3.OP_MUL, [a, b], [p])
+        g.add_node(m3.OP_SOFTMAX, [p], [q])
+        g.add_node(m3.OP_ADD, [c, d], [x])
+        g.add_node(m3.OP_ADD, [y, x], [z])
+        g.add_node(m3.OP_MUL, [z, a], [t])
+        g.add_node(m3.OP_TANH, [t], [out])
+        feeds = [(v, rng.standard_normal(shape).astype(np.float32))
+                 for v in (a, b, y)]
+        return g, feeds, [(q, shape), (out, shape)]
+    return build
+
+
+def _narrow_slot_graph():
+    """A softmax output s (F32) is read by a fused run whose F16 result h
+    is planned into s's slot once s is dead; element e of h covers bytes of
+    element e / 2 of s, which another element reads."""
+    def build():
+        rng = np.random.default_rng(4)
+        g = m3.Graph()
+        x = g.add_value(m3.INPUT, m3.F32, (8, 16))
+        w = g.add_value(m3.INPUT, m3.F32, (8, 16))
+        s = g.add_value(m3.TEMPORARY, m3.F32, (8, 16))
+        u = g.add_value(m3.TEMPORARY, m3.F32, (8, 16))
+        h = g.add_value(m3.TEMPORARY, m3.F16, (8, 16))
+        out = g.add_value(m3.OUTPUT, m3.F32, (8, 16))
+        g.add_node(m3.OP_SOFTMAX, [x], [s])
+        g.add_node(m3.OP_MUL, [s, w], [u])
+        g.add_node(m3.OP_CAST, [u], [h])
+        g.add_node(m3.OP_SOFTMAX, [h], [out])
+        feeds = [(x, rng.standard_normal((8, 16)).astype(np.float32)),
+                 (w, rng.standard_normal((8, 16)).astype(np.float32))]
+        return g, feeds, [(out, (8, 16))]
+    return build
+
+
+@pytest.mark.parametrize("graph", ["periodic", "narrow"])
+def test_fused_stores_never_land_on_operands_other_elements_read(fake,
+                                                                 graph):
+    """With slots shared by liveness, the planner does not fuse a run whose
+    store would overwrite an operand other elements still read: fused
+    results equal unfused ones in either element order, the slot plan is
+    unchanged."""
+    build = _periodic_slot_graph() if graph == "periodic" \
+        else _narrow_slot_graph()
+    fused_runs, plain = _both_orders(fake, build)
+    for fused in fused_runs:
+        assert fused[1] == plain[1]
+        for a, b in zip(fused[0], plain[0]):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 
 from conftest import m3
-from harness import ViewSpec, as_bytes, ref_available, run_oracle, run_ref
+from harness import (ViewSpec, as_bytes, ref_available, run_oracle, run_ref,
+                     subnormal_tie_rows)
 
 pytestmark = pytest.mark.skipif(
     not ref_available(),
@@ -174,6 +175,36 @@ def test_softmax_finite_rows(dtype, width):
     views = [ViewSpec(0, dtype, (rows, width)),
              ViewSpec(1, dtype, (rows, width))]
     same(m3.OP_SOFTMAX, [data, np.zeros(span(views[1]), np.uint8)], views)
+
+
+def test_softmax_subnormal_ties():
+    """Rows whose quotients fall exactly on subnormal rounding midpoints:
+    the oracle equals the compiled reference, and the rows do contain
+    quotients where RN_f32(e * RN_f64(1/sum)) (a product of the reciprocal
+    in double) is not the F32 quotient, so the GPU test with the same rows
+    (test_gpu_parity.py) tells the two apart."""
+    import ctypes
+    import ctypes.util
+
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    rng = np.random.default_rng(13128)
+    rows, width = 64, 128
+    logits = subnormal_tie_rows(rng, rows, width)
+    views = [ViewSpec(0, m3.F32, (rows, width)),
+             ViewSpec(1, m3.F32, (rows, width))]
+    same(m3.OP_SOFTMAX, [as_bytes(logits), np.zeros(logits.nbytes, np.uint8)],
+         views)
+    differ = 0
+    for r in range(rows):
+        zeros = int(np.count_nonzero(logits[r] == 0.0))
+        for v in logits[r][np.isfinite(logits[r]) & (logits[r] != 0.0)]:
+            e = np.float32(libm.expf(float(v)))
+            quotient = e / np.float32(zeros)
+            product = np.float32(np.float64(e) * (1.0 / np.float64(zeros)))
+            differ += quotient.view(np.uint32) != product.view(np.uint32)
+    assert differ > 100
 
 
 def test_softmax_nan_preflight():
