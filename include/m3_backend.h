@@ -362,9 +362,9 @@ m3_status m3_backend_create_internal(const m3_backend_vtable *vtable,
                                      void *context,
                                      const m3_backend_info *info,
                                      m3_backend **backend, m3_error *error);
-/* Opens HIP device 0. Returns M3_STATUS_UNSUPPORTED when no HIP device is
- * present, like m3_backend_create_metal without a Metal device. */
-m3_status m3_backend_create_hip(m3_backend **backend, m3_error *error);
+/* Host memory executed by the CPU provider (src/m3_backend.h:37). The HIP
+ * backend's constructor is in m3_backend_hip.h. */
+m3_status m3_backend_create_host(m3_backend **backend, m3_error *error);
 void m3_backend_free(m3_backend *backend);
 m3_status m3_backend_get_info(const m3_backend *backend,
                               m3_backend_info *info, m3_error *error);

@@ -151,7 +151,8 @@ class HipKernelTime(ctypes.Structure):
 
 
 # Every exported symbol of include/m3.h, include/m3_backend.h,
-# include/m3_rng.h (libm3.so) and include/m3_hip.h (libm3_hip.so).
+# include/m3_backend_hip.h, include/m3_rng.h (libm3.so) and
+# include/m3_hip.h (libm3_hip.so).
 EXPORTS_M3 = [
     "m3_version", "m3_status_string", "m3_error_reset", "m3_error_message",
     "m3_graph_value_desc_init", "m3_graph_node_desc_init",
@@ -169,7 +170,9 @@ EXPORTS_M3 = [
     "m3_tensor_permute", "m3_scratch_arena_init", "m3_scratch_arena_mark",
     "m3_scratch_arena_rewind", "m3_command_validate",
     "m3_commands_scratch_bytes", "m3_backend_execute", "m3_backend_finish",
-    "m3_backend_create_internal", "m3_backend_create_hip", "m3_backend_free",
+    "m3_backend_create_internal", "m3_backend_create_hip",
+    "m3_backend_create_host", "m3_hip_owns_execute", "m3_hip_context_device",
+    "m3_backend_free",
     "m3_backend_get_info", "m3_backend_get_allocation_stats",
     "m3_backend_reserve", "m3_backend_context_internal",
     "m3_storage_allocate", "m3_storage_free", "m3_storage_size",
@@ -264,6 +267,7 @@ def load():
              P(ScratchArena), err)
     _declare(lib, "m3_backend_finish", st, vp, err)
     _declare(lib, "m3_backend_create_hip", st, P(vp), err)
+    _declare(lib, "m3_backend_create_host", st, P(vp), err)
     _declare(lib, "m3_backend_free", None, vp)
     _declare(lib, "m3_backend_get_info", st, vp, P(BackendInfo), err)
     _declare(lib, "m3_backend_get_allocation_stats", st, vp,

@@ -28,8 +28,9 @@
  * command is enqueued in order on the device stream and the list waits
  * once at the end.
  */
-#include "m3_internal.h"
+#include "m3_backend_internal.h"
 
+#include "m3_backend_hip.h"
 #include "m3_hip.h"
 
 #include <stdio.h>
@@ -190,7 +191,27 @@ static m3_status m3_hip_reserve(void *opaque, size_t byte_count,
     return M3_STATUS_OK;
 }
 
-/* handle: NULL for storage carved from an arena, else the hipMalloc base. */
+/* The arena holding [address, address + 1), or NULL for memory that has
+ * its own hipMalloc. */
+static const m3_hip_arena *m3_hip_arena_of(
+    const m3_hip_backend_context *context, const void *address)
+{
+    const uint8_t *at = address;
+    size_t i;
+
+    for (i = 0U; i < context->arena_count; ++i) {
+        const m3_hip_arena *arena = &context->arenas[i];
+
+        if (at >= arena->base && at < arena->base + arena->size) {
+            return arena;
+        }
+    }
+    return NULL;
+}
+
+/* handle and data are both the device address of the storage (the
+ * backend's storages are reached through m3_storage_handle_internal);
+ * storage carved from an arena is told apart by its address. */
 static m3_status m3_hip_allocate(void *opaque, size_t byte_count,
                                  size_t alignment, void **handle, void **data,
                                  m3_error *error)
@@ -216,6 +237,7 @@ static m3_status m3_hip_allocate(void *opaque, size_t byte_count,
             byte_count <= arena->size - start) {
             arena->used = start + byte_count;
             *data = arena->base + start;
+            *handle = *data;
             return M3_STATUS_OK;
         }
     }
@@ -234,7 +256,7 @@ static void m3_hip_free_storage(void *opaque, void *handle, void *data)
     m3_hip_backend_context *context = opaque;
 
     m3_hip_forget_storage(context, data);
-    if (handle != NULL) {
+    if (handle != NULL && m3_hip_arena_of(context, handle) == NULL) {
         /* queued commands may still use the memory */
         (void)m3_hip_synchronize(context->device, NULL, 0U);
         m3_hip_arena_release(context->device, handle);
@@ -276,7 +298,7 @@ static void m3_hip_view_of(const m3_tensor_view *view, m3_hip_view *out)
     uint8_t axis;
 
     (void)memset(out, 0, sizeof(*out));
-    out->base = m3_storage_device_data(view->storage);
+    out->base = m3_storage_handle_internal(view->storage);
     out->byte_offset = (uint64_t)view->byte_offset;
     out->element_count = (uint64_t)view->metadata.element_count;
     out->rank = view->metadata.rank;
@@ -284,6 +306,48 @@ static void m3_hip_view_of(const m3_tensor_view *view, m3_hip_view *out)
     for (axis = 0U; axis < view->metadata.rank; ++axis) {
         out->shape[axis] = view->metadata.shape[axis];
         out->byte_strides[axis] = (uint64_t)view->byte_strides[axis];
+    }
+}
+
+/* The binary descriptor of ADD, MUL, SUB and DIV commands, else NULL. */
+static const m3_op_binary *m3_hip_binary_of(const m3_command *command)
+{
+    switch (command->kind) {
+    case M3_OP_ADD:
+        return &command->descriptor.add;
+    case M3_OP_MUL:
+        return &command->descriptor.mul;
+    case M3_OP_SUB:
+        return &command->descriptor.sub;
+    case M3_OP_DIV:
+        return &command->descriptor.div;
+    default:
+        return NULL;
+    }
+}
+
+/* The view a command writes (NULL for an elementwise program, whose
+ * outputs are those of its commands). */
+static const m3_tensor_view *m3_hip_output_of(const m3_command *command)
+{
+    const m3_op_binary *binary = m3_hip_binary_of(command);
+
+    if (binary != NULL) {
+        return binary->output;
+    }
+    switch (command->kind) {
+    case M3_OP_COPY:
+    case M3_OP_CAST:
+    case M3_OP_SOFTMAX:
+    case M3_OP_TANH:
+        /* the unary descriptors share one layout */
+        return command->descriptor.copy.output;
+    case M3_OP_SNAKE1D:
+        return command->descriptor.snake1d.output;
+    case M3_OP_GATED_SILU:
+        return command->descriptor.gated_silu.output;
+    default:
+        return NULL;
     }
 }
 
@@ -311,7 +375,7 @@ static const m3_tensor_view *m3_hip_checked_input(const m3_command *command,
 static bool m3_hip_writes(const m3_command *command,
                           const m3_storage *storage)
 {
-    const m3_tensor_view *output = m3_op_output_of(command);
+    const m3_tensor_view *output = m3_hip_output_of(command);
 
     if (command->kind == M3_OP_ELEMENTWISE_PROGRAM) {
         const m3_op_elementwise_program *program =
@@ -345,7 +409,7 @@ static bool m3_hip_written_before(const m3_command *commands, size_t index,
 static void m3_hip_forget_outputs(m3_hip_backend_context *context,
                                   const m3_command *command)
 {
-    const m3_tensor_view *output = m3_op_output_of(command);
+    const m3_tensor_view *output = m3_hip_output_of(command);
 
     if (command->kind == M3_OP_ELEMENTWISE_PROGRAM) {
         const m3_op_elementwise_program *program =
@@ -359,7 +423,7 @@ static void m3_hip_forget_outputs(m3_hip_backend_context *context,
     }
     if (output != NULL) {
         m3_hip_forget_storage(context,
-                              m3_storage_device_data(output->storage));
+                              m3_storage_handle_internal(output->storage));
     }
 }
 
@@ -501,7 +565,7 @@ static int m3_hip_enqueue(m3_hip_backend_context *context,
                           const m3_command *command, char *message,
                           size_t capacity)
 {
-    const m3_op_binary *binary = m3_op_binary_of(command);
+    const m3_op_binary *binary = m3_hip_binary_of(command);
     m3_hip_view a;
     m3_hip_view b;
     m3_hip_view c;
@@ -512,7 +576,7 @@ static int m3_hip_enqueue(m3_hip_backend_context *context,
 
         return m3_hip_launch_program(
             context->device, program->words,
-            (const uint8_t *)m3_storage_device_data(program->storage) +
+            (const uint8_t *)m3_storage_handle_internal(program->storage) +
                 program->byte_offset,
             program->word_count, message, capacity);
     }
@@ -667,14 +731,16 @@ m3_status m3_backend_create_hip(m3_backend **backend, m3_error *error)
     return status;
 }
 
-void *m3_backend_hip_device(const m3_backend *backend)
+bool m3_hip_owns_execute(m3_status (*execute)(void *, const m3_command *,
+                                            size_t, m3_scratch_arena *,
+                                            m3_error *))
 {
-    m3_hip_backend_context *context;
+    return execute == m3_hip_execute;
+}
 
-    if (m3_backend_vtable_of(backend) == NULL ||
-        m3_backend_vtable_of(backend)->execute != m3_hip_execute) {
-        return NULL;
-    }
-    context = m3_backend_context_internal(backend);
-    return context == NULL ? NULL : (void *)context->device;
+void *m3_hip_context_device(void *context)
+{
+    return context == NULL ? NULL
+                           : (void *)((m3_hip_backend_context *)context)
+                                 ->device;
 }

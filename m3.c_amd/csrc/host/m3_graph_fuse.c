@@ -15,7 +15,7 @@
  * M3_HIP_FUSION is "0" when the session is created; then every node runs
  * as its own command (used to compare the two paths).
  */
-#include "m3_graph_internal.h"
+#include "m3_session_internal.h"
 
 #include "m3_fuse.h"
 #include "m3_hip.h"
@@ -45,6 +45,7 @@ static void m3_runs_unfused(m3_session *session)
     for (n = 0U; n < session->node_count; ++n) {
         session->run_commands[n] = session->commands[n];
         session->run_providers[n] = session->providers[n];
+        session->run_first_node[n] = n;
     }
     session->run_count = session->node_count;
 }
@@ -176,6 +177,7 @@ static void m3_runs_fused(m3_session *session, const m3_fuse_plan *plan,
             program->storage = session->program_storage;
             program->byte_offset = offsets[gi] * sizeof(uint32_t);
             session->run_providers[out] = session->providers[n];
+            session->run_first_node[out] = n;
             out += 1U;
             n += group->node_count;
             gi += 1U;
@@ -183,6 +185,7 @@ static void m3_runs_fused(m3_session *session, const m3_fuse_plan *plan,
         }
         session->run_commands[out] = session->commands[n];
         session->run_providers[out] = session->providers[n];
+        session->run_first_node[out] = n;
         out += 1U;
         n += 1U;
     }
@@ -222,9 +225,13 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
     m3_status status;
 
     (void)memset(&plan, 0, sizeof(plan));
+    (void)graph;
     session->run_commands = calloc(count, sizeof(*session->run_commands));
     session->run_providers = calloc(count, sizeof(*session->run_providers));
-    if (session->run_commands == NULL || session->run_providers == NULL) {
+    session->run_first_node = calloc(count,
+                                     sizeof(*session->run_first_node));
+    if (session->run_commands == NULL || session->run_providers == NULL ||
+        session->run_first_node == NULL) {
         return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY,
                             "cannot allocate the session run list");
     }
@@ -243,18 +250,18 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
     for (v = 0U; v < session->value_count; ++v) {
         const m3_tensor_view *view = &session->views[v];
 
-        fuse_values[v].role = session->values[v].description.role;
-        fuse_values[v].dtype = session->values[v].metadata.dtype;
+        fuse_values[v].role = session->values[v].desc.role;
+        fuse_values[v].dtype = session->values[v].meta.dtype;
         fuse_values[v].element_count =
-            (uint64_t)session->values[v].metadata.element_count;
+            (uint64_t)session->values[v].meta.element_count;
         fuse_values[v].address =
             (uint64_t)(uintptr_t)m3_storage_device_data(view->storage) +
             (uint64_t)view->byte_offset;
         fuse_values[v].byte_count =
-            (uint64_t)session->values[v].metadata.byte_count;
+            (uint64_t)session->values[v].meta.byte_count;
     }
     for (n = 0U; n < session->node_count; ++n) {
-        const m3_graph_node_desc *node = &graph->nodes[n];
+        const m3_graph_node_desc *node = &session->nodes[n];
         size_t i;
 
         fuse_nodes[n].kind = node->kind;
@@ -271,7 +278,7 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
         fuse_nodes[n].right = fuse_nodes[n].output;
         if (m3_op_binary_of(&session->commands[n]) != NULL) {
             const m3_tensor_metadata *output =
-                &session->values[node->outputs[0]].metadata;
+                &session->values[node->outputs[0]].meta;
 
             fuse_nodes[n].left = (uint32_t)node->inputs[0];
             fuse_nodes[n].right = (uint32_t)node->inputs[1];
@@ -279,9 +286,9 @@ m3_status m3_session_plan_runs(m3_session *session, const m3_graph *graph,
             fuse_nodes[n].eligible =
                 session->providers[n] == M3_PROVIDER_HIP;
             fuse_nodes[n].left_trailing = m3_trailing_broadcast(
-                &session->values[node->inputs[0]].metadata, output);
+                &session->values[node->inputs[0]].meta, output);
             fuse_nodes[n].right_trailing = m3_trailing_broadcast(
-                &session->values[node->inputs[1]].metadata, output);
+                &session->values[node->inputs[1]].meta, output);
         } else if (node->kind == M3_OP_CAST || node->kind == M3_OP_COPY) {
             fuse_nodes[n].left = (uint32_t)node->inputs[0];
             fuse_nodes[n].right = (uint32_t)node->inputs[0];
@@ -341,8 +348,10 @@ void m3_session_free_runs(m3_session *session)
     free(session->program_words);
     free(session->run_commands);
     free(session->run_providers);
+    free(session->run_first_node);
     session->program_words = NULL;
     session->run_commands = NULL;
     session->run_providers = NULL;
+    session->run_first_node = NULL;
     session->run_count = 0U;
 }

@@ -5,6 +5,7 @@
 #define M3_INTERNAL_H
 
 #include "m3_backend.h"
+#include "m3_backend_hip.h"
 
 #include <stdbool.h>
 #include <stddef.h>
@@ -41,9 +42,19 @@ const m3_tensor_view *m3_op_output_of(const m3_command *command);
 /* True when the HIP provider runs this operation kind. */
 bool m3_op_kind_supported(m3_op_kind kind);
 
-/* ---- backend internals (m3_backend.c) --------------------------------- */
+/* ---- backend internals (m3_buffers.c) --------------------------------- */
 
 const m3_backend_vtable *m3_backend_vtable_of(const m3_backend *backend);
+/* True when the backend's storages are host memory. */
+bool m3_backend_host_visible(const m3_backend *backend);
+
+/* ---- CPU provider (m3_cpu_provider.c) --------------------------------- */
+
+bool m3_cpu_kind_supported(m3_op_kind kind);
+/* Runs a validated list over host storage, each command's data check
+ * right before it. */
+m3_status m3_cpu_execute(const m3_command *commands, size_t count,
+                         m3_error *error);
 
 /* ---- provider scheduler (m3_provider.c) ------------------------------- */
 

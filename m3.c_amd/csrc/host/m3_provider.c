@@ -1,29 +1,83 @@
 /*
- * m3_provider.c - provider scheduler: storage backend choice and per-list
- * provider selection.
+ * m3_provider.c - the scheduler: which backend holds a session's storage,
+ * and which provider runs each command list.
  *
- * Mirrors src/m3_provider.c of the reference with the HIP provider in the
- * place of Metal:
- *   m3_backend_create_preferred  (:35-60)  GPU first when allowed
- *   m3_provider_select_regular   (:62-99)  GPU iff the storage backend is
- *                                          the GPU and every kind is
- *                                          supported
- *   m3_provider_execute_regular  (:101-129)
- * This library has no CPU provider. Where the reference would fall back to
- * its host backend, the scheduler returns M3_STATUS_UNSUPPORTED with a
- * message saying so; nothing is computed on the CPU.
+ * Storage. With the GPU provider allowed (allow_metal, or the neural
+ * engine option, which here means "any provider") the storage is the HIP
+ * device's; a missing device is an error (UNSUPPORTED), never a silent
+ * move to the CPU. With only the CPU provider allowed the storage is host
+ * memory (m3_host_backend.c).
  *
- * m3_provider_set_gpu_factory replaces the GPU backend constructor. Tests
- * use it to run the graph compiler and scheduler against a recording
- * backend on machines without a GPU; NULL restores m3_backend_create_hip.
+ * Lists. A list goes to the GPU provider when the GPU is allowed, the
+ * storage is the device's and the GPU takes every kind in it; otherwise to
+ * the CPU provider when that is allowed and has every kind; otherwise the
+ * list is UNSUPPORTED. The GPU takes every kind this library has, except
+ * the kinds named in the environment variable M3_HIP_CPU_KINDS (a comma
+ * list of COPY, CAST, ADD, MUL, SUB, DIV, SOFTMAX, SNAKE1D, TANH,
+ * GATED_SILU), which go to the CPU provider. That switch exists to compare
+ * the providers node by node and to run sessions that mix them; a session
+ * reads it once, when it is created.
+ *
+ * This is the reference's scheduling (src/m3_provider.c:35-129) with HIP
+ * in the place of Metal. It differs where the reference would use its
+ * CPU provider because the GPU is missing, or for kinds outside this
+ * library: here both are UNSUPPORTED.
+ *
+ * m3_provider_set_gpu_factory replaces the GPU backend's constructor;
+ * tests use it to compile sessions against a recording backend on
+ * machines without a GPU.
  */
 #include "m3_internal.h"
+
+#include <stdlib.h>
+#include <string.h>
 
 static m3_backend_factory m3_gpu_factory = NULL;
 
 void m3_provider_set_gpu_factory(m3_backend_factory factory)
 {
     m3_gpu_factory = factory;
+}
+
+static const char *const m3_kind_names[] = {
+    "COPY",      "CAST",        "ADD",        "MUL",
+    "EMBEDDING", "MATMUL",      "LINEAR",     "RMS_NORM",
+    "LAYER_NORM", "ROPE",       "ATTENTION",  "GATED_SILU",
+    "SOFTMAX",   "TOP_K",       "CATEGORICAL", "CONV1D",
+    "CONV_TRANSPOSE1D", "NEAREST_RESIZE1D", "SNAKE1D", "TANH",
+    "SUB",       "DIV"};
+
+/* True when `kind` is named in M3_HIP_CPU_KINDS. */
+static bool m3_left_to_cpu(m3_op_kind kind)
+{
+    const char *list = getenv("M3_HIP_CPU_KINDS");
+    const char *name;
+    size_t length;
+
+    if (list == NULL ||
+        (unsigned int)kind >=
+            sizeof(m3_kind_names) / sizeof(m3_kind_names[0])) {
+        return false;
+    }
+    name = m3_kind_names[kind];
+    length = strlen(name);
+    while (*list != '\0') {
+        const char *end = strchr(list, ',');
+        const size_t token = end == NULL ? strlen(list)
+                                         : (size_t)(end - list);
+
+        if (token == length && strncmp(list, name, length) == 0) {
+            return true;
+        }
+        list += token;
+        list += *list == ',' ? 1 : 0;
+    }
+    return false;
+}
+
+static bool m3_gpu_takes(m3_op_kind kind)
+{
+    return m3_op_kind_supported(kind) && !m3_left_to_cpu(kind);
 }
 
 m3_status m3_backend_create_preferred(bool allow_gpu, bool allow_cpu,
@@ -33,24 +87,31 @@ m3_status m3_backend_create_preferred(bool allow_gpu, bool allow_cpu,
 
     if (backend == NULL) {
         return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
-                            "preferred backend output is null");
+                            "no place to return the storage backend");
     }
     *backend = NULL;
     if (!allow_gpu && !allow_cpu) {
         return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
-                            "at least one storage provider is required");
+                            "neither the GPU nor the CPU provider is "
+                            "allowed");
     }
     if (!allow_gpu) {
-        return m3_error_set(error, M3_STATUS_UNSUPPORTED,
-                            "this library has no CPU provider; enable the "
-                            "GPU provider (allow_metal)");
+        return m3_backend_create_host(backend, error);
     }
     status = m3_gpu_factory != NULL ? m3_gpu_factory(backend, error)
                                     : m3_backend_create_hip(backend, error);
-    if (status == M3_STATUS_UNSUPPORTED && allow_cpu) {
+    if (status == M3_STATUS_UNSUPPORTED) {
+        char cause[M3_ERROR_MESSAGE_CAPACITY] = "";
+
+        if (error != NULL) {
+            (void)memcpy(cause, error->message, sizeof(cause));
+            cause[sizeof(cause) - 1U] = '\0';
+        }
         return m3_error_set(error, M3_STATUS_UNSUPPORTED,
-                            "no HIP device is available and this library "
-                            "has no CPU provider");
+                            "no HIP device: %s%s", cause,
+                            allow_cpu ? " (allow_metal = false selects the "
+                                        "CPU provider)"
+                                      : "");
     }
     return status;
 }
@@ -63,38 +124,40 @@ m3_status m3_provider_select_regular(const m3_backend *storage_backend,
                                      m3_error *error)
 {
     m3_backend_info info;
-    size_t index;
+    bool gpu = allow_gpu;
+    bool cpu = allow_cpu;
+    size_t i;
     m3_status status;
 
     if (storage_backend == NULL || provider == NULL ||
-        (command_count != 0U && commands == NULL)) {
+        (commands == NULL && command_count != 0U)) {
         return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
-                            "regular provider selection is incomplete");
+                            "provider choice needs a backend, commands and "
+                            "a place for the result");
     }
     status = m3_backend_get_info(storage_backend, &info, error);
     if (status != M3_STATUS_OK) {
         return status;
     }
-    if (allow_gpu && info.kind == M3_BACKEND_HIP) {
-        for (index = 0U; index < command_count; ++index) {
-            if (!m3_op_kind_supported(commands[index].kind)) {
-                break;
-            }
-        }
-        if (index == command_count) {
-            *provider = M3_PROVIDER_HIP;
-            m3_error_reset(error);
-            return M3_STATUS_OK;
-        }
-        if (allow_cpu) {
+    gpu = gpu && info.kind == M3_BACKEND_HIP;
+    for (i = 0U; i < command_count; ++i) {
+        gpu = gpu && m3_gpu_takes(commands[i].kind);
+        cpu = cpu && m3_cpu_kind_supported(commands[i].kind);
+    }
+    if (gpu || cpu) {
+        *provider = gpu ? M3_PROVIDER_HIP : M3_PROVIDER_CPU;
+        m3_error_reset(error);
+        return M3_STATUS_OK;
+    }
+    for (i = 0U; i < command_count; ++i) {
+        if (!m3_op_kind_supported(commands[i].kind)) {
             return m3_error_set(error, M3_STATUS_UNSUPPORTED,
-                                "operation kind %d needs the CPU provider, "
-                                "which this library does not include",
-                                (int)commands[index].kind);
+                                "kind %d is outside this library",
+                                (int)commands[i].kind);
         }
     }
     return m3_error_set(error, M3_STATUS_UNSUPPORTED,
-                        "no enabled provider supports the command list");
+                        "no allowed provider runs this command list");
 }
 
 m3_status m3_provider_execute_regular(m3_backend *storage_backend,
@@ -104,10 +167,29 @@ m3_status m3_provider_execute_regular(m3_backend *storage_backend,
                                       m3_scratch_arena *scratch,
                                       m3_error *error)
 {
-    if (provider != M3_PROVIDER_HIP) {
-        return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
-                            "provider cannot execute regular operations");
+    size_t wanted = 0U;
+    m3_status status;
+
+    if (provider == M3_PROVIDER_HIP) {
+        return m3_backend_execute(storage_backend, commands, command_count,
+                                  scratch, error);
     }
-    return m3_backend_execute(storage_backend, commands, command_count,
-                              scratch, error);
+    if (provider != M3_PROVIDER_CPU) {
+        return m3_error_set(error, M3_STATUS_INVALID_ARGUMENT,
+                            "provider %d does not run regular commands",
+                            (int)provider);
+    }
+    status = m3_commands_scratch_bytes(storage_backend, commands,
+                                       command_count, &wanted, error);
+    if (status != M3_STATUS_OK) {
+        return status;
+    }
+    if (wanted != 0U &&
+        (scratch == NULL || scratch->offset > scratch->capacity ||
+         wanted > scratch->capacity - scratch->offset)) {
+        return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY,
+                            "the CPU provider wants %zu scratch bytes",
+                            wanted);
+    }
+    return m3_cpu_execute(commands, command_count, error);
 }

@@ -38,6 +38,12 @@ static size_t g_periodic; /* periodic operands of the programs run */
  * store that lands on bytes another element still reads changes the
  * result in one of the two. */
 static int g_decreasing;
+/* When set, backends made afterwards declare their memory device memory
+ * (write/read hooks, which copy and count): the session then runs CPU
+ * provider nodes on host mirrors, as it does over HIP memory. */
+static int g_device_memory;
+static size_t g_host_to_device;
+static size_t g_device_to_host;
 
 void oracle_backend_reset(void);
 size_t oracle_backend_log(int *kinds, int *lists, size_t capacity);
@@ -47,6 +53,8 @@ void oracle_backend_fail_allocation_at(size_t index);
 size_t oracle_backend_programs(void);
 size_t oracle_backend_periodic(void);
 void oracle_backend_set_program_order(int decreasing);
+void oracle_backend_set_device_memory(int on);
+size_t oracle_backend_transfers(int to_device);
 m3_status oracle_backend_create(m3_backend **backend, m3_error *error);
 
 void oracle_backend_reset(void)
@@ -58,11 +66,23 @@ void oracle_backend_reset(void)
     g_reserved = 0U;
     g_programs = 0U;
     g_periodic = 0U;
+    g_host_to_device = 0U;
+    g_device_to_host = 0U;
 }
 
 void oracle_backend_set_program_order(int decreasing)
 {
     g_decreasing = decreasing;
+}
+
+void oracle_backend_set_device_memory(int on)
+{
+    g_device_memory = on;
+}
+
+size_t oracle_backend_transfers(int to_device)
+{
+    return to_device ? g_host_to_device : g_device_to_host;
 }
 
 size_t oracle_backend_programs(void)
@@ -153,7 +173,7 @@ static void to_oracle(const m3_tensor_view *view, oracle_view *out)
     uint8_t axis;
 
     memset(out, 0, sizeof(*out));
-    out->data = m3_storage_data(view->storage);
+    out->data = m3_storage_device_data(view->storage);
     out->byte_offset = view->byte_offset;
     out->dtype = (uint32_t)view->metadata.dtype;
     out->rank = view->metadata.rank;
@@ -266,7 +286,7 @@ static int run_program(const m3_op_elementwise_program *program)
     const uint32_t *periods = operands + 2U * operand_count;
     const uint32_t *code = periods + 2U * period_count;
     const uint8_t *stored =
-        (const uint8_t *)m3_storage_data(program->storage);
+        (const uint8_t *)m3_storage_device_data(program->storage);
     uint64_t i;
 
     if (stored == NULL ||
@@ -425,10 +445,37 @@ static m3_status execute(void *context, const m3_command *commands,
     return M3_STATUS_OK;
 }
 
+static m3_status write_hook(void *context, void *data, size_t byte_offset,
+                            const void *source, size_t byte_count,
+                            m3_error *error)
+{
+    (void)context;
+    (void)error;
+    memcpy((uint8_t *)data + byte_offset, source, byte_count);
+    g_host_to_device += 1U;
+    return M3_STATUS_OK;
+}
+
+static m3_status read_hook(void *context, const void *data,
+                           size_t byte_offset, void *destination,
+                           size_t byte_count, m3_error *error)
+{
+    (void)context;
+    (void)error;
+    memcpy(destination, (const uint8_t *)data + byte_offset, byte_count);
+    g_device_to_host += 1U;
+    return M3_STATUS_OK;
+}
+
 m3_status oracle_backend_create(m3_backend **backend, m3_error *error)
 {
-    static const m3_backend_vtable vtable = {destroy, allocate, free_storage,
-                                             execute, NULL, NULL, reserve};
+    static const m3_backend_vtable host_vtable = {
+        destroy, allocate, free_storage, execute, NULL, NULL, reserve};
+    static const m3_backend_vtable device_vtable = {
+        destroy,    allocate,  free_storage, execute,
+        write_hook, read_hook, reserve};
+    const m3_backend_vtable *chosen =
+        g_device_memory ? &device_vtable : &host_vtable;
     m3_backend_info info;
     oracle_backend_context *context = calloc(1U, sizeof(*context));
     m3_status status;
@@ -441,7 +488,8 @@ m3_status oracle_backend_create(m3_backend **backend, m3_error *error)
     info.kind = M3_BACKEND_HIP;
     info.unified_memory = true;
     info.maximum_storage_bytes = (uint64_t)SIZE_MAX;
-    status = m3_backend_create_internal(&vtable, context, &info, backend,
+    info.unified_memory = !g_device_memory;
+    status = m3_backend_create_internal(chosen, context, &info, backend,
                                         error);
     if (status != M3_STATUS_OK) {
         free(context);

@@ -10,6 +10,7 @@ that name the same storage alias exactly as they do in the reference.
                     when it was built in this container
 * ``HipFixture``  - the product: storages on the HIP backend, commands
                     through m3_backend_execute (include/m3_backend.h)
+* ``HostFixture`` - the product's CPU provider, on the host backend
 """
 import ctypes
 import os
@@ -176,15 +177,17 @@ def run_ref(kind, storages, views):
     return status, out
 
 
-class HipFixture:
-    """Storages and views on one HIP backend (m3_backend_create_hip)."""
+class BackendFixture:
+    """Storages and views on one backend made by `constructor`, commands
+    through m3_backend_execute."""
 
-    def __init__(self):
+    def __init__(self, constructor):
         self.lib, _ = m3.load()
         self.backend = ctypes.c_void_p()
         error = m3.Error()
-        m3.check(self.lib.m3_backend_create_hip(ctypes.byref(self.backend),
-                                                ctypes.byref(error)), error)
+        make = getattr(self.lib, constructor)
+        m3.check(make(ctypes.byref(self.backend), ctypes.byref(error)),
+                 error)
         self.storages = []
         self.keep = []
 
@@ -259,6 +262,20 @@ class HipFixture:
         if self.backend:
             self.lib.m3_backend_free(self.backend)
             self.backend = ctypes.c_void_p()
+
+
+class HipFixture(BackendFixture):
+    """The HIP backend (m3_backend_create_hip): the GPU provider."""
+
+    def __init__(self):
+        super().__init__("m3_backend_create_hip")
+
+
+class HostFixture(BackendFixture):
+    """The host backend (m3_backend_create_host): the CPU provider."""
+
+    def __init__(self):
+        super().__init__("m3_backend_create_host")
 
 
 def as_bytes(array):

@@ -10,7 +10,7 @@ import pytest
 from conftest import ROOT, m3
 
 HEADERS = {
-    "libm3.so": ["m3.h", "m3_backend.h", "m3_rng.h"],
+    "libm3.so": ["m3.h", "m3_backend.h", "m3_backend_hip.h", "m3_rng.h"],
     "libm3_hip.so": ["m3_hip.h"],
 }
 

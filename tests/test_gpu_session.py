@@ -334,20 +334,94 @@ def test_euler_cfg_graph(gpu):
     session.free()
 
 
-def test_gpu_provider_disabled_is_unsupported(gpu):
-    """With the GPU provider disallowed there is no CPU fallback."""
-    g = m3.Graph()
-    vi = g.add_value(m3.INPUT, m3.F32, (4,))
-    vo = g.add_value(m3.OUTPUT, m3.F32, (4,))
-    g.add_node(m3.OP_SOFTMAX, [vi], [vo])
-    lib, _ = m3.load()
-    handle = ctypes.c_void_p()
-    error = m3.Error()
-    options = m3.SessionOptions(False, False, True)
-    status = lib.m3_session_create(ctypes.byref(handle), g.handle,
-                                   ctypes.byref(options), ctypes.byref(error))
-    assert status == m3.UNSUPPORTED and not handle
+def test_gpu_provider_disabled_runs_on_the_cpu_provider(gpu):
+    """With the GPU provider disallowed the session keeps host storage and
+    runs every node on the CPU provider, as the reference does
+    (src/m3_provider.c:35-99); the result is the oracle's, bit for bit,
+    and the GPU-provider session of the same graph gives the same bits."""
+    rng = np.random.default_rng(77)
+    shape = (64, 300)
+    logits = (rng.standard_normal(shape) * 3).astype(np.float32)
+    outs = []
+    for allow_metal in (False, True):
+        g = m3.Graph()
+        vi = g.add_value(m3.INPUT, m3.F32, shape)
+        vo = g.add_value(m3.OUTPUT, m3.F32, shape)
+        g.add_node(m3.OP_SOFTMAX, [vi], [vo])
+        session = m3.Session(g, allow_metal=allow_metal,
+                             allow_neural_engine=False)
+        g.free()
+        assert session.provider(0) == (m3.PROVIDER_HIP if allow_metal
+                                       else m3.PROVIDER_CPU)
+        session.write(vi, logits)
+        session.run()
+        outs.append(session.read(vo, np.zeros(shape, np.float32)))
+        session.free()
+    status, storages = run_oracle(
+        m3.OP_SOFTMAX, [as_bytes(logits), as_bytes(np.zeros_like(logits))],
+        [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, shape)])
+    assert status == m3.OK
+    expected = storages[1].view(np.float32).reshape(shape)
+    for out in outs:
+        assert np.array_equal(bits(out), bits(expected))
+
+
+def _mixed_session_outputs(cpu_kinds, shape, seed):
+    """x * c -> SOFTMAX -> + x -> TANH -> * c = y, and SOFTMAX(x) = z, with
+    the kinds in `cpu_kinds` left to the CPU provider."""
+    rng = np.random.default_rng(seed)
+    import os
+    previous = os.environ.get("M3_HIP_CPU_KINDS")
+    if cpu_kinds:
+        os.environ["M3_HIP_CPU_KINDS"] = cpu_kinds
+    try:
+        g = m3.Graph()
+        x = g.add_value(m3.INPUT, m3.F32, shape)
+        c = g.add_value(m3.CONSTANT, m3.F32, shape[-1:])
+        g.set_constant(c, rng.standard_normal(shape[-1:]).astype(np.float32))
+        t = [g.add_value(m3.TEMPORARY, m3.F32, shape) for _ in range(4)]
+        y = g.add_value(m3.OUTPUT, m3.F32, shape)
+        z = g.add_value(m3.OUTPUT, m3.F32, shape)
+        g.add_node(m3.OP_MUL, [x, c], [t[0]])
+        g.add_node(m3.OP_SOFTMAX, [t[0]], [t[1]])
+        g.add_node(m3.OP_ADD, [t[1], x], [t[2]])
+        g.add_node(m3.OP_TANH, [t[2]], [t[3]])
+        g.add_node(m3.OP_MUL, [t[3], c], [y])
+        g.add_node(m3.OP_SOFTMAX, [x], [z])
+        session = m3.Session(g)
+    finally:
+        if previous is None:
+            os.environ.pop("M3_HIP_CPU_KINDS", None)
+        else:
+            os.environ["M3_HIP_CPU_KINDS"] = previous
     g.free()
+    providers = [session.provider(n) for n in range(6)]
+    results = []
+    for _ in range(2):
+        session.write(x, (rng.standard_normal(shape) * 2).astype(np.float32))
+        session.run()
+        results.append([session.read(v, np.zeros(shape, np.float32))
+                        for v in (y, z)])
+    session.free()
+    return providers, results
+
+
+def test_mixed_gpu_and_cpu_session(gpu):
+    """SOFTMAX and TANH on the CPU provider between GPU nodes of one HIP
+    session: the CPU nodes run on host mirrors of the device values, with
+    one device -> host copy per value they read and one host -> device
+    copy per value a GPU node or the caller reads next. Two runs on fresh
+    inputs equal the all-GPU session's bits."""
+    shape = (96, 1024)
+    gpu_providers, expected = _mixed_session_outputs(None, shape, 5)
+    providers, results = _mixed_session_outputs("SOFTMAX,TANH", shape, 5)
+    assert gpu_providers == [m3.PROVIDER_HIP] * 6
+    assert providers == [m3.PROVIDER_HIP, m3.PROVIDER_CPU, m3.PROVIDER_HIP,
+                         m3.PROVIDER_CPU, m3.PROVIDER_HIP, m3.PROVIDER_CPU]
+    for run, want in zip(results, expected):
+        for a, b in zip(run, want):
+            assert np.array_equal(bits(a), bits(b))
+    assert not np.array_equal(results[0][0], results[1][0])
 
 
 def test_two_sessions_interleave(gpu):

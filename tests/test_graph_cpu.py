@@ -239,14 +239,47 @@ def test_provider_options(fake):
     g, _, _, _ = reference_graph()
     assert _session_status(g, (False, False, False))[0] == \
         m3.INVALID_ARGUMENT
+    # the CPU provider alone: host storage, no GPU backend made
     status, made, text = _session_status(g, (False, False, True))
-    assert status == m3.UNSUPPORTED and not made
-    assert "no CPU provider" in text
+    assert status == m3.OK and made, text
+    assert fake.oracle_backend_reserved() == 0
     assert _session_status(g, (False, True, False))[0] == m3.OK
     # Neural Engine alone gives GPU storage but no provider for regular
     # nodes, as in the reference (src/m3_provider.c:62-99).
     assert _session_status(g, (True, False, False))[0] == m3.UNSUPPORTED
     g.free()
+
+
+def test_reference_graph_kat_on_the_cpu_provider(fake):
+    """tests/test_graph_runtime.c:87-160 of the reference: with the Neural
+    Engine and GPU providers disabled the session compiles to host storage,
+    every node runs on the CPU provider, the plan is 6 values, 4 nodes,
+    5 slots, 80 bytes, the result equals tanhf(x + c) * c + x exactly, and
+    I/O keeps roles and exact byte counts. Nothing reaches the GPU
+    backend."""
+    g, x, y, constant = reference_graph()
+    session = m3.Session(g, allow_neural_engine=False, allow_metal=False)
+    g.free()
+    plan = session.plan()
+    assert (plan.value_count, plan.node_count, plan.storage_slot_count,
+            plan.allocated_bytes) == (6, 4, 5, 80)
+    assert [session.provider(i) for i in range(4)] == [m3.PROVIDER_CPU] * 4
+    data = np.array([1.0, 2.0, -3.0, 0.25], np.float32)
+    session.write(x, data)
+    session.run()
+    out = session.read(y, np.zeros(4, np.float32))
+    expected = ((c_tanhf(data + constant) * constant).astype(np.float32)
+                + data).astype(np.float32)
+    assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
+    assert log_of(fake) == ([], [])
+    assert fake.oracle_backend_reserved() == 0
+    with pytest.raises(m3.M3Error) as failure:
+        session.write(y, data)
+    assert failure.value.status == m3.INVALID_ARGUMENT
+    with pytest.raises(m3.M3Error) as failure:
+        session.read(x, np.zeros(4, np.float32))
+    assert failure.value.status == m3.INVALID_ARGUMENT
+    session.free()
 
 
 def test_out_of_scope_operation_is_unsupported(fake):
@@ -830,4 +863,101 @@ def test_fused_stores_never_land_on_operands_other_elements_read(fake,
     for fused in fused_runs:
         assert fused[1] == plain[1]
         for a, b in zip(fused[0], plain[0]):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---- sessions that mix the GPU and CPU providers ----------------------------
+
+def _mixed_graph(seed):
+    """MUL (GPU) -> SOFTMAX (CPU) -> ADD (GPU) -> TANH (CPU) -> MUL (GPU),
+    and a CPU-only branch from the input and a constant to an OUTPUT:
+    x * c -> softmax -> + x -> tanh -> * c = y; softmax(x + 0) read only by
+    the CPU = z."""
+    def build():
+        rng = np.random.default_rng(seed)
+        shape = (4, 64)
+        g = m3.Graph()
+        x = g.add_value(m3.INPUT, m3.F32, shape)
+        c = g.add_value(m3.CONSTANT, m3.F32, (64,))
+        g.set_constant(c, rng.standard_normal(64).astype(np.float32))
+        t = [g.add_value(m3.TEMPORARY, m3.F32, shape) for _ in range(4)]
+        y = g.add_value(m3.OUTPUT, m3.F32, shape)
+        z = g.add_value(m3.OUTPUT, m3.F32, shape)
+        g.add_node(m3.OP_MUL, [x, c], [t[0]])
+        g.add_node(m3.OP_SOFTMAX, [t[0]], [t[1]])
+        g.add_node(m3.OP_ADD, [t[1], x], [t[2]])
+        g.add_node(m3.OP_TANH, [t[2]], [t[3]])
+        g.add_node(m3.OP_MUL, [t[3], c], [y])
+        g.add_node(m3.OP_SOFTMAX, [x], [z])
+        return g, x, (y, z), shape, rng
+    return build
+
+
+def _run_mixed(fake, build, cpu_kinds, device_memory):
+    previous = os.environ.get("M3_HIP_CPU_KINDS")
+    if cpu_kinds:
+        os.environ["M3_HIP_CPU_KINDS"] = cpu_kinds
+    fake.oracle_backend_set_device_memory(1 if device_memory else 0)
+    try:
+        g, x, outputs, shape, rng = build()
+        session = m3.Session(g)
+    finally:
+        fake.oracle_backend_set_device_memory(0)
+        if previous is None:
+            os.environ.pop("M3_HIP_CPU_KINDS", None)
+        else:
+            os.environ["M3_HIP_CPU_KINDS"] = previous
+    g.free()
+    providers = [session.provider(n) for n in range(6)]
+    runs = []
+    for _ in range(2):
+        session.write(x, rng.standard_normal(shape).astype(np.float32))
+        before = (fake.oracle_backend_transfers(1),
+                  fake.oracle_backend_transfers(0))
+        session.run()
+        moved = (fake.oracle_backend_transfers(1) - before[0],
+                 fake.oracle_backend_transfers(0) - before[1])
+        runs.append(([session.read(v, np.zeros(shape, np.float32))
+                      for v in outputs], moved))
+    session.free()
+    return providers, runs
+
+
+def test_mixed_session_stages_once_per_value(fake):
+    """SOFTMAX and TANH left to the CPU provider over device memory: they
+    run on host mirrors; per run the session copies device -> host the
+    softmax input, the TANH input and x (3 copies, the constant is
+    mirrored at creation) and host -> device the two values GPU nodes read
+    next (softmax and tanh results) and the CPU-written OUTPUT z (3
+    copies). Results equal the all-GPU session's bit for bit, on fresh
+    inputs each run."""
+    build = _mixed_graph(31)
+    fake.oracle_backend_reset()
+    fake.oracle_backend_transfers.restype = ctypes.c_size_t
+    fake.oracle_backend_transfers.argtypes = [ctypes.c_int]
+    gpu_providers, gpu_runs = _run_mixed(fake, build, None, True)
+    providers, runs = _run_mixed(fake, build, "SOFTMAX,TANH", True)
+    assert gpu_providers == [m3.PROVIDER_HIP] * 6
+    assert providers == [m3.PROVIDER_HIP, m3.PROVIDER_CPU, m3.PROVIDER_HIP,
+                         m3.PROVIDER_CPU, m3.PROVIDER_HIP, m3.PROVIDER_CPU]
+    for (outputs, moved), (expected, _) in zip(runs, gpu_runs):
+        assert moved == (3, 3)
+        for a, b in zip(outputs, expected):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # the two runs saw different inputs
+    assert not np.array_equal(runs[0][0][0], runs[1][0][0])
+
+
+def test_cpu_kinds_over_host_memory_run_in_place(fake):
+    """Over host-visible memory the CPU provider's nodes need no mirrors
+    and nothing is copied; results equal the all-GPU session's."""
+    build = _mixed_graph(32)
+    fake.oracle_backend_transfers.restype = ctypes.c_size_t
+    fake.oracle_backend_transfers.argtypes = [ctypes.c_int]
+    _, gpu_runs = _run_mixed(fake, build, None, False)
+    providers, runs = _run_mixed(fake, build, "SOFTMAX,TANH", False)
+    assert providers.count(m3.PROVIDER_CPU) == 3
+    for (outputs, moved), (expected, _) in zip(runs, gpu_runs):
+        assert moved == (0, 0)
+        for a, b in zip(outputs, expected):
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
