@@ -37,14 +37,18 @@ struct m3_hip_device {
     uint64_t total_bytes;
     uint32_t compute_units;
     uint32_t lds_per_block; /* bytes of LDS one workgroup may use */
-    /* device flags for data scans and their host mirror */
+    /* device flags for data scans (a view's word holds the epoch of the
+     * last scan that found an offending element in it), the epoch of the
+     * next scan, and the flags' host mirror in coherent pinned memory */
     uint32_t *scan_flags;
-    size_t scan_capacity;
+    uint32_t scan_epoch;
     uint32_t *host_flags;
     /* completion word in coherent pinned host memory (may be null) and the
      * last sequence number a kernel was queued to store there */
     uint32_t *done_word;
     uint32_t done_sequence;
+    uint32_t unchecked_polls; /* polled completions since the last query
+                               * of the stream's error state */
     bool timing;
     std::vector<m3_hip_pending_time> pending;
     std::vector<hipEvent_t> spare_events;

@@ -167,6 +167,9 @@ void m3_plan_index_space(const m3_hip_view *output,
 
 /* ---- device lifetime ---------------------------------------------------- */
 
+/* Views one data scan takes: one flag word each. */
+constexpr uint32_t kScanViews = 64U;
+
 extern "C" int m3_hip_device_count(int *count, char *message,
                                    size_t capacity)
 {
@@ -238,8 +241,8 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
                         "hipStreamCreateWithFlags", message, capacity);
     if (code == M3_HIP_OK) {
         code = m3_hip_check(hipHostMalloc((void **)&device->host_flags,
-                                          64U * sizeof(uint32_t),
-                                          hipHostMallocDefault),
+                                          kScanViews * sizeof(uint32_t),
+                                          hipHostMallocCoherent),
                             "hipHostMalloc", message, capacity);
     }
     if (code != M3_HIP_OK) {
@@ -515,6 +518,53 @@ __global__ __launch_bounds__(64) void m3_done_kernel(uint32_t *word,
  * on the stream instead. */
 constexpr double kDonePollSeconds = 1.0e-3;
 
+/* Completions seen through the completion word between two queries of
+ * the stream's error state. A query (hipStreamQuery) measured 17.5 us on
+ * MI355X against 8.4 us for a whole launch and polled completion, so it
+ * is made once per this many polled completions, not after each. */
+constexpr uint32_t kPollsPerErrorQuery = 64U;
+
+/* After a completion seen through the completion word: every
+ * kPollsPerErrorQuery of them, an error the stream has recorded (a
+ * kernel fault, say) is reported; not ready (the runtime has not retired
+ * the work yet) is no error. Storage reads, frees and destroy wait on the
+ * stream itself, which reports such errors too. */
+static int m3_hip_stream_errors(m3_hip_device *device, char *message,
+                                size_t capacity)
+{
+    hipError_t state;
+
+    device->unchecked_polls += 1U;
+    if (device->unchecked_polls < kPollsPerErrorQuery) {
+        return M3_HIP_OK;
+    }
+    device->unchecked_polls = 0U;
+    state = hipStreamQuery(device->stream);
+    if (state == hipSuccess || state == hipErrorNotReady) {
+        return M3_HIP_OK;
+    }
+    return m3_hip_check(state, "stream (queued work)", message, capacity);
+}
+
+/* Polls the completion word for `sequence` for at most kDonePollSeconds;
+ * true when it arrived. */
+static bool m3_hip_poll_done(const m3_hip_device *device, uint32_t sequence)
+{
+    const auto start = std::chrono::steady_clock::now();
+
+    for (uint32_t spin = 0U;; ++spin) {
+        if (__atomic_load_n(device->done_word, __ATOMIC_ACQUIRE) == sequence) {
+            return true;
+        }
+        if ((spin & 255U) == 255U &&
+            std::chrono::duration<double>(std::chrono::steady_clock::now() -
+                                          start)
+                    .count() > kDonePollSeconds) {
+            return false;
+        }
+    }
+}
+
 extern "C" int m3_hip_synchronize(m3_hip_device *device, char *message,
                                   size_t capacity)
 {
@@ -538,20 +588,9 @@ extern "C" int m3_hip_synchronize(m3_hip_device *device, char *message,
         hipLaunchKernelGGL(m3_done_kernel, dim3(1), dim3(64), 0,
                            device->stream, device->done_word, sequence);
         if (hipGetLastError() == hipSuccess) {
-            const auto start = std::chrono::steady_clock::now();
-
             device->done_sequence = sequence;
-            for (uint32_t spin = 0U;; ++spin) {
-                if (__atomic_load_n(device->done_word, __ATOMIC_ACQUIRE) ==
-                    sequence) {
-                    return M3_HIP_OK;
-                }
-                if ((spin & 255U) == 255U &&
-                    std::chrono::duration<double>(
-                        std::chrono::steady_clock::now() - start)
-                            .count() > kDonePollSeconds) {
-                    break;
-                }
+            if (m3_hip_poll_done(device, sequence)) {
+                return m3_hip_stream_errors(device, message, capacity);
             }
         }
     }
@@ -561,14 +600,28 @@ extern "C" int m3_hip_synchronize(m3_hip_device *device, char *message,
 
 /* ---- data scans (preflight) -------------------------------------------- */
 
-/* Strided element walk shared by the scans: element `flat` of a view whose
- * (coalesced) index space is `plan`, operand 0. */
+/*
+ * A scan checks each of up to kScanViews views for its condition (no NaN
+ * for a softmax input, finite and in [-2^31, 2^31) for a float-to-I32
+ * cast input) and hands the host one flag per view, without a device to
+ * host copy or a stream wait:
+ *   - every scan call has an epoch; a wave that finds an offending element
+ *     stores the epoch into its view's flag word (device memory, written
+ *     only on failure, so the words need no clearing between scans);
+ *   - one publish wave then writes "flag == epoch" for every view into
+ *     the device's coherent pinned host flags, fences at system scope, and
+ *     stores the call's completion sequence into the pinned completion
+ *     word, which the host polls (as m3_hip_synchronize does) before it
+ *     reads the flags; the stream wait remains the fallback.
+ */
+
 struct m3_scan_args {
     const uint8_t *base;
     uint64_t count;
     uint32_t rank;
     uint32_t dtype;
     uint32_t kind;
+    uint32_t epoch;
     uint64_t shape[M3_HIP_MAX_RANK];
     int64_t strides[M3_HIP_MAX_RANK];
     uint32_t *flag;
@@ -600,6 +653,16 @@ __device__ __forceinline__ uint32_t m3_scan_offends(uint32_t bits,
                : 1U;
 }
 
+/* The lanes that found an offending element store the epoch (all store
+ * the same word, so their order does not matter). */
+__device__ __forceinline__ void m3_scan_mark(uint32_t found, uint32_t *flag,
+                                             uint32_t epoch)
+{
+    if (__any(found != 0U) && found != 0U) {
+        *flag = epoch;
+    }
+}
+
 __global__ void m3_scan_kernel(m3_scan_args args)
 {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -620,9 +683,7 @@ __global__ void m3_scan_kernel(m3_scan_args args)
         found |= m3_scan_offends(m3_scan_load(args.base + offset, args.dtype),
                                  args.kind);
     }
-    if (__any(found != 0U) && found != 0U) {
-        atomicOr(args.flag, 1U);
-    }
+    m3_scan_mark(found, args.flag, args.epoch);
 }
 
 /* Contiguous F32 scan: 16-byte loads. */
@@ -630,7 +691,8 @@ __global__ void m3_scan_f32_contiguous_kernel(const uint4 *data,
                                               uint64_t quads,
                                               const uint32_t *tail,
                                               uint32_t tail_count,
-                                              uint32_t kind, uint32_t *flag)
+                                              uint32_t kind, uint32_t *flag,
+                                              uint32_t epoch)
 {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     uint32_t found = 0U;
@@ -645,70 +707,57 @@ __global__ void m3_scan_f32_contiguous_kernel(const uint4 *data,
     if (blockIdx.x == 0U && threadIdx.x < tail_count) {
         found |= m3_scan_offends(tail[threadIdx.x], kind);
     }
-    if (__any(found != 0U) && found != 0U) {
-        atomicOr(flag, 1U);
+    m3_scan_mark(found, flag, epoch);
+}
+
+/* Zeroes `count` flag words (one wave). */
+__global__ __launch_bounds__(64) void m3_scan_clear_kernel(uint32_t *flags,
+                                                          uint32_t count)
+{
+    if (threadIdx.x < count) {
+        flags[threadIdx.x] = 0U;
     }
 }
 
-__global__ void m3_clear_flags_kernel(uint32_t *flags, uint32_t count)
+/* One wave: host_flags[v] = (flags[v] == epoch) for the first `count`
+ * views, a system-scope fence, then the completion sequence (when the
+ * device has a completion word). */
+__global__ __launch_bounds__(64) void m3_scan_publish_kernel(
+    const uint32_t *flags, uint32_t count, uint32_t epoch,
+    uint32_t *host_flags, uint32_t *done_word, uint32_t sequence)
 {
-    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t lane = threadIdx.x;
 
-    if (i < count) {
-        flags[i] = 0U;
+    if (lane < count) {
+        __hip_atomic_store(&host_flags[lane], flags[lane] == epoch ? 1U : 0U,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __threadfence_system();
+    if (lane == 0U && done_word != nullptr) {
+        __hip_atomic_store(done_word, sequence, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
-extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
-                                 const m3_hip_view *views, size_t count,
-                                 uint32_t *flags, char *message,
-                                 size_t capacity)
+/* Scans views[0, count) into the flag words `flags` with `epoch` and
+ * returns one flag per view in `result`. */
+static int m3_hip_scan_into(m3_hip_device *device, uint32_t *flags,
+                            uint32_t epoch, const uint32_t *kinds,
+                            const m3_hip_view *views, size_t count,
+                            uint32_t *result, bool timed, char *message,
+                            size_t capacity)
 {
-    int code;
+    int code = M3_HIP_OK;
+    uint32_t sequence = device->done_sequence;
+    /* untimed launches take no timing events (whose pool may grow) */
+    const bool was_timing = device->timing;
 
-    if (device == nullptr || (count != 0U && (kinds == nullptr ||
-                                              views == nullptr ||
-                                              flags == nullptr))) {
-        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
-                           "scan arguments are incomplete");
-    }
-    if (count == 0U) {
-        return M3_HIP_OK;
-    }
-    if (count > 64U) {
-        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
-                           "at most 64 views can be scanned at once");
-    }
-    if (device->scan_capacity < count) {
-        if (device->scan_flags != nullptr) {
-            (void)hipFree(device->scan_flags);
-            device->scan_flags = nullptr;
-        }
-        code = m3_hip_check(hipMalloc((void **)&device->scan_flags,
-                                      64U * sizeof(uint32_t)),
-                            "hipMalloc(scan flags)", message, capacity);
-        if (code != M3_HIP_OK) {
-            device->scan_capacity = 0U;
-            return code;
-        }
-        device->scan_capacity = 64U;
-    }
-    code = m3_hip_launch(
-        device, "m3_clear_flags",
-        [&](hipEvent_t start, hipEvent_t stop) {
-            hipExtLaunchKernelGGL(m3_clear_flags_kernel, dim3(1), dim3(64), 0,
-                                  device->stream, start, stop, 0U,
-                                  device->scan_flags, (uint32_t)count);
-        },
-        message, capacity);
+    device->timing = device->timing && timed;
+
     for (size_t i = 0U; code == M3_HIP_OK && i < count; ++i) {
         const m3_hip_view *view = &views[i];
-        uint32_t *flag = device->scan_flags + i;
+        uint32_t *flag = flags + i;
 
-        if (!m3_view_is_valid(view) || kinds[i] > M3_HIP_SCAN_I32_RANGE) {
-            return m3_hip_fail(message, capacity, M3_HIP_INVALID,
-                               "scan view %zu is malformed", i);
-        }
         if (view->element_count == 0U) {
             continue;
         }
@@ -732,7 +781,7 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
                                           device->stream, start, stop, 0U,
                                           (const uint4 *)base, quads,
                                           (const uint32_t *)base + quads * 4U,
-                                          tail, kinds[i], flag);
+                                          tail, kinds[i], flag, epoch);
                 },
                 message, capacity);
         } else {
@@ -744,6 +793,7 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
             args.rank = plan.rank;
             args.dtype = view->dtype;
             args.kind = kinds[i];
+            args.epoch = epoch;
             args.flag = flag;
             for (uint32_t axis = 0U; axis < plan.rank; ++axis) {
                 args.shape[axis] = plan.shape[axis];
@@ -763,22 +813,111 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
         }
     }
     if (code == M3_HIP_OK) {
-        code = m3_hip_check(hipMemcpyAsync(device->host_flags,
-                                           device->scan_flags,
-                                           count * sizeof(uint32_t),
-                                           hipMemcpyDeviceToHost,
-                                           device->stream),
-                            "hipMemcpyAsync(scan flags)", message, capacity);
+        sequence += 1U;
+        code = m3_hip_launch(
+            device, "m3_scan_publish",
+            [&](hipEvent_t start, hipEvent_t stop) {
+                hipExtLaunchKernelGGL(m3_scan_publish_kernel, dim3(1),
+                                      dim3(64), 0, device->stream, start,
+                                      stop, 0U, flags, (uint32_t)count,
+                                      epoch, device->host_flags,
+                                      device->done_word, sequence);
+            },
+            message, capacity);
     }
-    if (code == M3_HIP_OK) {
+    device->timing = was_timing;
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    if (device->done_word != nullptr) {
+        device->done_sequence = sequence;
+    }
+    if (device->done_word != nullptr && !device->timing &&
+        m3_hip_poll_done(device, sequence)) {
+        code = m3_hip_stream_errors(device, message, capacity);
+    } else {
         code = m3_hip_check(hipStreamSynchronize(device->stream),
                             "hipStreamSynchronize", message, capacity);
     }
-    if (code == M3_HIP_OK) {
-        std::memcpy(flags, device->host_flags, count * sizeof(uint32_t));
+    for (size_t i = 0U; code == M3_HIP_OK && i < count; ++i) {
+        result[i] = __atomic_load_n(&device->host_flags[i], __ATOMIC_ACQUIRE);
     }
     return code;
 }
+
+static int m3_hip_scan_arguments(const m3_hip_device *device,
+                                 const uint32_t *kinds,
+                                 const m3_hip_view *views, size_t count,
+                                 const uint32_t *flags, char *message,
+                                 size_t capacity)
+{
+    if (device == nullptr || (count != 0U && (kinds == nullptr ||
+                                              views == nullptr ||
+                                              flags == nullptr))) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "scan arguments are incomplete");
+    }
+    if (count > kScanViews) {
+        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
+                           "at most %u views can be scanned at once (%zu "
+                           "given)",
+                           kScanViews, count);
+    }
+    for (size_t i = 0U; i < count; ++i) {
+        if (!m3_view_is_valid(&views[i]) ||
+            kinds[i] > M3_HIP_SCAN_I32_RANGE) {
+            return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                               "scan view %zu is malformed", i);
+        }
+    }
+    return M3_HIP_OK;
+}
+
+extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
+                                 const m3_hip_view *views, size_t count,
+                                 uint32_t *flags, char *message,
+                                 size_t capacity)
+{
+    int code = m3_hip_scan_arguments(device, kinds, views, count, flags,
+                                     message, capacity);
+
+    if (code != M3_HIP_OK || count == 0U) {
+        return code;
+    }
+    bool fresh = false;
+
+    if (device->scan_flags == nullptr) {
+        code = m3_hip_check(hipMalloc((void **)&device->scan_flags,
+                                      kScanViews * sizeof(uint32_t)),
+                            "hipMalloc(scan flags)", message, capacity);
+        fresh = true;
+    }
+    /* 0 is what the words hold after a clear and is never a scan's epoch;
+     * a fresh array, and one whose epochs wrapped, is cleared first */
+    device->scan_epoch += 1U;
+    if (device->scan_epoch == 0U) {
+        device->scan_epoch = 1U;
+        fresh = true;
+    }
+    if (code == M3_HIP_OK && fresh) {
+        code = m3_hip_launch(
+            device, "m3_scan_clear",
+            [&](hipEvent_t start, hipEvent_t stop) {
+                hipExtLaunchKernelGGL(m3_scan_clear_kernel, dim3(1),
+                                      dim3(64), 0, device->stream, start,
+                                      stop, 0U, device->scan_flags,
+                                      kScanViews);
+            },
+            message, capacity);
+    }
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    return m3_hip_scan_into(device, device->scan_flags, device->scan_epoch,
+                            kinds, views, count, flags, true, message,
+                            capacity);
+}
+
 
 /* ---- timing ------------------------------------------------------------- */
 

@@ -349,3 +349,76 @@ def subnormal_tie_rows(rng, rows, width):
     logits[0, :98] = 0.0
     logits[0, 98] = np.float32(float.fromhex("-0x1.892ae8p+6"))
     return logits
+
+
+class HipScanFixture:
+    """One HIP device handle and one arena, driven through the C-ABI
+    (include/m3_hip.h): upload host arrays, describe them as m3_hip_view
+    blocks, and call a data-scan entry point by name."""
+
+    def __init__(self, arena_bytes=1 << 26):
+        _, self.hip = m3.load()
+        vp, sz = ctypes.c_void_p, ctypes.c_size_t
+        self.hip.m3_hip_arena_reserve.argtypes = [vp, sz,
+                                                  ctypes.POINTER(vp),
+                                                  ctypes.c_char_p, sz]
+        self.hip.m3_hip_arena_release.argtypes = [vp, vp]
+        self.hip.m3_hip_copy_h2d.argtypes = [vp, vp, vp, sz,
+                                             ctypes.c_char_p, sz]
+        self.message = ctypes.create_string_buffer(256)
+        self.device = ctypes.c_void_p()
+        assert self.hip.m3_hip_device_open(0, ctypes.byref(self.device),
+                                           self.message, 256) == 0
+        self.base = ctypes.c_void_p()
+        assert self.hip.m3_hip_arena_reserve(self.device, arena_bytes,
+                                             ctypes.byref(self.base),
+                                             self.message, 256) == 0
+        self.size = arena_bytes
+        self.used = 0
+
+    def upload(self, array):
+        """Copies `array` into the arena (256-byte aligned); its address."""
+        data = np.ascontiguousarray(array)
+        at = self.base.value + self.used
+        assert self.used + data.nbytes <= self.size
+        self.used += (data.nbytes + 255) // 256 * 256
+        assert self.hip.m3_hip_copy_h2d(
+            self.device, ctypes.c_void_p(at),
+            data.ctypes.data_as(ctypes.c_void_p), data.nbytes,
+            self.message, 256) == 0, self.message.value
+        return at
+
+    @staticmethod
+    def view(address, dtype, shape, strides=None):
+        size = m3.DTYPE_SIZES[dtype]
+        view = m3.HipView()
+        view.base = address
+        view.rank = len(shape)
+        view.dtype = dtype
+        view.element_count = int(np.prod(shape)) if shape else 1
+        step = size
+        dense = []
+        for dim in reversed(shape):
+            dense.append(step)
+            step *= dim
+        dense = list(reversed(dense))
+        for axis, dim in enumerate(shape):
+            view.shape[axis] = dim
+            view.byte_strides[axis] = (strides or dense)[axis]
+        return view
+
+    def scan(self, entry, kinds, views):
+        """Calls entry(device, kinds, views, count, flags, ...); returns
+        (code, flags, message)."""
+        count = len(views)
+        kind_array = (ctypes.c_uint32 * max(count, 1))(*kinds)
+        view_array = (m3.HipView * max(count, 1))(*views)
+        flags = (ctypes.c_uint32 * max(count, 1))(*([7] * max(count, 1)))
+        code = getattr(self.hip, entry)(self.device, kind_array, view_array,
+                                        count, flags, self.message, 256)
+        return code, list(flags[:count]), self.message.value.decode()
+
+    def close(self):
+        if self.base.value:
+            self.hip.m3_hip_arena_release(self.device, self.base)
+        self.hip.m3_hip_device_close(self.device)

@@ -166,3 +166,55 @@ def test_clean_input_cache_sees_later_writes(hip):
     assert hip.execute([(m3.OP_MUL, [sm_in, other, sm_in])])[0] == m3.OK
     assert hip.execute([(m3.OP_SOFTMAX, [sm_in, sm_out])])[0] == \
         m3.OUT_OF_RANGE
+
+
+def test_scan_flags_follow_each_call(gpu):
+    """m3_hip_scan_views through the C-ABI, call after call: flags are set
+    exactly for the views that offend in that call (a NaN, or a value
+    outside [-2^31, 2^31) for the I32 kind), in contiguous F32, strided
+    and 16-bit views, whatever earlier calls found; an empty list and an
+    empty view leave no trace."""
+    from harness import HipScanFixture
+
+    scan = HipScanFixture()
+    try:
+        rng = np.random.default_rng(12)
+        clean = rng.standard_normal(1 << 20).astype(np.float32)
+        dirty = clean.copy()
+        dirty[777777] = np.nan
+        big = np.full(4099, 3.0e9, np.float32)
+        halves = rng.standard_normal(3001).astype(np.float16)
+        halves_nan = halves.copy()
+        halves_nan[3000] = np.float16("nan")
+        a = {name: scan.upload(array) for name, array in
+             (("clean", clean), ("dirty", dirty), ("big", big),
+              ("halves", halves.view(np.uint16)),
+              ("halves_nan", halves_nan.view(np.uint16)))}
+        nan, rng32 = 0, 1
+        v_clean = scan.view(a["clean"], m3.F32, (1 << 20,))
+        v_dirty = scan.view(a["dirty"], m3.F32, (1 << 20,))
+        # every other element: 777777 is odd, so this view misses the NaN
+        v_even = scan.view(a["dirty"], m3.F32, (1 << 19,), (8,))
+        v_big = scan.view(a["big"], m3.F32, (4099,))
+        v_half = scan.view(a["halves"], m3.F16, (3001,))
+        v_half_nan = scan.view(a["halves_nan"], m3.F16, (3001,))
+        v_empty = scan.view(a["clean"], m3.F32, (0,))
+        calls = [
+            ([nan, nan, nan], [v_clean, v_dirty, v_even], [0, 1, 0]),
+            ([nan, nan], [v_clean, v_clean], [0, 0]),
+            ([rng32, rng32, nan], [v_big, v_clean, v_half_nan], [1, 0, 1]),
+            ([nan, nan, rng32], [v_half, v_empty, v_clean], [0, 0, 0]),
+            ([], [], []),
+            ([nan] * 64, [v_dirty] * 63 + [v_clean], [1] * 63 + [0]),
+            ([nan], [v_clean], [0]),
+        ]
+        for kinds, views, expected in calls:
+            code, flags, message = scan.scan("m3_hip_scan_views", kinds,
+                                             views)
+            assert code == 0, message
+            assert flags == expected, (kinds, flags, expected)
+        code, _, message = scan.scan("m3_hip_scan_views", [nan] * 65,
+                                     [v_clean] * 65)
+        assert code != 0 and "64" in message
+    finally:
+        scan.close()
