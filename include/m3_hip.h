@@ -265,6 +265,22 @@ int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
                       const m3_hip_view *views, size_t count,
                       uint32_t *flags, char *message, size_t capacity);
 
+/* No counterpart in the reference. m3_hip_scan_views for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same scan and results, with the
+ * per-view flag words in a static device array of M3_HIP_STATIC_SCAN_VIEWS
+ * words (256 bytes on each GPU, held until the process ends) instead of
+ * memory the library allocates on first use. It calls no hipMalloc,
+ * hipFree or other allocating routine and records no timing events. More
+ * than M3_HIP_STATIC_SCAN_VIEWS views is M3_HIP_UNSUPPORTED. Every call on
+ * one GPU, from any device handle, shares the array and clears the words
+ * it uses first: calls that overlap on one GPU race. */
+#define M3_HIP_STATIC_SCAN_VIEWS 64U
+int m3_hip_scan_views_static(m3_hip_device *device, const uint32_t *kinds,
+                             const m3_hip_view *views, size_t count,
+                             uint32_t *flags, char *message,
+                             size_t capacity);
+
 /* Waits for all work on the device stream and reports any kernel error. */
 int m3_hip_synchronize(m3_hip_device *device, char *message,
                        size_t capacity);

@@ -195,7 +195,7 @@ EXPORTS_HIP = [
     "m3_hip_scan_views", "m3_hip_synchronize", "m3_hip_timing_enable",
     "m3_hip_timing_reset", "m3_hip_timing_read", "m3_hip_stream",
     "m3_hip_launch_program", "m3_hip_launch_tanh", "m3_hip_launch_gated_silu",
-    "m3_hip_prepare_program",
+    "m3_hip_prepare_program", "m3_hip_scan_views_static",
 ]
 
 _LIB = None

@@ -43,6 +43,8 @@ struct m3_hip_device {
     uint32_t *scan_flags;
     uint32_t scan_epoch;
     uint32_t *host_flags;
+    /* the device address of the static scan scratch (m3_hip_runtime.hip) */
+    uint32_t *static_scratch;
     /* completion word in coherent pinned host memory (may be null) and the
      * last sequence number a kernel was queued to store there */
     uint32_t *done_word;

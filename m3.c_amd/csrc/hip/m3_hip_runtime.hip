@@ -170,6 +170,18 @@ void m3_plan_index_space(const m3_hip_view *output,
 /* Views one data scan takes: one flag word each. */
 constexpr uint32_t kScanViews = 64U;
 
+/* The flag words of m3_hip_scan_views_static: a file-scope device array
+ * (each GPU holds its own copy until the process ends), so that scan
+ * allocates nothing. Host code never uses this name as an address; it
+ * uses the address hipGetSymbolAddress gives for the device, kept per
+ * device ordinal below. */
+static __device__ __align__(256) uint32_t scratch[kScanViews];
+
+constexpr int kScratchOrdinals = 64;
+/* scratch's address on device ordinal i, looked up at the first open of
+ * that device (with the device current) */
+static void *m3_scratch_address[kScratchOrdinals];
+
 extern "C" int m3_hip_device_count(int *count, char *message,
                                    size_t capacity)
 {
@@ -233,6 +245,20 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
                   properties.name, properties.gcnArchName);
     std::snprintf(device->arch, sizeof(device->arch), "%s",
                   properties.gcnArchName);
+    if (ordinal < kScratchOrdinals && m3_scratch_address[ordinal] == nullptr) {
+        void *address = nullptr;
+
+        code = m3_hip_check(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)),
+                            "hipGetSymbolAddress(scratch)", message, capacity);
+        if (code != M3_HIP_OK) {
+            delete device;
+            return code;
+        }
+        m3_scratch_address[ordinal] = address;
+    }
+    device->static_scratch = ordinal < kScratchOrdinals
+                                 ? (uint32_t *)m3_scratch_address[ordinal]
+                                 : nullptr;
     device->total_bytes = (uint64_t)properties.totalGlobalMem;
     device->compute_units = (uint32_t)properties.multiProcessorCount;
     device->lds_per_block = (uint32_t)properties.sharedMemPerBlock;
@@ -918,6 +944,36 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
                             capacity);
 }
 
+extern "C" int m3_hip_scan_views_static(m3_hip_device *device,
+                                        const uint32_t *kinds,
+                                        const m3_hip_view *views,
+                                        size_t count, uint32_t *flags,
+                                        char *message, size_t capacity)
+{
+    int code = m3_hip_scan_arguments(device, kinds, views, count, flags,
+                                     message, capacity);
+
+    if (code != M3_HIP_OK || count == 0U) {
+        return code;
+    }
+    if (device->static_scratch == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
+                           "no static scan scratch on device %d",
+                           device->ordinal);
+    }
+    /* other handles on this GPU share the words: start from zero, and
+     * mark with epoch 1 */
+    hipLaunchKernelGGL(m3_scan_clear_kernel, dim3(1), dim3(64), 0,
+                       device->stream, device->static_scratch,
+                       (uint32_t)count);
+    code = m3_hip_check(hipGetLastError(), "m3_scan_clear", message,
+                        capacity);
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    return m3_hip_scan_into(device, device->static_scratch, 1U, kinds, views,
+                            count, flags, false, message, capacity);
+}
 
 /* ---- timing ------------------------------------------------------------- */
 
