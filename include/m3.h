@@ -234,10 +234,11 @@ m3_status m3_graph_add_coreml_partition(
     m3_error *error);
 
 /* A session owns its storage backend and compiled plan; the graph may be
- * freed after creation. In this library a session runs its regular nodes on
- * the HIP provider and needs allow_metal; a session that allows only the
- * CPU provider is rejected with M3_STATUS_UNSUPPORTED. Sessions are not
- * thread-safe. Reference: include/m3.h:240-259. */
+ * freed after creation. With allow_metal the storage is the HIP device's
+ * and regular nodes run on the HIP provider (M3_STATUS_UNSUPPORTED when no
+ * HIP device is present); with only allow_cpu the storage is host memory
+ * and nodes run on the CPU provider. Sessions are not thread-safe.
+ * Reference: include/m3.h:240-259. */
 m3_status m3_session_create(m3_session **session, const m3_graph *graph,
                              const m3_session_options *options,
                              m3_error *error);
