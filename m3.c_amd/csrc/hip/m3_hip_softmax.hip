@@ -10,28 +10,33 @@
  *           maximum is +inf gives 1/k on its +inf entries and 0 elsewhere.
  * Rounding is reproduced, not approximated:
  *   - the maximum and k are order-independent, so they are reduced across
- *     the 64 lanes of a wavefront;
+ *     the 64 lanes of a wavefront (DPP row operations);
  *   - e_j uses m3_expf (the libm algorithm restated bit for bit);
- *   - the sum keeps the reference's left-to-right F32 order: one lane per
+ *   - the sum keeps the reference's left-to-right F32 order: a lane per
  *     row walks the row's e_j in LDS;
  *   - p_j is the IEEE F32 quotient e_j / sum, formed as
  *     RN_f32(e_j * RN_f64(1/sum)) where that is exact (m3_softmax_scale4).
  *
- * Kernels, chosen by layout and width (rows contiguous along the last axis
- * with a uniform row stride and width a multiple of 4 use the first two):
+ * Kernels for rows contiguous along the last axis, by width; "VEC" rows
+ * have aligned starts and a width that is a multiple of 4 and move in 16-
+ * or 8-byte accesses, other rows element by element; row starts may be
+ * evenly spaced or follow several outer axes (m3_softmax_row):
  *   - width <= 2048: wave-independent rows (m3_softmax_rows_kernel). A wave
- *     holds R rows in VGPRs, reduces max and k with shuffles, forms e_j in
- *     place and streams 256-column chunks through a wave-private LDS tile
- *     where one lane per row continues the in-order sum; no workgroup
- *     barrier separates the phases, so waves overlap memory and arithmetic.
- *   - width <= 8192: a 256-thread workgroup owns a tile of rows; each wave
- *     owns rows w, w+4, ... of the tile; phase 1 loads a row with 16-byte
- *     accesses (8-byte for 16-bit dtypes), reduces max and k, and writes
- *     e_j to LDS; phase 2 has one lane per row sum its row in order from
- *     LDS and form 1/sum in double; phase 3 reads e_j back, scales, rounds
- *     to the output dtype and stores coalesced. LDS rows are padded by 4
- *     floats so the per-row walks of phase 2 hit distinct banks.
- *   - any other layout: one thread per row through the three passes.
+ *     holds R rows in VGPRs, reduces max and k, forms e_j in place and
+ *     streams 256-column chunks through a wave-private LDS tile where the
+ *     in-order sums run; no workgroup barrier separates the phases, so
+ *     waves overlap memory and arithmetic.
+ *   - VEC rows with evenly spaced starts up to 8192 columns: a 256-thread
+ *     workgroup owns a tile of whole rows in LDS (m3_softmax_tiled_kernel);
+ *     phase 1 loads a row, reduces max and k and writes e_j to LDS; phase 2
+ *     has one lane per row sum its row in order and form 1/sum in double;
+ *     phase 3 reads e_j back, scales, rounds and stores coalesced. LDS rows
+ *     are padded by 4 floats so the per-row walks hit distinct banks.
+ *   - any other row: three streamed passes over 256-column chunks
+ *     (m3_softmax_stream_kernel), carrying the in-order sum across chunks
+ *     and reading the row again for the scale pass.
+ * A last axis that is not contiguous runs one thread per row through the
+ * three passes (m3_softmax_general_kernel).
  */
 #include "m3_hip_internal.h"
 #include "m3_libm.h"
@@ -50,7 +55,8 @@ constexpr uint32_t kPad = 4U;
 constexpr uint32_t kChunk = 256U;         /* columns per LDS chunk */
 constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
 constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
-constexpr uint32_t kSumLanes = 16U;       /* lanes that run the in-order sums */
+constexpr uint32_t kStreamRows = 4U;      /* rows per wave, streamed kernel */
+constexpr uint32_t kStreamBatch = 4U;     /* chunks per batch of loads */
 
 /* Four F32 -inf: what a load past the end of a row reads instead. Never
  * written; not const, so that it is in the global address space like the
@@ -62,38 +68,83 @@ struct m3_softmax_args {
     const uint8_t *input;
     uint8_t *output;
     uint64_t rows;
-    uint64_t row_stride; /* input bytes between rows */
+    uint64_t row_stride; /* input bytes between rows (outer_rank <= 1) */
     uint32_t width;
     uint32_t in_dtype;
     uint32_t out_dtype;
     uint32_t tile_rows;
+    /* Rows whose starts are not evenly spaced (outer_rank > 1): row r
+     * starts at input + sum over axes of coordinate(r, axis) * stride. */
+    uint32_t outer_rank;
+    uint64_t outer_shape[M3_HIP_MAX_RANK];
+    int64_t outer_strides[M3_HIP_MAX_RANK];
 };
+
+/* Start of input row `row`. */
+__device__ __forceinline__ const uint8_t *m3_softmax_row(
+    const m3_softmax_args &a, uint64_t row)
+{
+    if (a.outer_rank <= 1U) {
+        return a.input + row * a.row_stride;
+    }
+    int64_t offset = 0;
+    uint64_t rest = row;
+
+    for (int axis = (int)a.outer_rank - 1; axis >= 0; --axis) {
+        const uint64_t dim = a.outer_shape[axis];
+        const uint64_t q = rest / dim;
+
+        offset += (int64_t)(rest - q * dim) * a.outer_strides[axis];
+        rest = q;
+    }
+    return a.input + offset;
+}
+
+/* Wave64 reductions through DPP row operations, which stay in the VALU
+ * (a shuffle is an LDS permute with its round-trip latency):
+ *   quad_perm [1,0,3,2] and [2,3,0,1]  - quads,
+ *   row_half_mirror, row_mirror        - 8 and 16 lanes,
+ *   row_bcast:15 into rows 1 and 3     - pairs of rows,
+ *   row_bcast:31 into rows 2 and 3     - lane 63 holds the whole wave.
+ * `identity` is what the lanes of a row outside the row mask contribute.
+ * The result is read from lane 63 into a scalar register. */
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t m3_dpp(uint32_t identity, uint32_t x)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)identity, (int)x, CTRL,
+                                                 ROW_MASK, 0xF, false);
+}
+
+template <typename Op>
+__device__ __forceinline__ uint32_t m3_wave_reduce(uint32_t v,
+                                                   uint32_t identity, Op op)
+{
+    v = op(v, m3_dpp<0xB1, 0xF>(identity, v));
+    v = op(v, m3_dpp<0x4E, 0xF>(identity, v));
+    v = op(v, m3_dpp<0x141, 0xF>(identity, v));
+    v = op(v, m3_dpp<0x140, 0xF>(identity, v));
+    v = op(v, m3_dpp<0x142, 0xA>(identity, v));
+    v = op(v, m3_dpp<0x143, 0xC>(identity, v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
 
 __device__ __forceinline__ float m3_wave_max(float v)
 {
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        v = fmaxf(v, __shfl_xor(v, mask, 64));
-    }
-    return v;
+    return m3_bits_f32(m3_wave_reduce(
+        m3_f32_bits(v), m3_f32_bits(-INFINITY), [](uint32_t x, uint32_t y) {
+            return m3_f32_bits(fmaxf(m3_bits_f32(x), m3_bits_f32(y)));
+        }));
 }
 
 __device__ __forceinline__ uint32_t m3_wave_sum(uint32_t v)
 {
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        v += __shfl_xor(v, mask, 64);
-    }
-    return v;
+    return m3_wave_reduce(v, 0U, [](uint32_t x, uint32_t y) { return x + y; });
 }
 
 __device__ __forceinline__ uint32_t m3_wave_max_u32(uint32_t v)
 {
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        v = max(v, (uint32_t)__shfl_xor((int)v, mask, 64));
-    }
-    return v;
+    return m3_wave_reduce(v, 0U,
+                          [](uint32_t x, uint32_t y) { return max(x, y); });
 }
 
 /* A value that is equal in every lane of the wave, moved to a scalar
@@ -120,21 +171,58 @@ __device__ __forceinline__ double m3_lane_f64(double v, int k)
     return __builtin_bit_cast(double, ((uint64_t)hi << 32U) | lo);
 }
 
-/* Four consecutive row elements starting at column c, as F32. */
+/* Four 16-bit values widened to F32. */
+__device__ __forceinline__ float4 m3_widen4(uint32_t lo, uint32_t hi,
+                                            uint32_t dtype)
+{
+    return make_float4(
+        m3_bits_f32(m3_load_as_f32_bits(lo & 0xffffU, dtype)),
+        m3_bits_f32(m3_load_as_f32_bits(lo >> 16U, dtype)),
+        m3_bits_f32(m3_load_as_f32_bits(hi & 0xffffU, dtype)),
+        m3_bits_f32(m3_load_as_f32_bits(hi >> 16U, dtype)));
+}
+
+/* Four consecutive row elements starting at column c, as F32, from an
+ * aligned row (16 bytes for F32, 8 for 16-bit dtypes). The rows are read
+ * once, so the loads are nontemporal. */
 template <bool F32IO>
 __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
                                                    uint64_t c, uint32_t dtype)
 {
     if (F32IO || dtype == M3N_F32) {
-        return *(const float4 *)(row + c * 4U);
-    }
-    uint2 h = *(const uint2 *)(row + c * 2U);
+        const m3_f32x4 w =
+            __builtin_nontemporal_load((const m3_f32x4 *)(row + c * 4U));
 
-    return make_float4(
-        m3_bits_f32(m3_load_as_f32_bits(h.x & 0xffffU, dtype)),
-        m3_bits_f32(m3_load_as_f32_bits(h.x >> 16U, dtype)),
-        m3_bits_f32(m3_load_as_f32_bits(h.y & 0xffffU, dtype)),
-        m3_bits_f32(m3_load_as_f32_bits(h.y >> 16U, dtype)));
+        return make_float4(w[0], w[1], w[2], w[3]);
+    }
+    const m3_u32x2 h =
+        __builtin_nontemporal_load((const m3_u32x2 *)(row + c * 2U));
+
+    return m3_widen4(h[0], h[1], dtype);
+}
+
+/* Columns c..c+3 of a row of `width` elements at any alignment, element
+ * by element; columns at or past the width read as -inf. */
+template <bool F32IO>
+__device__ __forceinline__ float4 m3_softmax_load4_masked(
+    const uint8_t *row, uint32_t c, uint32_t width, uint32_t dtype)
+{
+    float x[4];
+
+#pragma unroll
+    for (uint32_t i = 0U; i < 4U; ++i) {
+        const uint32_t col = min(c + i, width - 1U);
+        float value;
+
+        if (F32IO || dtype == M3N_F32) {
+            value = *(const float *)(row + (uint64_t)col * 4U);
+        } else {
+            value = m3_bits_f32(m3_load_as_f32_bits(
+                *(const uint16_t *)(row + (uint64_t)col * 2U), dtype));
+        }
+        x[i] = c + i < width ? value : -INFINITY;
+    }
+    return make_float4(x[0], x[1], x[2], x[3]);
 }
 
 /* Four results at column c, rounded to the output dtype (streaming
@@ -154,6 +242,59 @@ __device__ __forceinline__ void m3_softmax_store4(uint8_t *row, uint64_t c,
     packed.y = m3_store_from_f32_bits(m3_f32_bits(p.z), dtype) |
                (m3_store_from_f32_bits(m3_f32_bits(p.w), dtype) << 16U);
     m3_stream_store((uint2 *)(row + c * 2U), packed);
+}
+
+/* Stores the columns of c..c+3 that are inside the width, element by
+ * element (output rows of any width). */
+template <bool F32IO>
+__device__ __forceinline__ void m3_softmax_store4_masked(
+    uint8_t *row, uint32_t c, uint32_t width, uint32_t dtype, float4 p)
+{
+    const float x[4] = {p.x, p.y, p.z, p.w};
+
+#pragma unroll
+    for (uint32_t i = 0U; i < 4U; ++i) {
+        if (c + i >= width) {
+            continue;
+        }
+        if (F32IO || dtype == M3N_F32) {
+            __builtin_nontemporal_store(
+                x[i], (float *)(row + (uint64_t)(c + i) * 4U));
+        } else {
+            __builtin_nontemporal_store(
+                (uint16_t)m3_store_from_f32_bits(m3_f32_bits(x[i]), dtype),
+                (uint16_t *)(row + (uint64_t)(c + i) * 2U));
+        }
+    }
+}
+
+/* Loads and stores of four columns, vectorised for aligned rows whose
+ * width is a multiple of 4 (VEC) and element-wise otherwise. */
+template <bool F32IO, bool VEC>
+__device__ __forceinline__ float4 m3_softmax_get4(const uint8_t *row,
+                                                  uint32_t c, uint32_t width,
+                                                  uint32_t dtype)
+{
+    if (VEC) {
+        return c < width ? m3_softmax_load4<F32IO>(row, c, dtype)
+                         : make_float4(-INFINITY, -INFINITY, -INFINITY,
+                                       -INFINITY);
+    }
+    return m3_softmax_load4_masked<F32IO>(row, c, width, dtype);
+}
+
+template <bool F32IO, bool VEC>
+__device__ __forceinline__ void m3_softmax_put4(uint8_t *row, uint32_t c,
+                                                uint32_t width, uint32_t dtype,
+                                                float4 p)
+{
+    if (VEC) {
+        if (c < width) {
+            m3_softmax_store4<F32IO>(row, c, dtype, p);
+        }
+        return;
+    }
+    m3_softmax_store4_masked<F32IO>(row, c, width, dtype, p);
 }
 
 /* p = e / sum, the IEEE F32 quotient, for e >= 0 and sum >= 1 given
@@ -442,21 +583,75 @@ __device__ __forceinline__ void m3_wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-/* Wave-independent rows (width <= 256 * VPL, a multiple of 4). Each wave
- * takes R consecutive rows at a time and keeps them in VGPRs (VPL float4
- * per lane per row): it reduces max with shuffles, forms e_j in place,
- * then walks the row in 256-column chunks, writing each chunk of its R
- * rows to a wave-private LDS tile where lanes 0..R-1 continue their row's
- * left-to-right sum. The sum stops after the row's last nonzero e_j: the
- * trailing terms are +0 and leave a nonnegative F32 sum unchanged, so the
- * result is identical while masked (causal) rows cost half. p_j is formed
- * from the registers and streamed out with nontemporal stores. No
- * workgroup barrier is needed after the table copy, so waves of one CU
- * overlap their loads, arithmetic and sums freely. */
-template <int VPL, int R, int DEPTH, bool F32IO>
+/* Scales and stores one row of a register-resident task: p_j = e_j / sum
+ * for a finite maximum, zeros for an all -inf row, 1/k on the k +inf
+ * entries of a row whose maximum is +inf. `v` holds e_j (finite rows) or
+ * the inputs (other rows). */
+template <int VPL, bool F32IO, bool VEC>
+__device__ __forceinline__ void m3_softmax_emit_row(
+    const float4 (&v)[VPL], float maximum, double inverse, uint8_t *out,
+    uint32_t lane, uint32_t width, uint32_t out_dtype)
+{
+    if (maximum != INFINITY && maximum != -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const uint32_t c = lane * 4U + kChunk * j;
+
+            if (VEC && c >= width) {
+                continue;
+            }
+            m3_softmax_put4<F32IO, VEC>(out, c, width, out_dtype,
+                                        m3_softmax_scale4(v[j], inverse));
+        }
+        return;
+    }
+    float one_over_count = 0.0F;
+
+    if (maximum == INFINITY) {
+        uint32_t count = 0U;
+
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            count += (v[j].x == INFINITY) + (v[j].y == INFINITY) +
+                     (v[j].z == INFINITY) + (v[j].w == INFINITY);
+        }
+        one_over_count = 1.0F / (float)m3_wave_sum(count);
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const uint32_t c = lane * 4U + kChunk * j;
+        float4 p;
+
+        if (VEC && c >= width) {
+            continue;
+        }
+        p.x = v[j].x == INFINITY ? one_over_count : 0.0F;
+        p.y = v[j].y == INFINITY ? one_over_count : 0.0F;
+        p.z = v[j].z == INFINITY ? one_over_count : 0.0F;
+        p.w = v[j].w == INFINITY ? one_over_count : 0.0F;
+        m3_softmax_put4<F32IO, VEC>(out, c, width, out_dtype, p);
+    }
+}
+
+/* Wave-independent rows (width <= 256 * VPL). Each wave takes R
+ * consecutive rows at a time and keeps them in VGPRs, lane l holding
+ * columns 4l + 256j .. 4l + 256j + 3 (VPL float4 per lane per row). It
+ * reduces each row's maximum with DPP, forms e_j in place, then walks the
+ * row in 256-column chunks, writing each chunk of its R rows to a
+ * wave-private LDS tile where every lane continues the left-to-right sum
+ * of row l % R. All 64 lanes run that chain: a wave instruction takes the
+ * same issue slot at any lane count, and a full mask keeps the chain in
+ * one basic block with its LDS reads. The sum stops after the wave's last
+ * column holding something other than -inf: the later terms are +0 and
+ * leave a nonnegative F32 sum unchanged, so masked (causal) rows cost
+ * half. p_j is formed from the registers and streamed out. No workgroup
+ * barrier is needed after the table copy, so the waves of a CU overlap
+ * their loads, arithmetic and sums freely. VEC rows (aligned, width a
+ * multiple of 4) move in 16-byte (F32) or 8-byte (16-bit) accesses; other
+ * rows element by element, with columns past the width read as -inf. */
+template <int VPL, int R, int DEPTH, bool F32IO, bool VEC>
 __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
 {
-    static_assert(R <= (int)kSumLanes, "one summing lane per row");
     __shared__ float tiles[kWaves][R][kLine];
     __shared__ uint64_t exp_table[32];
     const uint32_t lane = threadIdx.x & 63U;
@@ -479,36 +674,38 @@ __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
         /* rows of this task that exist (the last task may be partial) */
         const uint32_t present =
             (uint32_t)min((uint64_t)R, a.rows - first_row);
-        const uint8_t *rows = a.input + first_row * a.row_stride;
         float4 v[R][VPL];
         float maximum[R];
-        uint32_t length[R]; /* elements up to the last nonzero e_j */
+        uint32_t last = 0U; /* 1 + index of the last float4 not all -inf */
 
         /* Every load is issued and none is under a branch, so the wave
          * waits for each row's data alone: row 0 is reduced and
          * exponentiated while the later rows are still arriving. A row past
          * the end of the tensor (the last task) reads the task's first row
-         * and is never stored. A column past the width reads four F32 -inf
-         * from m3_minus_inf4 (16-bit inputs: column 0, replaced by -inf).
-         * A variant serves widths above 256 * VPL / 2, so its chunks
+         * and is never stored. A VEC column past the width reads four F32
+         * -inf from m3_minus_inf4 (16-bit inputs: column 0, replaced by
+         * -inf). A variant serves widths above 256 * VPL / 2, so its chunks
          * j < VPL / 2 are always inside the row. */
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            const uint8_t *row =
-                rows + (uint64_t)((uint32_t)k < present ? (uint32_t)k : 0U) *
-                           a.row_stride;
+            const uint8_t *row = m3_softmax_row(
+                a, first_row + ((uint32_t)k < present ? (uint32_t)k : 0U));
 
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
                 const uint32_t c = lane * 4U + kChunk * j;
                 const bool inside = (VPL > 1 && j < VPL / 2) || c < width;
 
-                if (F32IO || in_dtype == M3N_F32) {
-                    const float4 *source =
-                        inside ? (const float4 *)(row + (uint64_t)c * 4U)
-                               : &m3_minus_inf4;
+                if (!VEC) {
+                    v[k][j] = m3_softmax_load4_masked<F32IO>(row, c, width,
+                                                             in_dtype);
+                } else if (F32IO || in_dtype == M3N_F32) {
+                    const m3_f32x4 *source =
+                        inside ? (const m3_f32x4 *)(row + (uint64_t)c * 4U)
+                               : (const m3_f32x4 *)&m3_minus_inf4;
+                    const m3_f32x4 w = __builtin_nontemporal_load(source);
 
-                    v[k][j] = *source;
+                    v[k][j] = make_float4(w[0], w[1], w[2], w[3]);
                 } else {
                     const float4 x = m3_softmax_load4<F32IO>(
                         row, inside ? c : 0U, in_dtype);
@@ -522,12 +719,14 @@ __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             float m = -INFINITY;
-            uint32_t last = 0U; /* 1 + index of the last nonzero float4 */
 
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
-                m = fmaxf(m, fmaxf(fmaxf(v[k][j].x, v[k][j].y),
-                                   fmaxf(v[k][j].z, v[k][j].w)));
+                const float t = fmaxf(fmaxf(v[k][j].x, v[k][j].y),
+                                      fmaxf(v[k][j].z, v[k][j].w));
+
+                m = fmaxf(m, t);
+                last = t != -INFINITY ? max(last, lane + 64U * j + 1U) : last;
             }
             m = m3_uniform_f32(m3_wave_max(m));
             maximum[k] = m;
@@ -538,28 +737,10 @@ __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
                     v[k][j].y = m3_expf_with_table(v[k][j].y - m, exp_table);
                     v[k][j].z = m3_expf_with_table(v[k][j].z - m, exp_table);
                     v[k][j].w = m3_expf_with_table(v[k][j].w - m, exp_table);
-
-                    uint32_t nonzero =
-                        m3_f32_bits(v[k][j].x) | m3_f32_bits(v[k][j].y) |
-                        m3_f32_bits(v[k][j].z) | m3_f32_bits(v[k][j].w);
-
-                    last = nonzero != 0U ? lane + 64U * j + 1U : last;
                 }
             }
-            length[k] = m3_uniform_u32(m3_wave_max_u32(last)) * 4U;
         }
-        uint32_t wave_length = 0U;
-
-#pragma unroll
-        for (int k = 0; k < R; ++k) {
-            wave_length = max(wave_length, length[k]);
-        }
-        /* The sums run on the 16 lanes of the wave's first lane group,
-         * lane l summing row l % R: a dependent add issued with a full
-         * 16-lane group measured about twice as fast on gfx950 as one
-         * issued for fewer lanes. Every lane sums up to the longest row's
-         * length; terms past a row's own length are +0 and leave its sum
-         * unchanged. Lanes 0..R-1 hold the R row sums. */
+        const uint32_t wave_length = m3_uniform_u32(m3_wave_max_u32(last)) * 4U;
         const float *line = tile + (lane % (uint32_t)R) * kLine;
         float sum = 0.0F;
 
@@ -575,124 +756,276 @@ __device__ __forceinline__ void m3_softmax_rows(const m3_softmax_args &a)
                 *(float4 *)(tile + k * kLine + lane * 4U) = v[k][j];
             }
             m3_wave_sync();
-            if (lane < kSumLanes) {
-                sum = m3_chunk_sum<DEPTH>(sum, line,
-                                          min(wave_length - base, kChunk));
-            }
+            sum = m3_chunk_sum<DEPTH>(sum, line,
+                                      min(wave_length - base, kChunk));
             m3_wave_sync();
         }
         const double inverse_of_lane = 1.0 / (double)sum;
 
-        uint8_t *out = a.output + first_row * out_pitch +
-                       (uint64_t)lane * 4U * out_size;
-
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            const float m = maximum[k];
-
             if ((uint32_t)k >= present) {
                 continue;
             }
-            if (m != INFINITY && m != -INFINITY) {
-                const double inverse = m3_lane_f64(inverse_of_lane, k);
-
-#pragma unroll
-                for (int j = 0; j < VPL; ++j) {
-                    const float4 e = v[k][j];
-                    float4 p;
-
-                    if (lane * 4U + kChunk * j >= width) {
-                        continue;
-                    }
-                    p = m3_softmax_scale4(e, inverse);
-                    m3_softmax_store4<F32IO>(out, (uint64_t)kChunk * j,
-                                             out_dtype, p);
-                }
-            } else if (m == -INFINITY) {
-                /* every entry is -inf: zeros */
-#pragma unroll
-                for (int j = 0; j < VPL; ++j) {
-                    if (lane * 4U + kChunk * j < width) {
-                        m3_softmax_store4<F32IO>(
-                            out, (uint64_t)kChunk * j, out_dtype,
-                            make_float4(0.0F, 0.0F, 0.0F, 0.0F));
-                    }
-                }
-            } else {
-                /* maximum +inf: 1/k on the k +inf entries, 0 elsewhere */
-                uint32_t count = 0U;
-
-#pragma unroll
-                for (int j = 0; j < VPL; ++j) {
-                    count += (v[k][j].x == INFINITY) +
-                             (v[k][j].y == INFINITY) +
-                             (v[k][j].z == INFINITY) +
-                             (v[k][j].w == INFINITY);
-                }
-                const float one_over_count =
-                    1.0F / (float)m3_wave_sum(count);
-
-#pragma unroll
-                for (int j = 0; j < VPL; ++j) {
-                    const float4 e = v[k][j];
-                    float4 p;
-
-                    if (lane * 4U + kChunk * j >= width) {
-                        continue;
-                    }
-                    p.x = e.x == INFINITY ? one_over_count : 0.0F;
-                    p.y = e.y == INFINITY ? one_over_count : 0.0F;
-                    p.z = e.z == INFINITY ? one_over_count : 0.0F;
-                    p.w = e.w == INFINITY ? one_over_count : 0.0F;
-                    m3_softmax_store4<F32IO>(out, (uint64_t)kChunk * j,
-                                             out_dtype, p);
-                }
-            }
-            out += out_pitch;
+            m3_softmax_emit_row<VPL, F32IO, VEC>(
+                v[k], maximum[k], m3_lane_f64(inverse_of_lane, k),
+                a.output + (first_row + (uint32_t)k) * out_pitch, lane, width,
+                out_dtype);
         }
     }
 }
 
-template <int VPL, int R, int DEPTH, bool F32IO>
+template <int VPL, int R, int DEPTH, bool F32IO, bool VEC>
 __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     m3_softmax_args a)
 {
-    m3_softmax_rows<VPL, R, DEPTH, F32IO>(a);
+    m3_softmax_rows<VPL, R, DEPTH, F32IO, VEC>(a);
+}
+
+/* Rows of any width, streamed: each wave owns kStreamRows consecutive rows
+ * and reads them three times, 256 columns at a time (lane l at columns
+ * 4l..4l+3 of each chunk):
+ *   pass 1  maximum, +inf count and the last column that is not -inf,
+ *           kStreamBatch chunks of loads in flight;
+ *   pass 2  e_j of each chunk into the wave's LDS tile, where every lane
+ *           continues the left-to-right sum of row l % kStreamRows; the
+ *           loads of the chunks kStreamBatch ahead are issued before each
+ *           chunk's sum, so they arrive while the chain runs;
+ *   pass 3  e_j again (the same function of the same input), scaled,
+ *           rounded and stored.
+ * Rows whose starts are not evenly spaced come from the outer axes. */
+template <bool F32IO, bool VEC>
+__global__ __launch_bounds__(256) void m3_softmax_stream_kernel(
+    m3_softmax_args a)
+{
+    constexpr int R = (int)kStreamRows;
+    constexpr int B = (int)kStreamBatch;
+    __shared__ float tiles[kWaves][R][kLine];
+    __shared__ uint64_t exp_table[32];
+    const uint32_t lane = threadIdx.x & 63U;
+    const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
+    const uint32_t width = a.width;
+    const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
+    const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
+    const uint32_t out_size = out_dtype == M3N_F32 ? 4U : 2U;
+    const uint64_t out_pitch = (uint64_t)width * out_size;
+    const uint64_t tasks = (a.rows + R - 1U) / R;
+    float *tile = &tiles[wave][0][0];
+
+    if (threadIdx.x < 32U) {
+        exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
+    }
+    __syncthreads();
+    for (uint64_t task = (uint64_t)blockIdx.x * kWaves + wave; task < tasks;
+         task += (uint64_t)gridDim.x * kWaves) {
+        const uint64_t first_row = task * R;
+        const uint32_t present =
+            (uint32_t)min((uint64_t)R, a.rows - first_row);
+        const uint8_t *rows[R];
+        float maximum[R];
+        uint32_t infinities[R];
+        uint32_t last[R];
+
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            rows[k] = m3_softmax_row(
+                a, first_row + ((uint32_t)k < present ? (uint32_t)k : 0U));
+            maximum[k] = -INFINITY;
+            infinities[k] = 0U;
+            last[k] = 0U;
+        }
+        /* pass 1 */
+        for (uint32_t c0 = 0U; c0 < width; c0 += kChunk * B) {
+            float4 x[R][B];
+
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    x[k][b] = m3_softmax_get4<F32IO, VEC>(
+                        rows[k], c0 + kChunk * b + lane * 4U, width, in_dtype);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    const float4 e = x[k][b];
+                    const float t = fmaxf(fmaxf(e.x, e.y), fmaxf(e.z, e.w));
+
+                    maximum[k] = fmaxf(maximum[k], t);
+                    infinities[k] += (e.x == INFINITY) + (e.y == INFINITY) +
+                                     (e.z == INFINITY) + (e.w == INFINITY);
+                    last[k] = t != -INFINITY
+                                  ? (c0 + kChunk * b) / 4U + lane + 1U
+                                  : last[k];
+                }
+            }
+        }
+        uint32_t wave_length = 0U;
+        bool finite[R];
+
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            maximum[k] = m3_uniform_f32(m3_wave_max(maximum[k]));
+            finite[k] = maximum[k] != INFINITY && maximum[k] != -INFINITY;
+            infinities[k] = m3_uniform_u32(m3_wave_sum(infinities[k]));
+            last[k] = m3_uniform_u32(m3_wave_max_u32(last[k])) * 4U;
+            if (finite[k]) {
+                wave_length = max(wave_length, last[k]);
+            }
+        }
+        /* pass 2: the in-order sums of the finite rows */
+        const float *line = tile + (lane % (uint32_t)R) * kLine;
+        float sum = 0.0F;
+        float4 ahead[B][R];
+
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                ahead[b][k] = m3_softmax_get4<F32IO, VEC>(
+                    rows[k], kChunk * b + lane * 4U, min(width, wave_length),
+                    in_dtype);
+            }
+        }
+        for (uint32_t c0 = 0U; c0 < wave_length; c0 += kChunk * B) {
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const uint32_t base = c0 + kChunk * b;
+
+                if (base >= wave_length) {
+                    break;
+                }
+#pragma unroll
+                for (int k = 0; k < R; ++k) {
+                    float4 e = ahead[b][k];
+
+                    if (finite[k]) {
+                        e.x = m3_expf_with_table(e.x - maximum[k], exp_table);
+                        e.y = m3_expf_with_table(e.y - maximum[k], exp_table);
+                        e.z = m3_expf_with_table(e.z - maximum[k], exp_table);
+                        e.w = m3_expf_with_table(e.w - maximum[k], exp_table);
+                    } else {
+                        e = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+                    }
+                    *(float4 *)(tile + k * kLine + lane * 4U) = e;
+                    ahead[b][k] = m3_softmax_get4<F32IO, VEC>(
+                        rows[k], base + kChunk * B + lane * 4U,
+                        min(width, wave_length), in_dtype);
+                }
+                m3_wave_sync();
+                sum = m3_chunk_sum<4>(
+                    sum, line, (min(wave_length - base, kChunk) + 3U) & ~3U);
+                m3_wave_sync();
+            }
+        }
+        const double inverse_of_lane = 1.0 / (double)sum;
+        double inverse[R];
+        float one_over_count[R];
+
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            inverse[k] = m3_lane_f64(inverse_of_lane, k);
+            one_over_count[k] = 1.0F / (float)infinities[k];
+        }
+        /* pass 3 */
+        for (uint32_t c0 = 0U; c0 < width; c0 += kChunk * B) {
+            float4 x[R][B];
+
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    x[k][b] = m3_softmax_get4<F32IO, VEC>(
+                        rows[k], c0 + kChunk * b + lane * 4U, width, in_dtype);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                if ((uint32_t)k >= present) {
+                    continue;
+                }
+                uint8_t *out = a.output + (first_row + (uint32_t)k) * out_pitch;
+
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    const uint32_t c = c0 + kChunk * b + lane * 4U;
+                    const float4 v = x[k][b];
+                    float4 p;
+
+                    if (finite[k]) {
+                        p.x = m3_expf_with_table(v.x - maximum[k], exp_table);
+                        p.y = m3_expf_with_table(v.y - maximum[k], exp_table);
+                        p.z = m3_expf_with_table(v.z - maximum[k], exp_table);
+                        p.w = m3_expf_with_table(v.w - maximum[k], exp_table);
+                        p = m3_softmax_scale4(p, inverse[k]);
+                    } else {
+                        const float q = maximum[k] == INFINITY
+                                            ? one_over_count[k]
+                                            : 0.0F;
+
+                        p.x = v.x == INFINITY ? q : 0.0F;
+                        p.y = v.y == INFINITY ? q : 0.0F;
+                        p.z = v.z == INFINITY ? q : 0.0F;
+                        p.w = v.w == INFINITY ? q : 0.0F;
+                    }
+                    if (c0 + kChunk * b < width) {
+                        m3_softmax_put4<F32IO, VEC>(out, c, width, out_dtype,
+                                                    p);
+                    }
+                }
+            }
+        }
+    }
 }
 
 typedef void (*m3_softmax_launcher)(dim3, hipStream_t, hipEvent_t,
                                     hipEvent_t, m3_softmax_args);
 
-template <int VPL, int R, int DEPTH, bool F32IO>
+template <int VPL, int R, int DEPTH, bool F32IO, bool VEC>
 void m3_launch_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                     hipEvent_t stop, m3_softmax_args args)
 {
-    hipExtLaunchKernelGGL((m3_softmax_rows_kernel<VPL, R, DEPTH, F32IO>),
+    hipExtLaunchKernelGGL((m3_softmax_rows_kernel<VPL, R, DEPTH, F32IO, VEC>),
                           grid, dim3(kThreads), 0, stream, start, stop, 0U,
                           args);
+}
+
+template <bool F32IO, bool VEC>
+void m3_launch_stream(dim3 grid, hipStream_t stream, hipEvent_t start,
+                      hipEvent_t stop, m3_softmax_args args)
+{
+    hipExtLaunchKernelGGL((m3_softmax_stream_kernel<F32IO, VEC>), grid,
+                          dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
 struct m3_rows_variant {
     uint32_t vectors_per_lane;
     uint32_t rows_per_wave;
-    m3_softmax_launcher f32;
-    m3_softmax_launcher other;
+    m3_softmax_launcher f32;      /* F32 in and out, VEC rows */
+    m3_softmax_launcher other;    /* any dtypes, VEC rows */
+    m3_softmax_launcher elements; /* any dtypes, element-wise rows */
 };
 
 /* Wave-independent variants; the first whose width class fits is used.
  * Rows per wave and sum prefetch depth are chosen for four waves per SIMD
- * (88, 98 and 120 VGPRs for the F32 instances up to width 1024); the
- * width-2048 instance and the 16-bit-IO instances from width 1024 take
- * 133-157 VGPRs, three waves per SIMD. */
+ * at widths up to 1024 with F32 in and out; the width-2048 instance and
+ * the 16-bit-IO instances from width 1024 take more VGPRs and run three
+ * waves per SIMD. */
 const m3_rows_variant m3_rows_variants[] = {
-    {1U, 8U, &m3_launch_rows<1, 8, 8, true>,
-     &m3_launch_rows<1, 8, 8, false>},
-    {2U, 4U, &m3_launch_rows<2, 4, 8, true>,
-     &m3_launch_rows<2, 4, 8, false>},
-    {4U, 4U, &m3_launch_rows<4, 4, 4, true>,
-     &m3_launch_rows<4, 4, 4, false>},
-    {8U, 2U, &m3_launch_rows<8, 2, 4, true>,
-     &m3_launch_rows<8, 2, 4, false>},
+    {1U, 8U, &m3_launch_rows<1, 8, 8, true, true>,
+     &m3_launch_rows<1, 8, 8, false, true>,
+     &m3_launch_rows<1, 8, 8, false, false>},
+    {2U, 4U, &m3_launch_rows<2, 4, 8, true, true>,
+     &m3_launch_rows<2, 4, 8, false, true>,
+     &m3_launch_rows<2, 4, 8, false, false>},
+    {4U, 4U, &m3_launch_rows<4, 4, 4, true, true>,
+     &m3_launch_rows<4, 4, 4, false, true>,
+     &m3_launch_rows<4, 4, 4, false, false>},
+    {8U, 2U, &m3_launch_rows<8, 2, 4, true, true>,
+     &m3_launch_rows<8, 2, 4, false, true>,
+     &m3_launch_rows<8, 2, 4, false, false>},
 };
 
 struct m3_softmax_general_args {
@@ -827,36 +1160,45 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
     outer.rank = input->rank - 1U;
     m3_plan_index_space(&outer, operands, 1U, &plan);
 
-    bool uniform_rows = plan.rank == 1U;
-    uint64_t row_stride = uniform_rows ? (uint64_t)plan.strides[0][0] : 0U;
-    bool columns_contiguous =
+    if (width > 0xffffffffULL) {
+        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
+                           "softmax rows longer than 2^32 are unsupported");
+    }
+    const bool uniform_rows = plan.rank == 1U || rows == 1U;
+    const bool columns_contiguous =
         width == 1U ||
         input->byte_strides[input->rank - 1U] == (uint64_t)in_size;
 
-    if (rows == 1U) {
-        uniform_rows = true;
-        row_stride = 0U;
-    }
-    if (uniform_rows && columns_contiguous && width % 4U == 0U &&
-        width <= kMaxWidth && row_stride % (4U * in_size) == 0U &&
-        ((uintptr_t)in % (4U * in_size)) == 0U &&
-        ((uintptr_t)out % (4U * out_size)) == 0U &&
-        plan.strides[0][0] >= 0) {
+    if (columns_contiguous) {
         m3_softmax_args args;
-        uint32_t pitch_bytes = ((uint32_t)width + kPad) * 4U;
-        uint32_t budget = device->lds_per_block > kStaticLds
-                              ? device->lds_per_block - kStaticLds
-                              : 0U;
-        bool f32 = input->dtype == M3_HIP_F32 && output->dtype == M3_HIP_F32;
+        /* VEC rows: every row start aligned for 4-element accesses */
+        bool vec = width % 4U == 0U &&
+                   ((uintptr_t)in % (4U * in_size)) == 0U &&
+                   ((uintptr_t)out % (4U * out_size)) == 0U;
+        const bool f32 =
+            input->dtype == M3_HIP_F32 && output->dtype == M3_HIP_F32;
 
         std::memset(&args, 0, sizeof(args));
         args.input = in;
         args.output = out;
         args.rows = rows;
-        args.row_stride = row_stride;
         args.width = (uint32_t)width;
         args.in_dtype = input->dtype;
         args.out_dtype = output->dtype;
+        if (uniform_rows) {
+            args.outer_rank = 1U;
+            args.row_stride = rows == 1U ? 0U : (uint64_t)plan.strides[0][0];
+            vec = vec && args.row_stride % (4U * in_size) == 0U;
+        } else {
+            args.outer_rank = plan.rank;
+            for (uint32_t axis = 0U; axis < plan.rank; ++axis) {
+                args.outer_shape[axis] = plan.shape[axis];
+                args.outer_strides[axis] = plan.strides[0][axis];
+                vec = vec && (uint64_t)plan.strides[0][axis] %
+                                     (4U * in_size) ==
+                                 0U;
+            }
+        }
         for (const m3_rows_variant &variant : m3_rows_variants) {
             if (width > kChunk * variant.vectors_per_lane) {
                 continue;
@@ -865,7 +1207,8 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
                 (rows + variant.rows_per_wave - 1U) / variant.rows_per_wave;
             uint64_t blocks = (tasks + kWaves - 1U) / kWaves;
             dim3 grid((uint32_t)(blocks < kMaxGrid ? blocks : kMaxGrid));
-            m3_softmax_launcher launcher = f32 ? variant.f32 : variant.other;
+            m3_softmax_launcher launcher =
+                !vec ? variant.elements : f32 ? variant.f32 : variant.other;
 
             return m3_hip_launch(
                 device, "m3_softmax_rows",
@@ -874,13 +1217,18 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
                 },
                 message, capacity);
         }
-        /* Rows wider than the register variants: whole rows in LDS,
-         * within the dynamic LDS a launch gets without opting in. */
+        /* Rows wider than the register variants: whole rows in LDS when
+         * they fit the dynamic LDS a launch gets without opting in. */
+        uint32_t pitch_bytes = ((uint32_t)width + kPad) * 4U;
+        uint32_t budget = device->lds_per_block > kStaticLds
+                              ? device->lds_per_block - kStaticLds
+                              : 0U;
+
         budget = budget > kTiledLdsCap ? kTiledLdsCap : budget;
-        uint32_t tile_rows = budget / pitch_bytes;
+        uint32_t tile_rows = width <= kMaxWidth ? budget / pitch_bytes : 0U;
 
         tile_rows = tile_rows > kMaxTileRows ? kMaxTileRows : tile_rows;
-        if (tile_rows != 0U) {
+        if (vec && uniform_rows && tile_rows != 0U) {
             args.tile_rows = tile_rows;
             uint64_t tiles = (rows + tile_rows - 1U) / tile_rows;
             uint32_t blocks =
@@ -906,6 +1254,20 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
                 },
                 message, capacity);
         }
+        /* Any other row: streamed through three passes. */
+        uint64_t tasks = (rows + kStreamRows - 1U) / kStreamRows;
+        uint64_t blocks = (tasks + kWaves - 1U) / kWaves;
+        dim3 grid((uint32_t)(blocks < kMaxGrid ? blocks : kMaxGrid));
+        m3_softmax_launcher launcher = !vec ? &m3_launch_stream<false, false>
+                                       : f32 ? &m3_launch_stream<true, true>
+                                             : &m3_launch_stream<false, true>;
+
+        return m3_hip_launch(
+            device, "m3_softmax_rows_streamed",
+            [&](hipEvent_t start, hipEvent_t stop) {
+                launcher(grid, device->stream, start, stop, args);
+            },
+            message, capacity);
     }
 
     m3_softmax_general_args general;
@@ -922,10 +1284,6 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
     for (uint32_t axis = 0U; axis < plan.rank; ++axis) {
         general.outer_shape[axis] = plan.shape[axis];
         general.outer_strides[axis] = plan.strides[0][axis];
-    }
-    if (width > 0xffffffffULL) {
-        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
-                           "softmax rows longer than 2^32 are unsupported");
     }
     uint32_t blocks = m3_grid_blocks(device, rows, 64U, 16U);
 

@@ -320,6 +320,88 @@ def test_softmax_subnormal_ties(hip, width):
             "softmax subnormal ties w=%d" % width)
 
 
+def softmax_source(logits, dtype):
+    if dtype == m3.F16:
+        return as_bytes(logits.astype(np.float16).view(np.uint16))
+    if dtype == m3.BF16:
+        return as_bytes((logits.view(np.uint32) >> 16).astype(np.uint16))
+    return as_bytes(logits)
+
+
+@pytest.mark.parametrize("width", [77, 1001, 2047, 2501, 9000, 9001, 16384,
+                                   32768])
+def test_softmax_any_width(hip, width):
+    """Widths that are not a multiple of 4 move element by element (77,
+    1001 and 2047 in registers, 2501 and 9001 streamed); rows wider than
+    the LDS tile (9000, 16384, 32768) stream through three passes."""
+    rng = np.random.default_rng(15000 + width)
+    rows = max(6, min(96, 600000 // width))
+    logits = softmax_logits(rng, rows, width)
+    if rows >= 6:
+        logits[4, width // 2:] = -np.inf
+        logits[5, :] = -200.0
+        logits[5, width - 1] = 0.0
+    views = [ViewSpec(0, m3.F32, (rows, width)),
+             ViewSpec(1, m3.F32, (rows, width))]
+    storages = [as_bytes(logits), np.zeros(logits.nbytes, np.uint8)]
+    compare(hip, m3.OP_SOFTMAX, storages, views, "softmax any w=%d" % width)
+
+
+@pytest.mark.parametrize("dtypes", [(m3.F16, m3.F16), (m3.BF16, m3.F32),
+                                    (m3.F32, m3.BF16)])
+@pytest.mark.parametrize("width", [77, 1001, 16384])
+def test_softmax_any_width_dtypes(hip, dtypes, width):
+    rng = np.random.default_rng(16000 + width + 7 * dtypes[0] + dtypes[1])
+    rows = 24
+    logits = softmax_logits(rng, rows, width)
+    views = [ViewSpec(0, dtypes[0], (rows, width)),
+             ViewSpec(1, dtypes[1], (rows, width))]
+    storages = [softmax_source(logits, dtypes[0]),
+                np.zeros(rows * width * m3.DTYPE_SIZES[dtypes[1]], np.uint8)]
+    compare(hip, m3.OP_SOFTMAX, storages, views,
+            "softmax any %s w=%d" % (dtypes, width))
+
+
+@pytest.mark.parametrize("width", [100, 1000, 12000])
+def test_softmax_row_layouts(hip, width):
+    """Row starts that are padded, unaligned, or not evenly spaced (outer
+    axes that do not merge), for register-resident and streamed rows."""
+    rng = np.random.default_rng(17000 + width)
+    rows = 24
+    logits = softmax_logits(rng, rows, width)
+    out = np.zeros(logits.nbytes, np.uint8)
+    # padded rows
+    pitch = width + 13
+    padded = np.full((rows, pitch), 5.0, np.float32)
+    padded[:, :width] = logits
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(padded), out],
+            [ViewSpec(0, m3.F32, (rows, width), (pitch * 4, 4)),
+             ViewSpec(1, m3.F32, (rows, width))],
+            "softmax padded odd pitch w=%d" % width)
+    # a row start 4 bytes past a 16-byte boundary
+    shifted = np.zeros(logits.size + 1, np.float32)
+    shifted[1:] = logits.ravel()
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(shifted), out],
+            [ViewSpec(0, m3.F32, (rows, width), None, 4),
+             ViewSpec(1, m3.F32, (rows, width))],
+            "softmax unaligned start w=%d" % width)
+    # outer axes (4, 6) read from a (6, 4, width) layout: uneven row starts
+    stack = logits.reshape(6, 4, width)
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(stack), out],
+            [ViewSpec(0, m3.F32, (4, 6, width),
+                      (width * 4, 4 * width * 4, 4)),
+             ViewSpec(1, m3.F32, (4, 6, width))],
+            "softmax uneven rows w=%d" % width)
+    # the same with 16-bit input and output
+    half = softmax_source(logits, m3.F16)
+    compare(hip, m3.OP_SOFTMAX,
+            [half, np.zeros(rows * width * 2, np.uint8)],
+            [ViewSpec(0, m3.F16, (4, 6, width),
+                      (width * 2, 4 * width * 2, 2)),
+             ViewSpec(1, m3.BF16, (4, 6, width))],
+            "softmax uneven rows f16->bf16 w=%d" % width)
+
+
 def test_softmax_strided_and_in_place(hip):
     rng = np.random.default_rng(9)
     logits = softmax_logits(rng, 64, 1024)
