@@ -510,8 +510,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--rotate", type=int, default=4)
     parser.add_argument("--classes",
-                        default="softmax,mul,cast,copy,snake,tanh,gated_silu,"
-                                "euler,executor",
+                        default="softmax,softmax_wide,mul,cast,copy,snake,"
+                                "tanh,gated_silu,euler,executor",
                         help="comma-separated op classes to run")
     parser.add_argument("--no-cpu", action="store_true",
                         help="skip the CPU baseline and CPU parity check")
@@ -569,6 +569,34 @@ def main():
         headline = (w.rotate, wall, kus, nbytes)
         w.free()
         log("softmax:", json.dumps(results["softmax"]))
+
+    if "softmax_wide" in classes:
+        log("softmax_wide: generating [4096,16384] logits")
+        s = m3.rng_fill("normal", 4096 * 16384, seed=1, a=3.0).reshape(
+            4096, 16384)
+        nbytes = 2 * s.nbytes
+        w = Workload("softmax_wide", build_softmax(s), [s], nbytes,
+                     ["m3_softmax_rows_streamed"], args.rotate, cpu)
+        wall, kus, launches, kernels, _ = w.measure(args.steps, args.warmup)
+        parity = None
+        cpu_seconds = None
+        if cpu is not None:
+            out = w.read_output()
+            status, storages, cpu_seconds = cpu.timed(
+                m3.OP_SOFTMAX, [as_bytes(s), np.zeros(s.nbytes, np.uint8)],
+                [spec(0, m3.F32, s.shape), spec(1, m3.F32, s.shape)])
+            ref = storages[1].view(np.float32).reshape(s.shape)
+            mismatches = int(np.count_nonzero(ref.view(np.uint32) !=
+                                              out.view(np.uint32)))
+            parity = "bit-exact" if mismatches == 0 else \
+                "%d of %d elements differ" % (mismatches, s.size)
+        results["softmax_wide"] = result_entry(
+            "softmax_wide", w, wall, kus, launches, nbytes, nbytes, parity,
+            cpu_seconds, nbytes)
+        results["softmax_wide"]["kernels"] = {
+            k: v[1] / max(v[0], 1) * 1000 for k, v in kernels.items()}
+        w.free()
+        log("softmax_wide:", json.dumps(results["softmax_wide"]))
 
     if "mul" in classes:
         log("mul: generating x[8,1024,1536], c[1536]")

@@ -55,8 +55,8 @@ constexpr uint32_t kPad = 4U;
 constexpr uint32_t kChunk = 256U;         /* columns per LDS chunk */
 constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
 constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
-constexpr uint32_t kStreamRows = 4U;      /* rows per wave, streamed kernel */
-constexpr uint32_t kStreamBatch = 4U;     /* chunks per batch of loads */
+constexpr uint32_t kStreamRows = 4U; /* rows per workgroup, streamed kernel */
+constexpr uint32_t kChainLanes = 16U; /* lanes of the streamed chains */
 
 /* Four F32 -inf: what a load past the end of a row reads instead. Never
  * written; not const, so that it is in the global address space like the
@@ -269,18 +269,33 @@ __device__ __forceinline__ void m3_softmax_store4_masked(
 }
 
 /* Loads and stores of four columns, vectorised for aligned rows whose
- * width is a multiple of 4 (VEC) and element-wise otherwise. */
+ * width is a multiple of 4 (VEC) and element-wise otherwise. No load sits
+ * under a branch: a column past the width loads from an address that is
+ * always valid (m3_minus_inf4, or the row's first columns) and the result
+ * is replaced, so the compiler can wait for each load alone instead of
+ * for every load in flight. */
 template <bool F32IO, bool VEC>
 __device__ __forceinline__ float4 m3_softmax_get4(const uint8_t *row,
                                                   uint32_t c, uint32_t width,
                                                   uint32_t dtype)
 {
-    if (VEC) {
-        return c < width ? m3_softmax_load4<F32IO>(row, c, dtype)
-                         : make_float4(-INFINITY, -INFINITY, -INFINITY,
-                                       -INFINITY);
+    if (!VEC) {
+        return m3_softmax_load4_masked<F32IO>(row, c, width, dtype);
     }
-    return m3_softmax_load4_masked<F32IO>(row, c, width, dtype);
+    const bool inside = c < width;
+
+    if (F32IO || dtype == M3N_F32) {
+        const m3_f32x4 *source =
+            inside ? (const m3_f32x4 *)(row + (uint64_t)c * 4U)
+                   : (const m3_f32x4 *)&m3_minus_inf4;
+        const m3_f32x4 w = __builtin_nontemporal_load(source);
+
+        return make_float4(w[0], w[1], w[2], w[3]);
+    }
+    const float4 x = m3_softmax_load4<F32IO>(row, inside ? c : 0U, dtype);
+
+    return inside ? x
+                  : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
 }
 
 template <bool F32IO, bool VEC>
@@ -782,25 +797,86 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     m3_softmax_rows<VPL, R, DEPTH, F32IO, VEC>(a);
 }
 
-/* Rows of any width, streamed: each wave owns kStreamRows consecutive rows
- * and reads them three times, 256 columns at a time (lane l at columns
- * 4l..4l+3 of each chunk):
- *   pass 1  maximum, +inf count and the last column that is not -inf,
- *           kStreamBatch chunks of loads in flight;
- *   pass 2  e_j of each chunk into the wave's LDS tile, where every lane
- *           continues the left-to-right sum of row l % kStreamRows; the
- *           loads of the chunks kStreamBatch ahead are issued before each
- *           chunk's sum, so they arrive while the chain runs;
- *   pass 3  e_j again (the same function of the same input), scaled,
- *           rounded and stored.
+/* The full 256-column left-to-right sum of an LDS line, continuing s, in
+ * eight groups of 32 columns: each group's reads are issued before the
+ * previous group's dependent additions, so 32 additions cover the LDS
+ * latency. An empty asm statement that takes the running sum and clobbers
+ * memory ends each group and keeps that shape; without it the compiler
+ * hoists all 64 reads ahead of the chain (256 registers), and a loop
+ * would copy the look-ahead registers each iteration. */
+__device__ __forceinline__ float m3_chunk_sum_full(float s, const float *line)
+{
+    float4 group[2][8];
+
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        group[0][i] = *(const float4 *)(line + 4 * i);
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        if (g + 1 < 8) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                group[(g + 1) & 1][i] =
+                    *(const float4 *)(line + 32 * (g + 1) + 4 * i);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            s = m3_add4(s, group[g & 1][i]);
+        }
+        asm volatile("" : "+v"(s) : : "memory");
+    }
+    return s;
+}
+
+/* x where mask is all ones, +0 where it is zero. */
+__device__ __forceinline__ float4 m3_keep4(float4 x, uint32_t mask)
+{
+    return make_float4(m3_bits_f32(m3_f32_bits(x.x) & mask),
+                       m3_bits_f32(m3_f32_bits(x.y) & mask),
+                       m3_bits_f32(m3_f32_bits(x.z) & mask),
+                       m3_bits_f32(m3_f32_bits(x.w) & mask));
+}
+
+/* e_j of four inputs against the row maximum m. */
+__device__ __forceinline__ float4 m3_exp4(float4 v, float m,
+                                          const uint64_t *table)
+{
+    return make_float4(m3_expf_with_table(v.x - m, table),
+                       m3_expf_with_table(v.y - m, table),
+                       m3_expf_with_table(v.z - m, table),
+                       m3_expf_with_table(v.w - m, table));
+}
+
+/* Rows of any width, streamed by a workgroup of four waves that owns R
+ * consecutive rows and reads them three times in 256-column chunks, lane l
+ * at columns 4l..4l+3 of a chunk:
+ *   pass 1  wave w takes the chunks w, w+4, ...: maximum, +inf count and
+ *           last column that is not -inf, combined through LDS;
+ *   pass 2  the in-order sums. One wave runs the chains (every lane l
+ *           continues the left-to-right sum of row l % R) while the other
+ *           three produce the e_j of the next chunks into an LDS ring, one
+ *           chunk each per step: the chain, a serial sum of width terms per
+ *           row, is the critical path, and the exponentials run beside it
+ *           on other SIMDs instead of in front of it;
+ *   pass 3  wave w takes the chunks w, w+4, ... again: e_j (the same
+ *           function of the same input), scaled, rounded and stored.
+ * The sums stop after the last column holding something other than -inf
+ * in a row with a finite maximum (later terms are +0). Rows past the end
+ * of the tensor repeat the task's first row and store its values again.
  * Rows whose starts are not evenly spaced come from the outer axes. */
 template <bool F32IO, bool VEC>
-__global__ __launch_bounds__(256) void m3_softmax_stream_kernel(
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
     m3_softmax_args a)
 {
     constexpr int R = (int)kStreamRows;
-    constexpr int B = (int)kStreamBatch;
-    __shared__ float tiles[kWaves][R][kLine];
+    constexpr int P = (int)kWaves - 1; /* producer waves */
+    __shared__ float ring[2 * P][R][kLine];
+    __shared__ float part_max[kWaves][R];
+    __shared__ uint32_t part_inf[kWaves][R];
+    __shared__ uint32_t part_last[kWaves][R];
     __shared__ uint64_t exp_table[32];
     const uint32_t lane = threadIdx.x & 63U;
     const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
@@ -810,173 +886,211 @@ __global__ __launch_bounds__(256) void m3_softmax_stream_kernel(
     const uint32_t out_size = out_dtype == M3N_F32 ? 4U : 2U;
     const uint64_t out_pitch = (uint64_t)width * out_size;
     const uint64_t tasks = (a.rows + R - 1U) / R;
-    float *tile = &tiles[wave][0][0];
+    const uint32_t chunks = (width + kChunk - 1U) / kChunk;
 
     if (threadIdx.x < 32U) {
         exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
     }
-    __syncthreads();
-    for (uint64_t task = (uint64_t)blockIdx.x * kWaves + wave; task < tasks;
-         task += (uint64_t)gridDim.x * kWaves) {
+    for (uint64_t task = blockIdx.x; task < tasks; task += gridDim.x) {
         const uint64_t first_row = task * R;
         const uint32_t present =
             (uint32_t)min((uint64_t)R, a.rows - first_row);
         const uint8_t *rows[R];
+        uint8_t *outs[R];
         float maximum[R];
         uint32_t infinities[R];
         uint32_t last[R];
 
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            rows[k] = m3_softmax_row(
-                a, first_row + ((uint32_t)k < present ? (uint32_t)k : 0U));
+            const uint64_t row =
+                first_row + ((uint32_t)k < present ? (uint32_t)k : 0U);
+
+            rows[k] = m3_softmax_row(a, row);
+            outs[k] = a.output + row * out_pitch;
             maximum[k] = -INFINITY;
             infinities[k] = 0U;
             last[k] = 0U;
         }
-        /* pass 1 */
-        for (uint32_t c0 = 0U; c0 < width; c0 += kChunk * B) {
-            float4 x[R][B];
+        /* pass 1: two chunks per iteration keep 2R loads in flight */
+        for (uint32_t j = wave; j < chunks; j += 2U * kWaves) {
+            float4 x[R][2];
 
 #pragma unroll
             for (int k = 0; k < R; ++k) {
 #pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    x[k][b] = m3_softmax_get4<F32IO, VEC>(
-                        rows[k], c0 + kChunk * b + lane * 4U, width, in_dtype);
+                for (int h = 0; h < 2; ++h) {
+                    x[k][h] = m3_softmax_get4<F32IO, VEC>(
+                        rows[k], (j + h * kWaves) * kChunk + lane * 4U, width,
+                        in_dtype);
                 }
             }
 #pragma unroll
             for (int k = 0; k < R; ++k) {
 #pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const float4 e = x[k][b];
+                for (int h = 0; h < 2; ++h) {
+                    const float4 e = x[k][h];
                     const float t = fmaxf(fmaxf(e.x, e.y), fmaxf(e.z, e.w));
 
                     maximum[k] = fmaxf(maximum[k], t);
                     infinities[k] += (e.x == INFINITY) + (e.y == INFINITY) +
                                      (e.z == INFINITY) + (e.w == INFINITY);
                     last[k] = t != -INFINITY
-                                  ? (c0 + kChunk * b) / 4U + lane + 1U
+                                  ? max(last[k], (j + h * kWaves) * 64U +
+                                                     lane + 1U)
                                   : last[k];
                 }
             }
         }
-        uint32_t wave_length = 0U;
-        bool finite[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const float m = m3_wave_max(maximum[k]);
+            const uint32_t n = m3_wave_sum(infinities[k]);
+            const uint32_t l = m3_wave_max_u32(last[k]);
+
+            if (lane == 0U) {
+                part_max[wave][k] = m;
+                part_inf[wave][k] = n;
+                part_last[wave][k] = l;
+            }
+        }
+        __syncthreads();
+        uint32_t length = 0U;
+        uint32_t finite[R]; /* all ones for a finite maximum, else zero */
 
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            maximum[k] = m3_uniform_f32(m3_wave_max(maximum[k]));
-            finite[k] = maximum[k] != INFINITY && maximum[k] != -INFINITY;
-            infinities[k] = m3_uniform_u32(m3_wave_sum(infinities[k]));
-            last[k] = m3_uniform_u32(m3_wave_max_u32(last[k])) * 4U;
-            if (finite[k]) {
-                wave_length = max(wave_length, last[k]);
-            }
-        }
-        /* pass 2: the in-order sums of the finite rows */
-        const float *line = tile + (lane % (uint32_t)R) * kLine;
-        float sum = 0.0F;
-        float4 ahead[B][R];
+            float m = part_max[0][k];
+            uint32_t n = part_inf[0][k];
+            uint32_t l = part_last[0][k];
 
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
+            for (uint32_t w = 1U; w < kWaves; ++w) {
+                m = fmaxf(m, part_max[w][k]);
+                n += part_inf[w][k];
+                l = max(l, part_last[w][k]);
+            }
+            maximum[k] = m3_uniform_f32(m);
+            infinities[k] = m3_uniform_u32(n);
+            finite[k] =
+                maximum[k] != INFINITY && maximum[k] != -INFINITY ? ~0U : 0U;
+            length = max(length, (m3_uniform_u32(l) * 4U) & finite[k]);
+        }
+        /* pass 2 */
+        const uint32_t sum_chunks = (min(width, length) + kChunk - 1U) / kChunk;
+        const uint32_t steps = (sum_chunks + P - 1U) / P;
+        float sum = 0.0F;
+
+        /* the consumer role rotates with the task so that the chains of the
+         * workgroups sharing a CU run on different SIMDs */
+        const uint32_t consumer = (uint32_t)(task % kWaves);
+        const uint32_t producer = (wave + kWaves - consumer - 1U) % kWaves;
+
+        /* a producer's inputs arrive two steps after their loads issue */
+        const uint32_t seen = min(width, length);
+        float4 x[2][R];
+
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int k = 0; k < R; ++k) {
-                ahead[b][k] = m3_softmax_get4<F32IO, VEC>(
-                    rows[k], kChunk * b + lane * 4U, min(width, wave_length),
+                x[h][k] = m3_softmax_get4<F32IO, VEC>(
+                    rows[k], (h * P + producer) * kChunk + lane * 4U, seen,
                     in_dtype);
             }
         }
-        for (uint32_t c0 = 0U; c0 < wave_length; c0 += kChunk * B) {
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const uint32_t base = c0 + kChunk * b;
+        for (uint32_t step = 0U; step <= steps; ++step) {
+            if (wave != consumer) {
+                /* producer p: chunk step * P + p into its ring slot (chunks
+                 * past the sums, -inf, give zeros nobody reads) */
+                float *slot = &ring[(step & 1U) * P + producer][0][0];
+                const uint32_t ahead = (step + 2U) * P + producer;
 
-                if (base >= wave_length) {
-                    break;
+#pragma unroll
+                for (int k = 0; k < R; ++k) {
+                    const float4 v = (step & 1U) != 0U ? x[1][k] : x[0][k];
+
+                    *(float4 *)(slot + k * kLine + lane * 4U) = m3_keep4(
+                        m3_exp4(v, maximum[k], exp_table), finite[k]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int k = 0; k < R; ++k) {
-                    float4 e = ahead[b][k];
+                    const float4 v = m3_softmax_get4<F32IO, VEC>(
+                        rows[k], ahead * kChunk + lane * 4U, seen, in_dtype);
 
-                    if (finite[k]) {
-                        e.x = m3_expf_with_table(e.x - maximum[k], exp_table);
-                        e.y = m3_expf_with_table(e.y - maximum[k], exp_table);
-                        e.z = m3_expf_with_table(e.z - maximum[k], exp_table);
-                        e.w = m3_expf_with_table(e.w - maximum[k], exp_table);
+                    if ((step & 1U) != 0U) {
+                        x[1][k] = v;
                     } else {
-                        e = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+                        x[0][k] = v;
                     }
-                    *(float4 *)(tile + k * kLine + lane * 4U) = e;
-                    ahead[b][k] = m3_softmax_get4<F32IO, VEC>(
-                        rows[k], base + kChunk * B + lane * 4U,
-                        min(width, wave_length), in_dtype);
                 }
-                m3_wave_sync();
-                sum = m3_chunk_sum<4>(
-                    sum, line, (min(wave_length - base, kChunk) + 3U) & ~3U);
-                m3_wave_sync();
+            } else if (step > 0U && lane < kChainLanes) {
+                /* consumer: the chunks of the previous step, in order, on
+                 * 16 lanes (R rows, each summed by 16 / R lanes): the LDS
+                 * reads of a full wave would take four times the LDS
+                 * bandwidth that the chains of a CU can use */
+                const uint32_t first = (step - 1U) * P;
+
+#pragma unroll 1
+                for (uint32_t i = 0U; i < P && first + i < sum_chunks; ++i) {
+                    sum = m3_chunk_sum_full(
+                        sum, &ring[((step - 1U) & 1U) * P + i][0][0] +
+                                 (lane % (uint32_t)R) * kLine);
+                }
             }
+            __syncthreads();
         }
-        const double inverse_of_lane = 1.0 / (double)sum;
+        /* the sums reach the other waves through LDS */
+        if (wave == consumer && lane < (uint32_t)R) {
+            part_max[0][lane] = sum;
+        }
+        __syncthreads();
         double inverse[R];
         float one_over_count[R];
 
 #pragma unroll
         for (int k = 0; k < R; ++k) {
-            inverse[k] = m3_lane_f64(inverse_of_lane, k);
-            one_over_count[k] = 1.0F / (float)infinities[k];
+            inverse[k] = 1.0 / (double)part_max[0][k];
+            one_over_count[k] =
+                maximum[k] == INFINITY ? 1.0F / (float)infinities[k] : 0.0F;
         }
         /* pass 3 */
-        for (uint32_t c0 = 0U; c0 < width; c0 += kChunk * B) {
-            float4 x[R][B];
+        for (uint32_t j = wave; j < chunks; j += kWaves) {
+            float4 x[R];
 
 #pragma unroll
             for (int k = 0; k < R; ++k) {
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    x[k][b] = m3_softmax_get4<F32IO, VEC>(
-                        rows[k], c0 + kChunk * b + lane * 4U, width, in_dtype);
-                }
+                x[k] = m3_softmax_get4<F32IO, VEC>(
+                    rows[k], j * kChunk + lane * 4U, width, in_dtype);
             }
 #pragma unroll
             for (int k = 0; k < R; ++k) {
-                if ((uint32_t)k >= present) {
-                    continue;
-                }
-                uint8_t *out = a.output + (first_row + (uint32_t)k) * out_pitch;
+                const float4 v = x[k];
+                const float4 p = m3_softmax_scale4(
+                    m3_exp4(v, maximum[k], exp_table), inverse[k]);
+                float4 q;
 
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const uint32_t c = c0 + kChunk * b + lane * 4U;
-                    const float4 v = x[k][b];
-                    float4 p;
-
-                    if (finite[k]) {
-                        p.x = m3_expf_with_table(v.x - maximum[k], exp_table);
-                        p.y = m3_expf_with_table(v.y - maximum[k], exp_table);
-                        p.z = m3_expf_with_table(v.z - maximum[k], exp_table);
-                        p.w = m3_expf_with_table(v.w - maximum[k], exp_table);
-                        p = m3_softmax_scale4(p, inverse[k]);
-                    } else {
-                        const float q = maximum[k] == INFINITY
-                                            ? one_over_count[k]
-                                            : 0.0F;
-
-                        p.x = v.x == INFINITY ? q : 0.0F;
-                        p.y = v.y == INFINITY ? q : 0.0F;
-                        p.z = v.z == INFINITY ? q : 0.0F;
-                        p.w = v.w == INFINITY ? q : 0.0F;
-                    }
-                    if (c0 + kChunk * b < width) {
-                        m3_softmax_put4<F32IO, VEC>(out, c, width, out_dtype,
-                                                    p);
-                    }
-                }
+                /* rows without a finite maximum: 1/k on +inf, else 0 */
+                q.x = v.x == INFINITY ? one_over_count[k] : 0.0F;
+                q.y = v.y == INFINITY ? one_over_count[k] : 0.0F;
+                q.z = v.z == INFINITY ? one_over_count[k] : 0.0F;
+                q.w = v.w == INFINITY ? one_over_count[k] : 0.0F;
+                q = make_float4(
+                    m3_bits_f32((m3_f32_bits(p.x) & finite[k]) |
+                                (m3_f32_bits(q.x) & ~finite[k])),
+                    m3_bits_f32((m3_f32_bits(p.y) & finite[k]) |
+                                (m3_f32_bits(q.y) & ~finite[k])),
+                    m3_bits_f32((m3_f32_bits(p.z) & finite[k]) |
+                                (m3_f32_bits(q.z) & ~finite[k])),
+                    m3_bits_f32((m3_f32_bits(p.w) & finite[k]) |
+                                (m3_f32_bits(q.w) & ~finite[k])));
+                m3_softmax_put4<F32IO, VEC>(outs[k], j * kChunk + lane * 4U,
+                                            width, out_dtype, q);
             }
         }
+        /* the LDS of this task is reused by the next */
+        __syncthreads();
     }
 }
 
@@ -1254,10 +1368,10 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
                 },
                 message, capacity);
         }
-        /* Any other row: streamed through three passes. */
+        /* Any other row: streamed through three passes, a workgroup per
+         * kStreamRows rows. */
         uint64_t tasks = (rows + kStreamRows - 1U) / kStreamRows;
-        uint64_t blocks = (tasks + kWaves - 1U) / kWaves;
-        dim3 grid((uint32_t)(blocks < kMaxGrid ? blocks : kMaxGrid));
+        dim3 grid((uint32_t)(tasks < kMaxGrid ? tasks : kMaxGrid));
         m3_softmax_launcher launcher = !vec ? &m3_launch_stream<false, false>
                                        : f32 ? &m3_launch_stream<true, true>
                                              : &m3_launch_stream<false, true>;
