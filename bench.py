@@ -101,6 +101,18 @@ class CpuBaseline:
         return status, out, time.perf_counter() - start
 
 
+def cpu_model():
+    """The host CPU's model name, as /proc/cpuinfo gives it."""
+    try:
+        with open("/proc/cpuinfo") as handle:
+            for line in handle:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 # ---- workloads -------------------------------------------------------------
 
 def softmax_input(rows_per_matrix=1024, matrices=16, seed=0):
@@ -553,6 +565,7 @@ def main():
                 "%d of %d elements differ" % (mismatches, s.size)
             cpu_line = {"value": round(nbytes / cpu_seconds / 1e9, 4),
                         "unit": "GB/s", "cores": 1, "kind": cpu.kind,
+                        "model": cpu_model(),
                         "sample": "the full [16,1024,1024] softmax, one "
                                   "run of the single-threaded CPU provider"}
         results["softmax"] = result_entry("softmax", w, wall, kus, launches,
@@ -823,10 +836,14 @@ def main():
             out = w.read_output()
             parity = euler_parity(cpu, x, vus, vcs, out)
         fused = launches == 1
-        entry = result_entry("euler", w, wall, kus, launches, nbytes,
+        # the rates use the unique tensor bytes the graph reads and writes
+        # (what one fused program moves); the sum over the 180 nodes of
+        # their own operand bytes is reported beside them, not as a rate
+        entry = result_entry("euler", w, wall, kus, launches, fused_bytes,
                              fused_bytes if fused else nbytes / 180.0,
                              parity)
         entry["kernel_time_per_run_ms"] = round(run_kernel_ms, 4)
+        entry["node_sum_bytes_per_run"] = nbytes
         entry["fused_lower_bound_bytes"] = 4 * tensor * 30
         entry["hbm_bytes_per_run"] = fused_bytes if fused else nbytes
         entry["slots"] = None

@@ -16,7 +16,10 @@ import os
 
 PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_ROOT = os.path.dirname(PACKAGE_DIR)
-LIBRARY_PATH = os.path.join(PACKAGE_DIR, "libm3.so")
+# M3_LIBRARY_DIR selects another build of the host layer (the sanitizer
+# build of the CPU suite); the kernels always come from this package.
+LIBRARY_PATH = os.path.join(os.environ.get("M3_LIBRARY_DIR", PACKAGE_DIR),
+                            "libm3.so")
 HIP_LIBRARY_PATH = os.path.join(PACKAGE_DIR, "libm3_hip.so")
 
 MAX_RANK = 8

@@ -17,19 +17,25 @@ import pytest
 from conftest import ROOT, m3
 
 BUILD = os.path.join(ROOT, "tests", "_build")
-LIB = os.path.join(BUILD, "liboracle_backend.so")
+# The sanitizer run (tests/test_sanitize_cpu.py) links the test backend
+# with the same sanitizers against the sanitized host layer.
+SANITIZE = os.environ.get("M3_SANITIZE") == "1"
+LIB_DIR = os.environ.get("M3_LIBRARY_DIR", os.path.join(ROOT, "m3.c_amd"))
+LIB = os.path.join(BUILD, "liboracle_backend%s.so" %
+                   ("_sanitize" if SANITIZE else ""))
 
 
 def _build_backend():
     os.makedirs(BUILD, exist_ok=True)
     sources = [os.path.join(ROOT, "tests", "csrc", "oracle_backend.c"),
                os.path.join(ROOT, "oracle", "m3_oracle.c")]
+    flags = (["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
+              "-fno-omit-frame-pointer", "-g"] if SANITIZE else [])
     subprocess.run(["gcc", "-std=c11", "-O2", "-fPIC", "-shared",
                     "-ffp-contract=off", "-mfma", "-D_POSIX_C_SOURCE=200809L",
                     "-I", os.path.join(ROOT, "include"),
-                    "-I", os.path.join(ROOT, "oracle")] + sources +
-                   ["-L", os.path.join(ROOT, "m3.c_amd"), "-lm3",
-                    "-Wl,-rpath," + os.path.join(ROOT, "m3.c_amd"), "-lm",
+                    "-I", os.path.join(ROOT, "oracle")] + flags + sources +
+                   ["-L", LIB_DIR, "-lm3", "-Wl,-rpath," + LIB_DIR, "-lm",
                     "-o", LIB], check=True)
 
 
