@@ -22,7 +22,13 @@
 namespace {
 
 constexpr uint32_t kThreads = 256U;
-constexpr uint32_t kUnroll = 2U; /* groups in flight per lane (measured best) */
+constexpr uint32_t kUnroll = 2U; /* groups in flight per lane, copies */
+/* groups in flight per lane of a conversion */
+constexpr uint32_t kCastUnroll = 2U;
+/* workgroups per CU of a conversion: up to 32, so that a 16M-element
+ * cast runs each lane's groups in one pass instead of a grid-stride loop
+ * (measured 2% faster for F16 -> F32 than 16 per CU) */
+constexpr uint32_t kCastBlocksPerCu = 32U;
 
 template <uint32_t DT>
 struct m3_vec_io;
@@ -74,15 +80,15 @@ __global__ __launch_bounds__(256) void m3_cast_vec_kernel(
     using out_io = m3_vec_io<m3_size_of(OUT)>;
     const typename in_io::type *in = (const typename in_io::type *)input;
     typename out_io::type *out = (typename out_io::type *)output;
-    const uint64_t step = (uint64_t)gridDim.x * kThreads * kUnroll;
+    const uint64_t step = (uint64_t)gridDim.x * kThreads * kCastUnroll;
 
-    for (uint64_t first = (uint64_t)blockIdx.x * kThreads * kUnroll +
+    for (uint64_t first = (uint64_t)blockIdx.x * kThreads * kCastUnroll +
                           threadIdx.x;
          first < groups; first += step) {
-        uint4 v[kUnroll];
+        uint4 v[kCastUnroll];
 
 #pragma unroll
-        for (uint32_t u = 0U; u < kUnroll; ++u) {
+        for (uint32_t u = 0U; u < kCastUnroll; ++u) {
             uint64_t g = first + u * kThreads;
 
             if (g < groups) {
@@ -90,7 +96,7 @@ __global__ __launch_bounds__(256) void m3_cast_vec_kernel(
             }
         }
 #pragma unroll
-        for (uint32_t u = 0U; u < kUnroll; ++u) {
+        for (uint32_t u = 0U; u < kCastUnroll; ++u) {
             uint64_t g = first + u * kThreads;
 
             if (g < groups) {
@@ -294,7 +300,8 @@ int m3_launch_unary(m3_hip_device *device, const m3_hip_view *input,
             uint64_t groups = count / 4U;
             uint32_t blocks = m3_grid_blocks(device,
                                              groups == 0U ? 1U : groups,
-                                             kThreads * kUnroll, 16U);
+                                             kThreads * kCastUnroll,
+                                             kCastBlocksPerCu);
 
             return m3_hip_launch(
                 device, name,
