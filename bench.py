@@ -197,30 +197,45 @@ class Workload:
         for i in range(steps):
             self.sessions[i % len(self.sessions)].run()
         wall = (time.perf_counter() - start) / steps
-        # the timed pass reads the events run by run, so that the median of
-        # the dominant kernel's per-run average can be reported beside the
-        # mean (VALU-bound kernels vary with the clock from run to run)
-        launches = 0
-        total_ms = 0.0
-        per_kernel = {}
-        self.run_kernel_us = []
-        for i in range(steps):
-            session = self.sessions[i % len(self.sessions)]
+        # the same steps again, back to back, with the library's timing
+        # events on every dispatch; the durations are read once at the end,
+        # so the runs follow each other as in the wall-clock pass (a host
+        # pause of tens of microseconds between runs slows the VALU-heavy
+        # kernels that follow it). Each run's dominant-kernel average is
+        # kept, for the median beside the mean (VALU-bound kernels vary
+        # with the clock from run to run).
+        for session in self.sessions:
             session.timing_reset()
             session.timing_enable(True)
-            session.run()
-            times = session.timing_read()
-            session.timing_enable(False)
-            run_count, run_ms = 0, 0.0
-            for name, (count, ms) in times.items():
+        for i in range(steps):
+            self.sessions[i % len(self.sessions)].run()
+        per_kernel = {}
+        per_session = []
+        for session in self.sessions:
+            for name, (count, ms) in session.timing_read().items():
                 previous = per_kernel.get(name, (0, 0.0))
                 per_kernel[name] = (previous[0] + count, previous[1] + ms)
-                if name in self.kernel:
-                    run_count += count
-                    run_ms += ms
-            launches += run_count
-            total_ms += run_ms
-            self.run_kernel_us.append(1000.0 * run_ms / max(run_count, 1))
+            samples = []
+            for name in self.kernel:
+                samples = session.timing_samples(name)
+                if samples:
+                    break
+            per_session.append(samples)
+            session.timing_enable(False)
+        launches = sum(per_kernel.get(name, (0, 0.0))[0]
+                       for name in self.kernel)
+        total_ms = sum(per_kernel.get(name, (0, 0.0))[1]
+                       for name in self.kernel)
+        # session j ran steps j, j + n, ...: its k-th group of launches is
+        # step j + k n
+        self.run_kernel_us = []
+        per_run = max(launches // steps, 1)
+        for i in range(steps):
+            n = len(self.sessions)
+            samples = per_session[i % n]
+            chunk = samples[(i // n) * per_run:(i // n + 1) * per_run]
+            if chunk:
+                self.run_kernel_us.append(1000.0 * sum(chunk) / len(chunk))
         kernel_us = 1000.0 * total_ms / max(launches, 1)
         runs_kernel_ms = sum(ms for _, ms in per_kernel.values()) / steps
         return wall * 1000.0, kernel_us, launches // steps, per_kernel, \

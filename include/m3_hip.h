@@ -293,6 +293,14 @@ int m3_hip_timing_reset(m3_hip_device *device);
 int m3_hip_timing_read(m3_hip_device *device, m3_hip_kernel_time *entries,
                        size_t capacity, size_t *count, char *message,
                        size_t message_capacity);
+/* The durations (ms) of the completed launches of kernel `name` since the
+ * last reset, in launch order (the first 4,096 are kept): *count receives
+ * how many there are, and up to `capacity` are copied. Synchronizes like
+ * m3_hip_timing_read. */
+int m3_hip_timing_samples(m3_hip_device *device, const char *name,
+                          float *durations_ms, size_t capacity,
+                          size_t *count, char *message,
+                          size_t message_capacity);
 /* The device's hipStream_t, for callers that order their own work with it. */
 void *m3_hip_stream(m3_hip_device *device);
 

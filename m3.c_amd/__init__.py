@@ -196,7 +196,8 @@ EXPORTS_HIP = [
     "m3_hip_fill_zero", "m3_hip_launch_binary", "m3_hip_launch_cast",
     "m3_hip_launch_copy", "m3_hip_launch_softmax", "m3_hip_launch_snake1d",
     "m3_hip_scan_views", "m3_hip_synchronize", "m3_hip_timing_enable",
-    "m3_hip_timing_reset", "m3_hip_timing_read", "m3_hip_stream",
+    "m3_hip_timing_reset", "m3_hip_timing_read", "m3_hip_timing_samples",
+    "m3_hip_stream",
     "m3_hip_launch_program", "m3_hip_launch_tanh", "m3_hip_launch_gated_silu",
     "m3_hip_prepare_program", "m3_hip_scan_views_static",
 ]
@@ -298,6 +299,8 @@ def load():
     _declare(hip, "m3_hip_timing_reset", st, vp)
     _declare(hip, "m3_hip_timing_read", st, vp, P(HipKernelTime), sz, P(sz),
              ctypes.c_char_p, sz)
+    _declare(hip, "m3_hip_timing_samples", st, vp, ctypes.c_char_p,
+             P(ctypes.c_float), sz, P(sz), ctypes.c_char_p, sz)
     _declare(hip, "m3_hip_stream", vp, vp)
     _declare(hip, "m3_hip_synchronize", st, vp, ctypes.c_char_p, sz)
     _declare(hip, "m3_hip_launch_program", st, vp, P(ctypes.c_uint32), vp,
@@ -477,6 +480,20 @@ class Session:
         return {entries[i].name.decode(): (entries[i].launches,
                                            entries[i].total_ms)
                 for i in range(min(count.value, 64))}
+
+    def timing_samples(self, name, capacity=4096):
+        """Durations (ms) of the launches of kernel `name` since the last
+        timing reset, in launch order."""
+        durations = (ctypes.c_float * capacity)()
+        count = ctypes.c_size_t()
+        message = ctypes.create_string_buffer(256)
+        status = self.hip.m3_hip_timing_samples(
+            self.hip_device(), name.encode(), durations, capacity,
+            ctypes.byref(count), message, 256)
+        if status != 0:
+            raise M3Error(INTERNAL, message.value.decode())
+        return [float(durations[i]) for i in range(min(count.value,
+                                                       capacity))]
 
     def free(self):
         if self.handle:

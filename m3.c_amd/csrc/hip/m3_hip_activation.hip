@@ -23,6 +23,12 @@
  * GATED_SILU's NaN rule costs a recomputation only in a wave where some
  * product is NaN: the plain arithmetic gives the host's bits for every
  * non-NaN result, and m3_gated_silu_bits gives them for all.
+ *
+ * All-BF16 GATED_SILU looks its activation up in a 16 KB table that each
+ * device builds once (m3_gated_silu_bf16_kernel): a BF16 gate has only
+ * 65,536 values, and the rounded activation depends on the gate alone.
+ * That takes the kernel from ~52 VALU instructions per element, clock-bound,
+ * to about a dozen, bound by HBM.
  */
 #include "m3_activation.h"
 #include "m3_hip_internal.h"
@@ -241,6 +247,149 @@ __device__ __forceinline__ void m3_silu4(const float g[4], const float u[4],
     }
 }
 
+/* GATED_SILU BF16 through a table of activations. A BF16 gate has 65,536
+ * bit patterns, and the activation, rounded through BF16, depends on the
+ * gate alone; the table holds it for every gate of magnitude in
+ * [2^-25, 2^7) (exponent fields 102-133, 32 binades of 128 values, both
+ * signs: 8,192 entries, 16 KB), which covers every gate that is not tiny,
+ * huge, infinite or NaN. The entries are the bits m3_gated_silu_bits gives
+ * with up = 1 (exact: the product of a finite BF16 activation and 1), built
+ * on the device when it is opened. Each workgroup copies the table into
+ * LDS; an element then costs one LDS read instead of the ~35 instructions
+ * of expf and the division. Gates outside the table take the arithmetic
+ * of m3_silu4 in the waves where a lane has one, and NaN products the
+ * exact recomputation, as in m3_gated_silu_vec_kernel. */
+constexpr uint32_t kSiluTableFirstField = 102U; /* exponent field of 2^-25 */
+constexpr uint32_t kSiluTableSpan = 32U << 7U;  /* entries per sign */
+constexpr uint32_t kSiluTableEntries = 2U * kSiluTableSpan;
+
+/* The BF16 bits of table entry i: bit 12 is the sign, the rest counts up
+ * from the first exponent field. */
+__host__ __device__ inline uint32_t m3_silu_table_gate(uint32_t i)
+{
+    return ((i & kSiluTableSpan) << 3U) |
+           ((kSiluTableFirstField << 7U) + (i & (kSiluTableSpan - 1U)));
+}
+
+__global__ __launch_bounds__(256) void m3_silu_table_build_kernel(
+    uint16_t *table)
+{
+    const uint32_t i = blockIdx.x * 256U + threadIdx.x;
+
+    if (i < kSiluTableEntries) {
+        const float gate = m3_bits_f32(m3_silu_table_gate(i) << 16U);
+
+        table[i] = (uint16_t)(m3_gated_silu_bits(gate, 1.0F, M3N_BF16) >>
+                              16U);
+    }
+}
+
+/* The activation of BF16 gate bits `raw` as F32 bits from the LDS table;
+ * *miss is set (and 0 returned) for a gate outside it. */
+__device__ __forceinline__ uint32_t m3_silu_table_lookup(
+    uint32_t raw, const uint16_t *table, bool *miss)
+{
+    const uint32_t index = (raw & 0x7fffU) - (kSiluTableFirstField << 7U);
+    const bool inside = index < kSiluTableSpan;
+
+    *miss = !inside;
+    return inside ? (uint32_t)table[index | ((raw >> 3U) & kSiluTableSpan)]
+                        << 16U
+                  : 0U;
+}
+
+__global__ __launch_bounds__(256) void m3_gated_silu_bf16_kernel(
+    m3_silu_vec_args a, const uint4 *source)
+{
+    const uint32_t step = gridDim.x * kThreads * kUnroll;
+    __shared__ uint16_t table[kSiluTableEntries];
+    __shared__ uint64_t exp_table[32];
+
+    for (uint32_t i = threadIdx.x; i < kSiluTableEntries / 8U; i += kThreads) {
+        ((uint4 *)table)[i] = source[i];
+    }
+    if (threadIdx.x < 32U) {
+        exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
+    }
+    __syncthreads();
+    for (uint32_t first = blockIdx.x * kThreads * kUnroll + threadIdx.x;
+         first < a.groups; first += step) {
+        uint2 gate[kUnroll];
+        uint2 up[kUnroll];
+
+        /* unconditional loads (groups past the end re-read the last one)
+         * so that all of them are in flight before the first use */
+#pragma unroll
+        for (uint32_t k = 0U; k < kUnroll; ++k) {
+            const uint32_t index = min(first + k * kThreads, a.groups - 1U);
+
+            gate[k] = m3_stream_load((const uint2 *)a.gate + index);
+            up[k] = m3_stream_load((const uint2 *)a.up + index);
+        }
+#pragma unroll
+        for (uint32_t k = 0U; k < kUnroll; ++k) {
+            const uint32_t index = first + k * kThreads;
+
+            if (index < a.groups) {
+                const uint32_t raw[4] = {gate[k].x & 0xffffU, gate[k].x >> 16U,
+                                         gate[k].y & 0xffffU, gate[k].y >> 16U};
+                const float u[4] = {m3_bits_f32(up[k].x << 16U),
+                                    m3_bits_f32(up[k].x & 0xffff0000U),
+                                    m3_bits_f32(up[k].y << 16U),
+                                    m3_bits_f32(up[k].y & 0xffff0000U)};
+                uint32_t activation[4];
+                bool miss[4];
+                float p[4];
+                uint32_t r[4];
+
+#pragma unroll
+                for (uint32_t e = 0U; e < 4U; ++e) {
+                    activation[e] = m3_silu_table_lookup(raw[e], table,
+                                                         &miss[e]);
+                }
+                if ((__ballot(miss[0]) | __ballot(miss[1]) |
+                     __ballot(miss[2]) | __ballot(miss[3])) != 0U) {
+#pragma unroll
+                    for (uint32_t e = 0U; e < 4U; ++e) {
+                        if (miss[e]) {
+                            activation[e] = m3_round_through_bf16_finite(
+                                m3_f32_bits(m3_silu_quotient_fast(
+                                    m3_bits_f32(raw[e] << 16U), exp_table)));
+                        }
+                    }
+                }
+#pragma unroll
+                for (uint32_t e = 0U; e < 4U; ++e) {
+                    p[e] = m3_bits_f32(activation[e]) * u[e];
+                }
+                /* a NaN activation makes its product NaN, so one test
+                 * covers both */
+                if ((__ballot(p[0] != p[0]) | __ballot(p[1] != p[1]) |
+                     __ballot(p[2] != p[2]) | __ballot(p[3] != p[3])) != 0U) {
+#pragma unroll
+                    for (uint32_t e = 0U; e < 4U; ++e) {
+                        p[e] = m3_bits_f32(m3_gated_silu_bits(
+                            m3_bits_f32(raw[e] << 16U), u[e], M3N_BF16));
+                    }
+                }
+#pragma unroll
+                for (uint32_t e = 0U; e < 4U; ++e) {
+                    r[e] = m3_f32_bits(p[e]);
+                }
+                m3_store4<M3N_BF16>(a.output, index, r);
+            }
+        }
+    }
+    if (blockIdx.x == 0U && threadIdx.x < a.tail) {
+        const uint64_t e = 4ULL * a.groups + threadIdx.x;
+        float g = m3_bits_f32(m3_load_element(a.gate + 2U * e, M3N_BF16));
+        float u = m3_bits_f32(m3_load_element(a.up + 2U * e, M3N_BF16));
+
+        m3_store_element(a.output + 2U * e, M3N_BF16,
+                         m3_gated_silu_bits(g, u, M3N_BF16));
+    }
+}
+
 /* Gate, up and output all of dtype D, contiguous and aligned. */
 template <uint32_t D>
 __global__ __launch_bounds__(256) void m3_gated_silu_vec_kernel(
@@ -374,12 +523,45 @@ template <uint32_t D>
 void m3_launch_silu_vec(m3_hip_device *device, const m3_silu_vec_args &args,
                         uint32_t blocks, hipEvent_t start, hipEvent_t stop)
 {
+    if (D == M3N_BF16) {
+        hipExtLaunchKernelGGL(m3_gated_silu_bf16_kernel, dim3(blocks),
+                              dim3(kThreads), 0, device->stream, start, stop,
+                              0U, args,
+                              (const uint4 *)device->silu_bf16_table);
+        return;
+    }
     hipExtLaunchKernelGGL((m3_gated_silu_vec_kernel<D>), dim3(blocks),
                           dim3(kThreads), 0, device->stream, start, stop, 0U,
                           args);
 }
 
 } // namespace
+
+int m3_silu_table_build(m3_hip_device *device, char *message,
+                        size_t capacity)
+{
+    int code = m3_hip_check(hipMalloc((void **)&device->silu_bf16_table,
+                                      kSiluTableEntries * sizeof(uint16_t)),
+                            "hipMalloc(GATED_SILU table)", message, capacity);
+
+    if (code != M3_HIP_OK) {
+        device->silu_bf16_table = nullptr;
+        return code;
+    }
+    hipLaunchKernelGGL(m3_silu_table_build_kernel,
+                       dim3(kSiluTableEntries / 256U), dim3(256), 0,
+                       device->stream, device->silu_bf16_table);
+    return m3_hip_check(hipGetLastError(), "m3_silu_table_build", message,
+                        capacity);
+}
+
+void m3_silu_table_release(m3_hip_device *device)
+{
+    if (device->silu_bf16_table != nullptr) {
+        (void)hipFree(device->silu_bf16_table);
+        device->silu_bf16_table = nullptr;
+    }
+}
 
 extern "C" int m3_hip_launch_tanh(m3_hip_device *device,
                                   const m3_hip_view *input,

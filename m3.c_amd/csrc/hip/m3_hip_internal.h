@@ -28,7 +28,12 @@ struct m3_hip_time_total {
     std::string name;
     uint64_t launches;
     double total_ms;
+    std::vector<float> samples; /* each launch's duration, in launch order,
+                                 * up to kTimingSamples of them */
 };
+
+/* Launch durations kept per kernel name between two timing resets. */
+constexpr size_t kTimingSamples = 4096U;
 
 struct m3_hip_device {
     int ordinal;
@@ -58,10 +63,19 @@ struct m3_hip_device {
     char arch[64]; /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
     /* kernels generated for elementwise programs (m3_hip_program.hip) */
     struct m3_program_cache *programs;
+    /* GATED_SILU's BF16 activation of every gate in the table's range
+     * (m3_hip_activation.hip) */
+    uint16_t *silu_bf16_table;
 };
 
 /* Unloads the generated kernels of a device (m3_hip_program.hip). */
 void m3_program_cache_release(m3_hip_device *device);
+
+/* Builds and frees the device's GATED_SILU BF16 activation table
+ * (m3_hip_activation.hip); the build is queued on the device stream. */
+int m3_silu_table_build(m3_hip_device *device, char *message,
+                        size_t capacity);
+void m3_silu_table_release(m3_hip_device *device);
 
 /* Writes a formatted message into a caller buffer (which may be NULL). */
 int m3_hip_fail(char *message, size_t capacity, int code, const char *format,

@@ -271,6 +271,9 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
                                           hipHostMallocCoherent),
                             "hipHostMalloc", message, capacity);
     }
+    if (code == M3_HIP_OK) {
+        code = m3_silu_table_build(device, message, capacity);
+    }
     if (code != M3_HIP_OK) {
         m3_hip_device_close(device);
         return code;
@@ -304,6 +307,7 @@ extern "C" void m3_hip_device_close(m3_hip_device *device)
         (void)hipEventDestroy(event);
     }
     m3_program_cache_release(device);
+    m3_silu_table_release(device);
     if (device->scan_flags != nullptr) {
         (void)hipFree(device->scan_flags);
     }
@@ -1043,12 +1047,15 @@ static void m3_hip_fold_pending(m3_hip_device *device)
             if (total.name == slot.name) {
                 total.launches += 1U;
                 total.total_ms += ms;
+                if (total.samples.size() < kTimingSamples) {
+                    total.samples.push_back(ms);
+                }
                 found = true;
                 break;
             }
         }
         if (!found) {
-            device->totals.push_back({slot.name, 1U, (double)ms});
+            device->totals.push_back({slot.name, 1U, (double)ms, {ms}});
         }
     }
     device->pending.clear();
@@ -1089,6 +1096,38 @@ extern "C" int m3_hip_timing_read(m3_hip_device *device,
                       device->totals[i].name.c_str());
         entries[i].launches = device->totals[i].launches;
         entries[i].total_ms = device->totals[i].total_ms;
+    }
+    return M3_HIP_OK;
+}
+
+extern "C" int m3_hip_timing_samples(m3_hip_device *device, const char *name,
+                                     float *durations_ms, size_t capacity,
+                                     size_t *count, char *message,
+                                     size_t message_capacity)
+{
+    int code;
+
+    if (device == nullptr || name == nullptr || count == nullptr ||
+        (capacity != 0U && durations_ms == nullptr)) {
+        return m3_hip_fail(message, message_capacity, M3_HIP_INVALID,
+                           "timing sample arguments are incomplete");
+    }
+    code = m3_hip_check(hipStreamSynchronize(device->stream),
+                        "hipStreamSynchronize", message, message_capacity);
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    m3_hip_fold_pending(device);
+    *count = 0U;
+    for (const m3_hip_time_total &total : device->totals) {
+        if (total.name == name) {
+            *count = total.samples.size();
+            for (size_t i = 0U; i < total.samples.size() && i < capacity;
+                 ++i) {
+                durations_ms[i] = total.samples[i];
+            }
+            break;
+        }
     }
     return M3_HIP_OK;
 }

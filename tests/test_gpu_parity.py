@@ -593,6 +593,45 @@ def test_gated_silu_dense_gate_sweep(hip):
     compare(hip, m3.OP_GATED_SILU, storages, views, "gated silu sweep")
 
 
+@pytest.mark.parametrize("count", [16 << 16, (1 << 16) + 3])
+def test_gated_silu_bf16_every_gate(hip, count):
+    """Every BF16 gate bit pattern, so every entry of the BF16 kernel's
+    activation table and every gate outside it (tiny, huge, subnormal,
+    infinite, NaN), times random BF16 up bits (NaN, infinities and zeros
+    included) and 1.0, through the vector path (with a 3-element tail for
+    the odd count)."""
+    rng = np.random.default_rng(35 + count)
+    gate = (np.arange(count, dtype=np.uint32) & 0xffff).astype(np.uint16)
+    up = random_bits16(rng, count)
+    up[::7] = 0x3f80
+    views = [ViewSpec(i, m3.BF16, (count,)) for i in range(3)]
+    storages = [as_bytes(gate), as_bytes(up), np.zeros(2 * count, np.uint8)]
+    compare(hip, m3.OP_GATED_SILU, storages, views,
+            "gated silu BF16 every gate, count %d" % count)
+
+
+def test_gated_silu_bf16_layouts_and_aliases(hip):
+    """The BF16 kernel's neighbours: a 2-byte offset (the general kernel),
+    the output over the gate and over up (the vector kernel in place)."""
+    rng = np.random.default_rng(36)
+    count = 4096
+    gate = np.frombuffer(storage_for(rng, m3.BF16, count + 1, specials=0.1),
+                         np.uint16).copy()
+    up = np.frombuffer(storage_for(rng, m3.BF16, count + 1, specials=0.1),
+                       np.uint16).copy()
+    shifted = [ViewSpec(0, m3.BF16, (count,), None, 2),
+               ViewSpec(1, m3.BF16, (count,)),
+               ViewSpec(2, m3.BF16, (count,))]
+    compare(hip, m3.OP_GATED_SILU,
+            [as_bytes(gate), as_bytes(up), np.zeros(2 * count, np.uint8)],
+            shifted, "gated silu BF16 offset gate")
+    exact = [ViewSpec(0, m3.BF16, (count,)), ViewSpec(1, m3.BF16, (count,))]
+    compare(hip, m3.OP_GATED_SILU, [as_bytes(gate), as_bytes(up)],
+            exact + [exact[0]], "gated silu BF16 gate alias")
+    compare(hip, m3.OP_GATED_SILU, [as_bytes(gate), as_bytes(up)],
+            exact + [exact[1]], "gated silu BF16 up alias")
+
+
 def test_gated_silu_strided_and_aliases(hip):
     rng = np.random.default_rng(34)
     gate = random_f32(rng, 2000, scale=6.0)
