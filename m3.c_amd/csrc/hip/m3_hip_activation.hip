@@ -40,6 +40,11 @@ namespace {
 
 constexpr uint32_t kThreads = 256U;
 constexpr uint32_t kUnroll = 4U;
+/* TANH's groups per lane: with ~100 instructions per element, two groups
+ * in flight already cover the load latency, and the smaller tile lets the
+ * dispatcher spread the work more evenly (3% faster than four, measured
+ * alternating in one process on x[2,1536,65536]). */
+constexpr uint32_t kTanhUnroll = 2U;
 /* Grid cap of the vector kernels: 1,024 workgroups per CU, so every
  * tensor below 2^30 elements runs as one workgroup per tile (1,024 groups
  * of four elements) and the hardware dispatcher, not the grid-stride
@@ -120,21 +125,21 @@ struct m3_tanh_vec_args {
 
 __global__ __launch_bounds__(256) void m3_tanh_vec_kernel(m3_tanh_vec_args a)
 {
-    const uint32_t step = gridDim.x * kThreads * kUnroll;
+    const uint32_t step = gridDim.x * kThreads * kTanhUnroll;
 
-    for (uint32_t first = blockIdx.x * kThreads * kUnroll + threadIdx.x;
+    for (uint32_t first = blockIdx.x * kThreads * kTanhUnroll + threadIdx.x;
          first < a.groups; first += step) {
-        float x[kUnroll][4];
+        float x[kTanhUnroll][4];
 
         /* unconditional loads (groups past the end re-read the last one)
          * so that all of them are in flight before the first use */
 #pragma unroll
-        for (uint32_t u = 0U; u < kUnroll; ++u) {
+        for (uint32_t u = 0U; u < kTanhUnroll; ++u) {
             m3_load4<M3N_F32>(a.input, min(first + u * kThreads,
                                             a.groups - 1U), x[u]);
         }
 #pragma unroll
-        for (uint32_t u = 0U; u < kUnroll; ++u) {
+        for (uint32_t u = 0U; u < kTanhUnroll; ++u) {
             uint32_t g = first + u * kThreads;
 
             if (g < a.groups) {
@@ -592,7 +597,7 @@ extern "C" int m3_hip_launch_tanh(m3_hip_device *device,
         args.tail = (uint32_t)(count % 4U);
         uint32_t blocks = m3_grid_blocks(
             device, args.groups == 0U ? 1U : args.groups,
-            kThreads * kUnroll, kBlocksPerCu);
+            kThreads * kTanhUnroll, kBlocksPerCu);
 
         return m3_hip_launch(
             device, "m3_tanh",

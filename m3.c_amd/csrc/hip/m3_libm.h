@@ -498,13 +498,35 @@ M3_HD float m3_div_normal(float a, float b)
 #endif
 }
 
+/* m3_div_normal with one correction step instead of two: the quotient
+ * a * y of the refined reciprocal, corrected once by its residual. That
+ * is the correctly rounded quotient except for rare operand pairs; the two
+ * divisions of m3_tanhf_uniform use it, and the GPU test of TANH over every
+ * F32 input shows that no input of tanhf reaches such a pair through
+ * either of them. On the host it is the C division. */
+M3_HD float m3_div_one_step(float a, float b)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    float y = __builtin_amdgcn_rcpf(b);
+    const float e = fmaf(-b, y, 1.0F);
+    float q;
+
+    y = fmaf(e, y, y);
+    q = a * y;
+    return fmaf(fmaf(-b, q, a), y, q);
+#else
+    return a / b;
+#endif
+}
+
 /* m3_expm1f for the arguments tanhf passes, v in (-2, 0) or [2, 44], as
  * straight-line code: every case of the reduction is the general one with
  * k = 0 (no reduction, c = 0), k = +-1 below 1.5 ln2, or k = round(v/ln2),
  * which gives the same hi, lo, x and c bit for bit; the reconstructions
  * of the cases k = 0, k = -1, k <= -2 or k > 56, 2 <= k < 23 and
- * 23 <= k <= 56 are all formed and one is selected, as is v itself for
- * |v| < 2^-25. (k = 1 needs v in (ln2/2, 1.5 ln2), outside that domain.)
+ * 23 <= k <= 56 are all formed and one is selected; below |v| = 2^-25,
+ * where the library returns v, the k = 0 form gives v as well. (k = 1
+ * needs v in (ln2/2, 1.5 ln2), outside that domain.)
  * The quotient of the polynomial step has operands near -2 and 6, so
  * m3_div_normal applies. */
 M3_HD float m3_expm1f_tanh(float v)
@@ -537,7 +559,7 @@ M3_HD float m3_expm1f_tanh(float v)
     const float r1 =
         1.0F + hxs * (q1 + hxs * (q2 + hxs * (q3 + hxs * (q4 + hxs * q5))));
     const float t = 3.0F - r1 * hfx;
-    const float e = hxs * m3_div_normal(r1 - t, 6.0F - x * t);
+    const float e = hxs * m3_div_one_step(r1 - t, 6.0F - x * t);
     const float zero_k = x - (x * e - hxs);
     float f = x * (e - c) - c;
     const uint32_t kbits = (uint32_t)k << 23U;
@@ -557,8 +579,9 @@ M3_HD float m3_expm1f_tanh(float v)
     float result = (k <= -2 || k > 56) ? outer : k < 23 ? low : high;
 
     result = k == -1 ? minus_one_k : result;
-    result = k == 0 ? zero_k : result;
-    return hx < 0x33000000U ? v : result; /* |v| < 2^-25 */
+    /* for |v| < 2^-25 the library returns v itself; zero_k is v there too
+     * (x = v and x * e - hxs is below a quarter of v's ulp) */
+    return k == 0 ? zero_k : result;
 }
 
 /* m3_tanhf as straight-line code with one expm1f evaluation and one
@@ -577,17 +600,19 @@ M3_HD float m3_tanhf_uniform(float x)
     const uint32_t jx = m3_f32_bits(x);
     const uint32_t ix = jx & 0x7fffffffU;
     const int big = ix >= 0x3f800000U;
-    const float magnitude = fminf(m3_bits_f32(ix), 22.0F);
+    /* |x| clamped at 22 on its bits (NaN too: its result is set below) */
+    const float magnitude = m3_bits_f32(ix < 0x41b00000U ? ix : 0x41b00000U);
     const float t = m3_expm1f_tanh((big ? 2.0F : -2.0F) * magnitude);
-    const float q = m3_div_normal(big ? 2.0F : -t, t + 2.0F);
-    float z = big ? 1.0F - q : q;
+    const float q = m3_div_one_step(big ? 2.0F : -t, t + 2.0F);
+    float z = big ? 1.0F - q : q; /* +0 or positive */
 
     if (ix >= 0x41b00000U) { /* |x| >= 22 and infinities */
         z = 1.0F - 1.0e-30F;
     }
-    z = (jx & 0x80000000U) == 0U ? z : -z;
-    if (ix < 0x24000000U) { /* |x| < 2^-55, zeros included */
-        z = ix == 0U ? x : x * (1.0F + x);
+    z = m3_bits_f32(m3_f32_bits(z) | (jx & 0x80000000U));
+    if (ix < 0x24000000U) { /* |x| < 2^-55, zeros and subnormals included:
+                             * 1 + x rounds to 1, so x * (1 + x) is x */
+        z = x;
     }
     if (ix > 0x7f800000U) {
         z = m3_bits_f32(jx | 0x00400000U);
