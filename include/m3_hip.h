@@ -265,6 +265,19 @@ int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
                       const m3_hip_view *views, size_t count,
                       uint32_t *flags, char *message, size_t capacity);
 
+/* m3_hip_scan_views in two halves, so that a scan can run while the host
+ * does other work: _begin queues the same scan and returns at once with a
+ * ticket; _collect waits for the scan with that ticket and writes its
+ * flags. Only the last started scan of a device can be collected (another
+ * _begin replaces it; blocking scans in between do not). The caller keeps
+ * the views unchanged until the scan is collected or discarded. */
+int m3_hip_scan_views_begin(m3_hip_device *device, const uint32_t *kinds,
+                            const m3_hip_view *views, size_t count,
+                            uint32_t *ticket, char *message, size_t capacity);
+int m3_hip_scan_views_collect(m3_hip_device *device, uint32_t ticket,
+                              size_t count, uint32_t *flags, char *message,
+                              size_t capacity);
+
 /* No counterpart in the reference. m3_hip_scan_views for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc): the same scan and results, with the

@@ -200,6 +200,7 @@ EXPORTS_HIP = [
     "m3_hip_stream",
     "m3_hip_launch_program", "m3_hip_launch_tanh", "m3_hip_launch_gated_silu",
     "m3_hip_prepare_program", "m3_hip_scan_views_static",
+    "m3_hip_scan_views_begin", "m3_hip_scan_views_collect",
 ]
 
 _LIB = None

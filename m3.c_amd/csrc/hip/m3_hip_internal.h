@@ -47,7 +47,12 @@ struct m3_hip_device {
      * next scan, and the flags' host mirror in coherent pinned memory */
     uint32_t *scan_flags;
     uint32_t scan_epoch;
-    uint32_t *host_flags;
+    uint32_t *host_flags; /* two halves: blocking scans, started scans */
+    /* the last scan started with m3_hip_scan_views_begin: its ticket, the
+     * completion sequence after its publication, and its view count */
+    uint32_t async_ticket;
+    uint32_t async_sequence;
+    uint32_t async_count;
     /* the device address of the static scan scratch (m3_hip_runtime.hip) */
     uint32_t *static_scratch;
     /* completion word in coherent pinned host memory (may be null) and the

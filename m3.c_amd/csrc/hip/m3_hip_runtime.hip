@@ -267,7 +267,7 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
                         "hipStreamCreateWithFlags", message, capacity);
     if (code == M3_HIP_OK) {
         code = m3_hip_check(hipHostMalloc((void **)&device->host_flags,
-                                          kScanViews * sizeof(uint32_t),
+                                          2U * kScanViews * sizeof(uint32_t),
                                           hipHostMallocCoherent),
                             "hipHostMalloc", message, capacity);
     }
@@ -577,13 +577,17 @@ static int m3_hip_stream_errors(m3_hip_device *device, char *message,
 }
 
 /* Polls the completion word for `sequence` for at most kDonePollSeconds;
- * true when it arrived. */
+ * true when it arrived or a later sequence did (sequences grow by one per
+ * completion queued on the stream, which stores them in order). */
 static bool m3_hip_poll_done(const m3_hip_device *device, uint32_t sequence)
 {
     const auto start = std::chrono::steady_clock::now();
 
     for (uint32_t spin = 0U;; ++spin) {
-        if (__atomic_load_n(device->done_word, __ATOMIC_ACQUIRE) == sequence) {
+        const uint32_t seen = __atomic_load_n(device->done_word,
+                                              __ATOMIC_ACQUIRE);
+
+        if ((int32_t)(seen - sequence) >= 0) {
             return true;
         }
         if ((spin & 255U) == 255U &&
@@ -769,13 +773,16 @@ __global__ __launch_bounds__(64) void m3_scan_publish_kernel(
     }
 }
 
-/* Scans views[0, count) into the flag words `flags` with `epoch` and
- * returns one flag per view in `result`. */
-static int m3_hip_scan_into(m3_hip_device *device, uint32_t *flags,
-                            uint32_t epoch, const uint32_t *kinds,
-                            const m3_hip_view *views, size_t count,
-                            uint32_t *result, bool timed, char *message,
-                            size_t capacity)
+/* Queues the scan of views[0, count) into the flag words `flags` with
+ * `epoch` and the publication of one flag per view into the pinned words
+ * `published`; *sequence receives the completion sequence that follows
+ * the publication. */
+static int m3_hip_scan_queue(m3_hip_device *device, uint32_t *flags,
+                             uint32_t epoch, const uint32_t *kinds,
+                             const m3_hip_view *views, size_t count,
+                             uint32_t *published, bool timed,
+                             uint32_t *sequence_out, char *message,
+                             size_t capacity)
 {
     int code = M3_HIP_OK;
     uint32_t sequence = device->done_sequence;
@@ -850,8 +857,8 @@ static int m3_hip_scan_into(m3_hip_device *device, uint32_t *flags,
                 hipExtLaunchKernelGGL(m3_scan_publish_kernel, dim3(1),
                                       dim3(64), 0, device->stream, start,
                                       stop, 0U, flags, (uint32_t)count,
-                                      epoch, device->host_flags,
-                                      device->done_word, sequence);
+                                      epoch, published, device->done_word,
+                                      sequence);
             },
             message, capacity);
     }
@@ -862,6 +869,18 @@ static int m3_hip_scan_into(m3_hip_device *device, uint32_t *flags,
     if (device->done_word != nullptr) {
         device->done_sequence = sequence;
     }
+    *sequence_out = sequence;
+    return M3_HIP_OK;
+}
+
+/* Waits until the publication that completion `sequence` follows has
+ * happened and copies its `count` flags from `published`. */
+static int m3_hip_scan_wait(m3_hip_device *device, uint32_t sequence,
+                            const uint32_t *published, size_t count,
+                            uint32_t *result, char *message, size_t capacity)
+{
+    int code;
+
     if (device->done_word != nullptr && !device->timing &&
         m3_hip_poll_done(device, sequence)) {
         code = m3_hip_stream_errors(device, message, capacity);
@@ -870,9 +889,29 @@ static int m3_hip_scan_into(m3_hip_device *device, uint32_t *flags,
                             "hipStreamSynchronize", message, capacity);
     }
     for (size_t i = 0U; code == M3_HIP_OK && i < count; ++i) {
-        result[i] = __atomic_load_n(&device->host_flags[i], __ATOMIC_ACQUIRE);
+        result[i] = __atomic_load_n(&published[i], __ATOMIC_ACQUIRE);
     }
     return code;
+}
+
+/* Scans views[0, count) into the flag words `flags` with `epoch` and
+ * returns one flag per view in `result`. */
+static int m3_hip_scan_into(m3_hip_device *device, uint32_t *flags,
+                            uint32_t epoch, const uint32_t *kinds,
+                            const m3_hip_view *views, size_t count,
+                            uint32_t *result, bool timed, char *message,
+                            size_t capacity)
+{
+    uint32_t sequence = 0U;
+    int code = m3_hip_scan_queue(device, flags, epoch, kinds, views, count,
+                                 device->host_flags, timed, &sequence,
+                                 message, capacity);
+
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    return m3_hip_scan_wait(device, sequence, device->host_flags, count,
+                            result, message, capacity);
 }
 
 static int m3_hip_scan_arguments(const m3_hip_device *device,
@@ -903,17 +942,13 @@ static int m3_hip_scan_arguments(const m3_hip_device *device,
     return M3_HIP_OK;
 }
 
-extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
-                                 const m3_hip_view *views, size_t count,
-                                 uint32_t *flags, char *message,
-                                 size_t capacity)
+/* The device's flag words (allocated on first use) and the next epoch:
+ * 0 is what the words hold after a clear and is never a scan's epoch; a
+ * fresh array, and one whose epochs wrapped, is cleared first. */
+static int m3_hip_scan_epoch(m3_hip_device *device, char *message,
+                             size_t capacity)
 {
-    int code = m3_hip_scan_arguments(device, kinds, views, count, flags,
-                                     message, capacity);
-
-    if (code != M3_HIP_OK || count == 0U) {
-        return code;
-    }
+    int code = M3_HIP_OK;
     bool fresh = false;
 
     if (device->scan_flags == nullptr) {
@@ -940,12 +975,83 @@ extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
             },
             message, capacity);
     }
+    return code;
+}
+
+extern "C" int m3_hip_scan_views(m3_hip_device *device, const uint32_t *kinds,
+                                 const m3_hip_view *views, size_t count,
+                                 uint32_t *flags, char *message,
+                                 size_t capacity)
+{
+    int code = m3_hip_scan_arguments(device, kinds, views, count, flags,
+                                     message, capacity);
+
+    if (code != M3_HIP_OK || count == 0U) {
+        return code;
+    }
+    code = m3_hip_scan_epoch(device, message, capacity);
     if (code != M3_HIP_OK) {
         return code;
     }
     return m3_hip_scan_into(device, device->scan_flags, device->scan_epoch,
                             kinds, views, count, flags, true, message,
                             capacity);
+}
+
+extern "C" int m3_hip_scan_views_begin(m3_hip_device *device,
+                                       const uint32_t *kinds,
+                                       const m3_hip_view *views,
+                                       size_t count, uint32_t *ticket,
+                                       char *message, size_t capacity)
+{
+    uint32_t sequence = 0U;
+    int code;
+
+    if (ticket == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "scan ticket output is null");
+    }
+    code = m3_hip_scan_arguments(device, kinds, views, count, ticket, message,
+                                 capacity);
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    code = m3_hip_scan_epoch(device, message, capacity);
+    if (code == M3_HIP_OK) {
+        code = m3_hip_scan_queue(device, device->scan_flags,
+                                 device->scan_epoch, kinds, views, count,
+                                 device->host_flags + kScanViews, true,
+                                 &sequence, message, capacity);
+    }
+    if (code != M3_HIP_OK) {
+        device->async_count = 0U;
+        return code;
+    }
+    device->async_ticket += 1U;
+    device->async_sequence = sequence;
+    device->async_count = (uint32_t)count;
+    *ticket = device->async_ticket;
+    return M3_HIP_OK;
+}
+
+extern "C" int m3_hip_scan_views_collect(m3_hip_device *device,
+                                         uint32_t ticket, size_t count,
+                                         uint32_t *flags, char *message,
+                                         size_t capacity)
+{
+    if (device == nullptr || (count != 0U && flags == nullptr)) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "scan collection arguments are incomplete");
+    }
+    if (ticket != device->async_ticket || count != device->async_count) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "scan ticket %u with %zu views is not the last "
+                           "started scan",
+                           ticket, count);
+    }
+    return m3_hip_scan_wait(device, device->async_sequence,
+                            device->host_flags + kScanViews, count, flags,
+                            message, capacity);
 }
 
 extern "C" int m3_hip_scan_views_static(m3_hip_device *device,

@@ -24,9 +24,13 @@
  * and the first command in list order that fails either check decides the
  * status (OUT_OF_RANGE for data), with no output modified. A view that
  * passed its check is remembered until its storage is written (host write,
- * kernel output) or freed, so an unchanged input is not scanned again. Then every
- * command is enqueued in order on the device stream and the list waits
- * once at the end.
+ * kernel output) or freed, so an unchanged input is not scanned again.
+ * Views the preflight has scanned are also watched: a host write to their
+ * storage starts their scan on the device right after the copy
+ * (m3_hip_scan_views_begin) and returns, and the next preflight collects
+ * its flags instead of scanning, so the scan runs while the host is busy
+ * between the write and the run. Then every command is enqueued in order
+ * on the device stream and the list waits once at the end.
  */
 #include "m3_backend_internal.h"
 
@@ -41,6 +45,7 @@
 #define M3_HIP_MAX_ARENAS 16U
 #define M3_HIP_MESSAGE 256U
 #define M3_HIP_CLEAN_VIEWS 64U
+#define M3_HIP_WATCHED_VIEWS 16U
 
 typedef struct {
     uint8_t *base;
@@ -63,6 +68,17 @@ typedef struct {
     uint32_t clean_kinds[M3_HIP_CLEAN_VIEWS];
     size_t clean_count;
     size_t clean_next;
+    /* views the preflight has scanned, rescanned early after host writes */
+    m3_hip_view watched[M3_HIP_WATCHED_VIEWS];
+    uint32_t watched_kinds[M3_HIP_WATCHED_VIEWS];
+    size_t watched_count;
+    /* the scan a host write started, until a preflight collects it; an
+     * entry whose storage is written again before that is dropped */
+    m3_hip_view started[M3_HIP_WATCHED_VIEWS];
+    uint32_t started_kinds[M3_HIP_WATCHED_VIEWS];
+    bool started_valid[M3_HIP_WATCHED_VIEWS];
+    size_t started_count;
+    uint32_t started_ticket;
 } m3_hip_backend_context;
 
 static bool m3_hip_same_view(const m3_hip_view *a, const m3_hip_view *b)
@@ -115,11 +131,19 @@ static void m3_hip_remember_clean(m3_hip_backend_context *context,
     context->clean_kinds[slot] = kind;
 }
 
-/* Forgets every clean view over the storage that starts at `base`. */
+/* Forgets every clean view over the storage that starts at `base`, and
+ * the started scan of any. */
 static void m3_hip_forget_storage(m3_hip_backend_context *context,
                                   const void *base)
 {
     size_t i = 0U;
+
+    for (i = 0U; i < context->started_count; ++i) {
+        if (context->started[i].base == base) {
+            context->started_valid[i] = false;
+        }
+    }
+    i = 0U;
 
     while (i < context->clean_count) {
         if (context->clean[i].base == base) {
@@ -147,6 +171,55 @@ static m3_status m3_hip_status(int code, const char *message,
     default:
         return m3_error_set(error, M3_STATUS_INTERNAL, "%s", message);
     }
+}
+
+/* Watches (view, kind) for early rescans after host writes. */
+static void m3_hip_watch(m3_hip_backend_context *context,
+                         const m3_hip_view *view, uint32_t kind)
+{
+    size_t i;
+
+    for (i = 0U; i < context->watched_count; ++i) {
+        if (context->watched_kinds[i] == kind &&
+            m3_hip_same_view(&context->watched[i], view)) {
+            return;
+        }
+    }
+    if (context->watched_count < M3_HIP_WATCHED_VIEWS) {
+        context->watched[context->watched_count] = *view;
+        context->watched_kinds[context->watched_count] = kind;
+        context->watched_count += 1U;
+    }
+}
+
+/* Collects the scan a host write started, if any: every entry still valid
+ * whose view passed is remembered clean (one that failed is left to the
+ * preflight, which scans it again and reports it). */
+static m3_status m3_hip_settle_started(m3_hip_backend_context *context,
+                                       m3_error *error)
+{
+    uint32_t flags[M3_HIP_WATCHED_VIEWS];
+    char message[M3_HIP_MESSAGE] = "";
+    size_t count = context->started_count;
+    size_t i;
+    int code;
+
+    if (count == 0U) {
+        return M3_STATUS_OK;
+    }
+    context->started_count = 0U;
+    code = m3_hip_scan_views_collect(context->device, context->started_ticket,
+                                     count, flags, message, sizeof(message));
+    if (code != M3_HIP_OK) {
+        return m3_hip_status(code, message, error);
+    }
+    for (i = 0U; i < count; ++i) {
+        if (context->started_valid[i] && flags[i] == 0U) {
+            m3_hip_remember_clean(context, &context->started[i],
+                                  context->started_kinds[i]);
+        }
+    }
+    return M3_STATUS_OK;
 }
 
 static void m3_hip_destroy(void *opaque)
@@ -254,8 +327,20 @@ static m3_status m3_hip_allocate(void *opaque, size_t byte_count,
 static void m3_hip_free_storage(void *opaque, void *handle, void *data)
 {
     m3_hip_backend_context *context = opaque;
+    size_t i = 0U;
 
     m3_hip_forget_storage(context, data);
+    /* memory at this address may later hold other storage */
+    while (i < context->watched_count) {
+        if (context->watched[i].base == data) {
+            context->watched_count -= 1U;
+            context->watched[i] = context->watched[context->watched_count];
+            context->watched_kinds[i] =
+                context->watched_kinds[context->watched_count];
+        } else {
+            ++i;
+        }
+    }
     if (handle != NULL && m3_hip_arena_of(context, handle) == NULL) {
         /* queued commands may still use the memory */
         (void)m3_hip_synchronize(context->device, NULL, 0U);
@@ -269,14 +354,48 @@ static m3_status m3_hip_write(void *opaque, void *data, size_t byte_offset,
 {
     m3_hip_backend_context *context = opaque;
     char message[M3_HIP_MESSAGE] = "";
+    m3_hip_view views[M3_HIP_WATCHED_VIEWS];
+    uint32_t kinds[M3_HIP_WATCHED_VIEWS];
+    size_t count = 0U;
+    size_t i;
+    m3_status status;
     int code;
 
     m3_hip_forget_storage(context, data);
     code = m3_hip_copy_h2d(context->device, (uint8_t *)data + byte_offset,
                                source, byte_count, message, sizeof(message));
-
-    return code == M3_HIP_OK ? M3_STATUS_OK
-                             : m3_hip_status(code, message, error);
+    if (code != M3_HIP_OK) {
+        return m3_hip_status(code, message, error);
+    }
+    for (i = 0U; i < context->watched_count; ++i) {
+        if (context->watched[i].base == data) {
+            views[count] = context->watched[i];
+            kinds[count] = context->watched_kinds[i];
+            count += 1U;
+        }
+    }
+    if (count == 0U) {
+        return M3_STATUS_OK;
+    }
+    /* only the last started scan can be collected: settle the previous one
+     * first (it has usually finished by now) */
+    status = m3_hip_settle_started(context, error);
+    if (status != M3_STATUS_OK) {
+        return status;
+    }
+    code = m3_hip_scan_views_begin(context->device, kinds, views, count,
+                                   &context->started_ticket, message,
+                                   sizeof(message));
+    if (code != M3_HIP_OK) {
+        return m3_hip_status(code, message, error);
+    }
+    for (i = 0U; i < count; ++i) {
+        context->started[i] = views[i];
+        context->started_kinds[i] = kinds[i];
+        context->started_valid[i] = true;
+    }
+    context->started_count = count;
+    return M3_STATUS_OK;
 }
 
 static m3_status m3_hip_read(void *opaque, const void *data,
@@ -477,8 +596,11 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
 {
     size_t scans = 0U;
     size_t i;
-    m3_status status;
+    m3_status status = m3_hip_settle_started(context, error);
 
+    if (status != M3_STATUS_OK) {
+        return status;
+    }
     for (i = 0U; i < count; ++i) {
         uint32_t kind = 0U;
         const m3_tensor_view *input = m3_hip_checked_input(&commands[i],
@@ -512,6 +634,8 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
         }
     }
     for (i = 0U; i < scans; ++i) {
+        m3_hip_watch(context, &context->scan_views[i],
+                     context->scan_kinds[i]);
         if (context->scan_flags[i] == 0U) {
             m3_hip_remember_clean(context, &context->scan_views[i],
                                   context->scan_kinds[i]);

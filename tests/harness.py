@@ -418,6 +418,24 @@ class HipScanFixture:
                                         count, flags, self.message, 256)
         return code, list(flags[:count]), self.message.value.decode()
 
+    def begin(self, kinds, views):
+        """m3_hip_scan_views_begin; returns (code, ticket, message)."""
+        count = len(views)
+        kind_array = (ctypes.c_uint32 * max(count, 1))(*kinds)
+        view_array = (m3.HipView * max(count, 1))(*views)
+        ticket = ctypes.c_uint32(0)
+        code = self.hip.m3_hip_scan_views_begin(
+            self.device, kind_array, view_array, count, ctypes.byref(ticket),
+            self.message, 256)
+        return code, ticket.value, self.message.value.decode()
+
+    def collect(self, ticket, count):
+        """m3_hip_scan_views_collect; returns (code, flags, message)."""
+        flags = (ctypes.c_uint32 * max(count, 1))(*([7] * max(count, 1)))
+        code = self.hip.m3_hip_scan_views_collect(
+            self.device, ticket, count, flags, self.message, 256)
+        return code, list(flags[:count]), self.message.value.decode()
+
     def close(self):
         if self.base.value:
             self.hip.m3_hip_arena_release(self.device, self.base)

@@ -168,6 +168,86 @@ def test_clean_input_cache_sees_later_writes(hip):
         m3.OUT_OF_RANGE
 
 
+def test_write_starts_rescan_of_watched_inputs(hip):
+    """A host write to an input the preflight has scanned starts its rescan
+    on the device; the next list collects it. Whatever happens between the
+    write and the run (a second write, a kernel writing the input, a NaN
+    written and then overwritten), the run sees the data it reads."""
+    print("gpu case write_starts_rescan", file=sys.stderr, flush=True)
+    arrays = [f32([0, 1, 2, 3]), np.zeros(16, np.uint8), f32([1, 1, 1, 1])]
+    h = hip.upload(arrays)
+    sm_in, sm_out, other = hip.views(
+        h, [ViewSpec(0, m3.F32, (4,)), ViewSpec(1, m3.F32, (4,)),
+            ViewSpec(2, m3.F32, (4,))])
+    assert hip.execute([(m3.OP_SOFTMAX, [sm_in, sm_out])])[0] == m3.OK
+    expected = values(hip, h[1], 4)
+    # clean write: the started scan passes and the run uses it
+    write(hip, h[0], f32([0, 1, 2, 3]))
+    assert hip.execute([(m3.OP_SOFTMAX, [sm_in, sm_out])])[0] == m3.OK
+    assert list(values(hip, h[1], 4)) == list(expected)
+    # NaN written, then overwritten before the run
+    write(hip, h[0], f32([0, math.nan, 2, 3]))
+    write(hip, h[0], f32([0, 1, 2, 3]))
+    assert hip.execute([(m3.OP_SOFTMAX, [sm_in, sm_out])])[0] == m3.OK
+    # clean written, then NaN before the run: rejected, output untouched
+    write(hip, h[0], f32([0, 1, 2, 3]))
+    write(hip, h[0], f32([math.nan, 1, 2, 3]))
+    hip_out_before = list(values(hip, h[1], 4))
+    assert hip.execute([(m3.OP_SOFTMAX, [sm_in, sm_out])])[0] == \
+        m3.OUT_OF_RANGE
+    assert list(values(hip, h[1], 4)) == hip_out_before
+    # clean written (scan started), then a kernel writes a NaN into the
+    # input in another list before the softmax runs
+    write(hip, h[0], f32([0, 1, 2, 3]))
+    write(hip, h[2], f32([math.nan, 1, 1, 1]))
+    assert hip.execute([(m3.OP_MUL, [sm_in, other, sm_in])])[0] == m3.OK
+    assert hip.execute([(m3.OP_SOFTMAX, [sm_in, sm_out])])[0] == \
+        m3.OUT_OF_RANGE
+    # and clean again
+    write(hip, h[0], f32([3, 2, 1, 0]))
+    assert hip.execute([(m3.OP_SOFTMAX, [sm_in, sm_out])])[0] == m3.OK
+    assert list(values(hip, h[1], 4)) == list(expected[::-1])
+
+
+def test_started_scans_through_the_c_abi(gpu):
+    """m3_hip_scan_views_begin/collect: the flags of a started scan are
+    those of the blocking scan of the same views, also with a blocking scan
+    in between; only the last started scan can be collected."""
+    from harness import HipScanFixture
+
+    scan = HipScanFixture()
+    try:
+        rng = np.random.default_rng(13)
+        clean = rng.standard_normal(1 << 20).astype(np.float32)
+        dirty = clean.copy()
+        dirty[123457] = np.nan
+        a_clean, a_dirty = scan.upload(clean), scan.upload(dirty)
+        v_clean = scan.view(a_clean, m3.F32, (1 << 20,))
+        v_dirty = scan.view(a_dirty, m3.F32, (1 << 20,))
+        v_odd = scan.view(a_dirty + 4, m3.F32, (1 << 19,), (8,))
+        nan = 0
+        code, ticket, message = scan.begin([nan, nan, nan],
+                                           [v_dirty, v_clean, v_odd])
+        assert code == 0, message
+        code, flags, message = scan.scan("m3_hip_scan_views", [nan, nan],
+                                         [v_clean, v_dirty])
+        assert code == 0 and flags == [0, 1], message
+        code, flags, message = scan.collect(ticket, 3)
+        assert code == 0, message
+        # 123457 is odd: the view from element 1 with stride 2 holds it
+        assert flags == [1, 0, 1]
+        code, first, message = scan.begin([nan], [v_clean])
+        assert code == 0, message
+        code, second, message = scan.begin([nan], [v_dirty])
+        assert code == 0, message
+        assert scan.collect(first, 1)[0] != 0
+        code, flags, message = scan.collect(second, 1)
+        assert code == 0 and flags == [1], message
+        assert scan.collect(second, 2)[0] != 0
+    finally:
+        scan.close()
+
+
 def test_scan_flags_follow_each_call(gpu):
     """m3_hip_scan_views through the C-ABI, call after call: flags are set
     exactly for the views that offend in that call (a NaN, or a value
