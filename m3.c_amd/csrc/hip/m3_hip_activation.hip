@@ -27,8 +27,8 @@
  * All-BF16 GATED_SILU looks its activation up in a 16 KB table that each
  * device builds once (m3_gated_silu_bf16_kernel): a BF16 gate has only
  * 65,536 values, and the rounded activation depends on the gate alone.
- * That takes the kernel from ~52 VALU instructions per element, clock-bound,
- * to about a dozen, bound by HBM.
+ * That takes the kernel from 52 VALU instructions per element, clock-bound,
+ * to 25, bound by HBM.
  */
 #include "m3_activation.h"
 #include "m3_hip_internal.h"
