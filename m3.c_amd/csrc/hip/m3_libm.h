@@ -39,6 +39,15 @@
 #define M3_LIBM_CONST static const
 #endif
 
+/* True when `condition` holds in any lane of the wave on the device, and
+ * simply `condition` on the host: straight-line code uses it to skip work
+ * that no lane of a wave needs. */
+#if defined(__HIP_DEVICE_COMPILE__)
+#define M3_ANY_LANE(condition) (__any(condition) != 0)
+#else
+#define M3_ANY_LANE(condition) (condition)
+#endif
+
 M3_HD uint64_t m3_f64_bits(double value)
 {
 #if defined(__HIPCC__)
@@ -523,10 +532,12 @@ M3_HD float m3_div_one_step(float a, float b)
  * straight-line code: every case of the reduction is the general one with
  * k = 0 (no reduction, c = 0), k = +-1 below 1.5 ln2, or k = round(v/ln2),
  * which gives the same hi, lo, x and c bit for bit; the reconstructions
- * of the cases k = 0, k = -1, k <= -2 or k > 56, 2 <= k < 23 and
- * 23 <= k <= 56 are all formed and one is selected; below |v| = 2^-25,
- * where the library returns v, the k = 0 form gives v as well. (k = 1
- * needs v in (ln2/2, 1.5 ln2), outside that domain.)
+ * of the cases k = 0, k = -1, k <= -2 and 2 <= k < 23 are all formed and
+ * one is selected, and those of 23 <= k <= 56 and k > 56 (tanh's |x| of
+ * 7.97 and more) only in a wave that has such an argument; below
+ * |v| = 2^-25, where the library returns v, the k = 0 form gives v as
+ * well. (k = 1 needs v in (ln2/2, 1.5 ln2), outside that domain, so
+ * 1.5 ln2 > |v| > ln2 / 2 means k = -1.)
  * The quotient of the polynomial step has operands near -2 and 6, so
  * m3_div_normal applies. */
 M3_HD float m3_expm1f_tanh(float v)
@@ -541,14 +552,15 @@ M3_HD float m3_expm1f_tanh(float v)
     const float q5 = -2.0109921195e-07F;
     const uint32_t hv = m3_f32_bits(v);
     const uint32_t hx = hv & 0x7fffffffU;
-    const int negative = (hv & 0x80000000U) != 0U;
-    int32_t k = (int32_t)(invln2 * v + (negative ? -0.5F : 0.5F));
-
-    if (hx <= 0x3eb17218U) { /* |v| <= ln2 / 2 */
-        k = 0;
-    } else if (hx < 0x3f851592U) { /* |v| < 1.5 ln2 */
-        k = negative ? -1 : 1;
-    }
+    /* +-0.5 with v's sign */
+    const float half = m3_bits_f32(0x3f000000U | (hv & 0x80000000U));
+    /* |v| <= ln2 / 2: k = 0; |v| < 1.5 ln2: k = -1 (v < 0 there); no
+     * other argument rounds to k = 0 or -1 */
+    const int k_zero = hx <= 0x3eb17218U;
+    const int k_minus_one = hx < 0x3f851592U;
+    const int32_t k = k_zero ? 0
+                      : k_minus_one ? -1
+                                    : (int32_t)(invln2 * v + half);
     const float kf = (float)k;
     const float hi = v - kf * ln2_hi;
     const float lo = kf * ln2_lo;
@@ -571,17 +583,23 @@ M3_HD float m3_expm1f_tanh(float v)
     const float low_t =
         m3_bits_f32(0x3f800000U - (0x1000000U >> ((uint32_t)k & 31U)));
     const float low = m3_bits_f32(m3_f32_bits(low_t - (f - x)) + kbits);
-    const float high_t = m3_bits_f32((uint32_t)(0x7f - k) << 23U);
-    float high = x - (f + high_t);
+    float result = k <= -2 ? outer : low;
+    /* k >= 23 (tanh's |x| from 7.97 on): formed only in a wave that has
+     * such an argument */
+    const int high_case = k >= 23;
 
-    high += 1.0F;
-    high = m3_bits_f32(m3_f32_bits(high) + kbits);
-    float result = (k <= -2 || k > 56) ? outer : k < 23 ? low : high;
+    if (M3_ANY_LANE(high_case)) {
+        const float high_t = m3_bits_f32((uint32_t)(0x7f - k) << 23U);
+        float high = x - (f + high_t);
 
-    result = k == -1 ? minus_one_k : result;
+        high += 1.0F;
+        high = m3_bits_f32(m3_f32_bits(high) + kbits);
+        result = k > 56 ? outer : high_case ? high : result;
+    }
+    result = k_minus_one ? minus_one_k : result;
     /* for |v| < 2^-25 the library returns v itself; zero_k is v there too
      * (x = v and x * e - hxs is below a quarter of v's ulp) */
-    return k == 0 ? zero_k : result;
+    return k_zero ? zero_k : result;
 }
 
 /* m3_tanhf as straight-line code with one expm1f evaluation and one
@@ -604,18 +622,25 @@ M3_HD float m3_tanhf_uniform(float x)
     const float magnitude = m3_bits_f32(ix < 0x41b00000U ? ix : 0x41b00000U);
     const float t = m3_expm1f_tanh((big ? 2.0F : -2.0F) * magnitude);
     const float q = m3_div_one_step(big ? 2.0F : -t, t + 2.0F);
+    const uint32_t sign = jx & 0x80000000U;
+    /* |x| >= 22, infinities and NaN, or |x| < 2^-55: handled only in a
+     * wave that has such an input */
+    const int rare = ix - 0x24000000U >= 0x41b00000U - 0x24000000U;
     float z = big ? 1.0F - q : q; /* +0 or positive */
 
-    if (ix >= 0x41b00000U) { /* |x| >= 22 and infinities */
-        z = 1.0F - 1.0e-30F;
-    }
-    z = m3_bits_f32(m3_f32_bits(z) | (jx & 0x80000000U));
-    if (ix < 0x24000000U) { /* |x| < 2^-55, zeros and subnormals included:
-                             * 1 + x rounds to 1, so x * (1 + x) is x */
-        z = x;
-    }
-    if (ix > 0x7f800000U) {
-        z = m3_bits_f32(jx | 0x00400000U);
+    z = m3_bits_f32(m3_f32_bits(z) | sign);
+    if (M3_ANY_LANE(rare)) {
+        if (ix >= 0x41b00000U) { /* |x| >= 22 and infinities */
+            z = m3_bits_f32(m3_f32_bits(1.0F - 1.0e-30F) | sign);
+        }
+        if (ix < 0x24000000U) { /* |x| < 2^-55, zeros and subnormals
+                                 * included: 1 + x rounds to 1, so
+                                 * x * (1 + x) is x */
+            z = x;
+        }
+        if (ix > 0x7f800000U) {
+            z = m3_bits_f32(jx | 0x00400000U);
+        }
     }
     return z;
 }

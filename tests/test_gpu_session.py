@@ -497,3 +497,37 @@ def test_scaled_scores_then_softmax(gpu):
     again = session.read(y, np.zeros(shape, np.float32))
     assert np.array_equal(again.view(np.uint32), out.view(np.uint32))
     session.free()
+
+
+def test_timing_samples_follow_the_launches(gpu):
+    """m3_hip_timing_samples gives one positive duration per launch of a
+    kernel, in launch order, and their sum is m3_hip_timing_read's total;
+    a reset empties both."""
+    shape = (4, 1024, 256)
+    x = m3.rng_fill("normal", int(np.prod(shape)), seed=3,
+                    a=1.0).reshape(shape)
+    g = m3.Graph()
+    vx = g.add_value(m3.INPUT, m3.F32, shape)
+    vy = g.add_value(m3.OUTPUT, m3.F32, shape)
+    g.add_node(m3.OP_TANH, [vx], [vy])
+    session = m3.Session(g)
+    g.free()
+    try:
+        session.write(vx, x)
+        session.run()
+        session.timing_reset()
+        session.timing_enable(True)
+        for _ in range(3):
+            session.run()
+        totals = session.timing_read()
+        samples = session.timing_samples("m3_tanh")
+        session.timing_enable(False)
+        assert totals["m3_tanh"][0] == 3
+        assert len(samples) == 3 and min(samples) > 0.0
+        assert abs(sum(samples) - totals["m3_tanh"][1]) <= \
+            1e-6 * max(1.0, totals["m3_tanh"][1])
+        assert session.timing_samples("no such kernel") == []
+        session.timing_reset()
+        assert session.timing_samples("m3_tanh") == []
+    finally:
+        session.free()
