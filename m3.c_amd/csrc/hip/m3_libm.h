@@ -507,21 +507,19 @@ M3_HD float m3_div_normal(float a, float b)
 #endif
 }
 
-/* m3_div_normal with one correction step instead of two: the quotient
- * a * y of the refined reciprocal, corrected once by its residual. That
- * is the correctly rounded quotient except for rare operand pairs; the two
- * divisions of m3_tanhf_uniform use it, and the GPU test of TANH over every
- * F32 input shows that no input of tanhf reaches such a pair through
- * either of them. On the host it is the C division. */
+/* a / b for TANH's two divisions: the product of a and the hardware
+ * reciprocal of b, corrected once by its residual (4 instructions;
+ * m3_div_normal refines the reciprocal first and corrects twice, 8). That
+ * is the correctly rounded quotient for most operand pairs but not for
+ * all; the GPU test of TANH over every F32 input shows that no input of
+ * tanhf reaches such a pair through either division. On the host it is the
+ * C division. */
 M3_HD float m3_div_one_step(float a, float b)
 {
 #if defined(__HIP_DEVICE_COMPILE__)
-    float y = __builtin_amdgcn_rcpf(b);
-    const float e = fmaf(-b, y, 1.0F);
-    float q;
+    const float y = __builtin_amdgcn_rcpf(b);
+    const float q = a * y;
 
-    y = fmaf(e, y, y);
-    q = a * y;
     return fmaf(fmaf(-b, q, a), y, q);
 #else
     return a / b;
