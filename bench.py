@@ -197,16 +197,23 @@ class Workload:
         for i in range(steps):
             self.sessions[i % len(self.sessions)].run()
         wall = (time.perf_counter() - start) / steps
-        # the same steps again, back to back, with the library's timing
+        # The same steps again, back to back, with the library's timing
         # events on every dispatch; the durations are read once at the end,
         # so the runs follow each other as in the wall-clock pass (a host
         # pause of tens of microseconds between runs slows the VALU-heavy
         # kernels that follow it). Each run's dominant-kernel average is
         # kept, for the median beside the mean (VALU-bound kernels vary
-        # with the clock from run to run).
+        # with the clock from run to run). Unmeasured timed runs come first,
+        # as many per session as the measured pass makes, so that every
+        # session's event pool already holds the events it will use (a
+        # launch that has to create its events reads a microsecond or two
+        # long).
+        visits = -(-steps // len(self.sessions))
         for session in self.sessions:
-            session.timing_reset()
             session.timing_enable(True)
+            for _ in range(visits):
+                session.run()
+            session.timing_reset()
         for i in range(steps):
             self.sessions[i % len(self.sessions)].run()
         per_kernel = {}
