@@ -377,17 +377,20 @@ static m3_status m3_hip_write(void *opaque, void *data, size_t byte_offset,
     if (count == 0U) {
         return M3_STATUS_OK;
     }
-    /* only the last started scan can be collected: settle the previous one
-     * first (it has usually finished by now) */
+    /* The data is written; starting its scan early is an optimization. If
+     * settling the previous started scan (only the last one can be
+     * collected) or starting this one fails, nothing is started and the
+     * next preflight scans these views itself, reporting any device error
+     * there. */
     status = m3_hip_settle_started(context, error);
-    if (status != M3_STATUS_OK) {
-        return status;
+    if (status == M3_STATUS_OK) {
+        code = m3_hip_scan_views_begin(context->device, kinds, views, count,
+                                       &context->started_ticket, message,
+                                       sizeof(message));
     }
-    code = m3_hip_scan_views_begin(context->device, kinds, views, count,
-                                   &context->started_ticket, message,
-                                   sizeof(message));
-    if (code != M3_HIP_OK) {
-        return m3_hip_status(code, message, error);
+    if (status != M3_STATUS_OK || code != M3_HIP_OK) {
+        m3_error_reset(error);
+        return M3_STATUS_OK;
     }
     for (i = 0U; i < count; ++i) {
         context->started[i] = views[i];
