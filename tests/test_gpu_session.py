@@ -531,3 +531,51 @@ def test_timing_samples_follow_the_launches(gpu):
         assert session.timing_samples("m3_tanh") == []
     finally:
         session.free()
+
+
+def test_started_scans_of_two_inputs(gpu):
+    """Two softmax inputs in separate storages: a write to one starts its
+    scan, a write to the other settles that scan and starts its own, and
+    every run sees the data it reads; a session freed with a scan still
+    started frees cleanly."""
+    shape = (16, 256)
+    rng_a = m3.rng_fill("normal", 16 * 256, seed=5, a=2.0).reshape(shape)
+    rng_b = m3.rng_fill("normal", 16 * 256, seed=6, a=2.0).reshape(shape)
+    dirty_a = rng_a.copy()
+    dirty_a[3, 100] = np.nan
+    g = m3.Graph()
+    va = g.add_value(m3.INPUT, m3.F32, shape)
+    vb = g.add_value(m3.INPUT, m3.F32, shape)
+    oa = g.add_value(m3.OUTPUT, m3.F32, shape)
+    ob = g.add_value(m3.OUTPUT, m3.F32, shape)
+    g.add_node(m3.OP_SOFTMAX, [va], [oa])
+    g.add_node(m3.OP_SOFTMAX, [vb], [ob])
+    session = m3.Session(g)
+    g.free()
+    lib, _ = m3.load()
+    want_a = _oracle_unary(m3.OP_SOFTMAX, rng_a, m3.F32, shape, m3.F32,
+                           np.float32)
+    want_b = _oracle_unary(m3.OP_SOFTMAX, rng_b, m3.F32, shape, m3.F32,
+                           np.float32)
+    try:
+        session.write(va, rng_a)
+        session.write(vb, rng_b)
+        session.run()  # the first run scans; both views are now watched
+        for _ in range(2):
+            session.write(va, rng_a)  # starts the scan of a
+            session.write(vb, rng_b)  # settles a's, starts b's
+            session.run()
+            assert np.array_equal(bits(session.read(oa, np.zeros(
+                shape, np.float32))), bits(want_a))
+            assert np.array_equal(bits(session.read(ob, np.zeros(
+                shape, np.float32))), bits(want_b))
+        session.write(va, dirty_a)
+        session.write(vb, rng_b)
+        assert lib.m3_session_run(session.handle, None) == m3.OUT_OF_RANGE
+        session.write(va, rng_a)
+        session.run()
+        assert np.array_equal(bits(session.read(oa, np.zeros(
+            shape, np.float32))), bits(want_a))
+        session.write(vb, rng_b)  # left started
+    finally:
+        session.free()
