@@ -12,8 +12,9 @@
  *   - the maximum and k are order-independent, so they are reduced across
  *     the 64 lanes of a wavefront (DPP row operations);
  *   - e_j uses m3_expf (the libm algorithm restated bit for bit);
- *   - the sum keeps the reference's left-to-right F32 order: a lane per
- *     row walks the row's e_j in LDS;
+ *   - the sum keeps the reference's left-to-right F32 order: one
+ *     dependent addition per column, the addends reaching the summing
+ *     lanes through LDS or DPP broadcasts;
  *   - p_j is the IEEE F32 quotient e_j / sum, formed as
  *     RN_f32(e_j * RN_f64(1/sum)) where that is exact (m3_softmax_scale4).
  *
@@ -21,11 +22,16 @@
  * have aligned starts and a width that is a multiple of 4 and move in 16-
  * or 8-byte accesses, other rows element by element; row starts may be
  * evenly spaced or follow several outer axes (m3_softmax_row):
- *   - width <= 2048: wave-independent rows (m3_softmax_rows_kernel). A wave
- *     holds R rows in VGPRs, reduces max and k, forms e_j in place and
- *     streams 256-column chunks through a wave-private LDS tile where the
- *     in-order sums run; no workgroup barrier separates the phases, so
- *     waves overlap memory and arithmetic.
+ *   - F32 VEC rows of 513..1024 columns: four rows per wave, one per
+ *     16-lane DPP row, the in-order sums carried in registers by additions
+ *     whose addends are broadcast from lane to lane (row_newbcast), with no
+ *     LDS traffic (m3_softmax_lane_rows_kernel).
+ *   - other rows up to 2048 columns: wave-independent rows
+ *     (m3_softmax_rows_kernel). A wave holds R rows in VGPRs, reduces max
+ *     and k, forms e_j in place and streams 256-column chunks through a
+ *     wave-private LDS tile where the in-order sums run; no workgroup
+ *     barrier separates the phases, so waves overlap memory and
+ *     arithmetic.
  *   - VEC rows with evenly spaced starts up to 8192 columns: a 256-thread
  *     workgroup owns a tile of whole rows in LDS (m3_softmax_tiled_kernel);
  *     phase 1 loads a row, reduces max and k and writes e_j to LDS; phase 2
@@ -42,6 +48,7 @@
 #include "m3_libm.h"
 
 #include <cstring>
+#include <utility>
 
 namespace {
 
@@ -797,6 +804,200 @@ __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     m3_softmax_rows<VPL, R, DEPTH, F32IO, VEC>(a);
 }
 
+/* x of lane CTRL selects within this lane's 16-lane DPP row (`identity`
+ * where the control names no lane). */
+template <int CTRL>
+__device__ __forceinline__ float m3_dpp_f32(float identity, float x)
+{
+    return m3_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(
+        (int)m3_f32_bits(identity), (int)m3_f32_bits(x), CTRL, 0xF, 0xF,
+        false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t m3_dpp_u32(uint32_t x)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF,
+                                                 false);
+}
+
+/* Maximum and sum over the 16 lanes of a DPP row, in every lane of it:
+ * quads, then the other quad of each half (row_half_mirror), then the
+ * other half (row_mirror). */
+__device__ __forceinline__ float m3_row16_max(float m)
+{
+    m = fmaxf(m, m3_dpp_f32<0xB1>(-INFINITY, m));
+    m = fmaxf(m, m3_dpp_f32<0x4E>(-INFINITY, m));
+    m = fmaxf(m, m3_dpp_f32<0x141>(-INFINITY, m));
+    return fmaxf(m, m3_dpp_f32<0x140>(-INFINITY, m));
+}
+
+__device__ __forceinline__ uint32_t m3_row16_sum(uint32_t n)
+{
+    n += m3_dpp_u32<0xB1>(n);
+    n += m3_dpp_u32<0x4E>(n);
+    n += m3_dpp_u32<0x141>(n);
+    return n + m3_dpp_u32<0x140>(n);
+}
+
+/* s + (e of lane N of this DPP row): row_newbcast:N hands every lane of
+ * the row the addend of lane N, so the 16 lanes carry the same sum. */
+template <int N>
+__device__ __forceinline__ float m3_add_from_lane(float s, float e)
+{
+    return s + m3_dpp_f32<0x150 + N>(0.0F, e);
+}
+
+/* Continues the left-to-right sum over the 64 columns of one block: lane
+ * N holds columns 4N..4N+3 of it in e. */
+template <int... N>
+__device__ __forceinline__ float m3_block_sum(float s, float4 e,
+                                              std::integer_sequence<int, N...>)
+{
+    ((s = m3_add_from_lane<N>(s, e.x), s = m3_add_from_lane<N>(s, e.y),
+      s = m3_add_from_lane<N>(s, e.z), s = m3_add_from_lane<N>(s, e.w)),
+     ...);
+    return s;
+}
+
+constexpr uint32_t kLaneBlocks = 16U; /* float4 per lane, lane-row kernel */
+constexpr uint32_t kLaneRowWidth = 64U * kLaneBlocks;
+
+/* F32 rows of kLaneRowWidth / 2 + 1 .. kLaneRowWidth columns (aligned,
+ * a multiple of 4 wide), with the in-order sum carried in registers. A
+ * wave takes four consecutive rows, one per 16-lane DPP row (lanes
+ * 16k..16k+15 hold row k); lane i of a row holds columns 4i + 64j ..
+ * 4i + 64j + 3 (block j = 0..15), so each load instruction reads four runs
+ * of 256 bytes. The maximum is reduced within the 16 lanes and e_j formed
+ * in place; then the left-to-right sum is one dependent addition per
+ * column, whose addend comes from the lane holding it (m3_add_from_lane),
+ * and the four rows advance together. Against the rows kernel this
+ * removes the LDS tile: there every lane group reads its row's e_j back
+ * from LDS, at a bandwidth cost per CU that set the sum's pace. As there,
+ * the sum stops after the wave's last float4 holding something other than
+ * -inf (later terms are +0). Rows whose maximum is +-inf are written from
+ * their inputs before the exponentials (zeros, or 1/k on their k +inf
+ * entries) behind a wave-uniform test. FULL rows are exactly
+ * kLaneRowWidth wide; otherwise blocks of the second half may lie past the
+ * width, read four -inf from m3_minus_inf4 there and are not stored. */
+template <bool FULL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void m3_softmax_lane_rows_kernel(m3_softmax_args a)
+{
+    __shared__ uint64_t exp_table[32];
+    const uint32_t lane = threadIdx.x & 63U;
+    const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
+    const uint32_t sub = lane & 15U;
+    const uint32_t width = a.width;
+    const uint64_t out_pitch = (uint64_t)width * 4U;
+    const uint64_t tasks = (a.rows + 3U) / 4U;
+
+    if (threadIdx.x < 32U) {
+        exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
+    }
+    __syncthreads();
+    for (uint64_t task = (uint64_t)blockIdx.x * kWaves + wave; task < tasks;
+         task += (uint64_t)gridDim.x * kWaves) {
+        const uint64_t row = task * 4U + (lane >> 4U);
+        const bool present = row < a.rows;
+        /* a row past the end of the tensor reads the task's first row */
+        const uint8_t *in = m3_softmax_row(a, present ? row : task * 4U);
+        uint8_t *out = a.output + row * out_pitch;
+        float4 v[kLaneBlocks];
+        float m = -INFINITY;
+        uint32_t last = 0U; /* 1 + index of the last float4 not all -inf */
+
+#pragma unroll
+        for (int j = 0; j < (int)kLaneBlocks; ++j) {
+            const bool inside = FULL || j < (int)kLaneBlocks / 2 ||
+                                sub * 4U + 64U * j < width;
+            const m3_f32x4 *source =
+                inside ? (const m3_f32x4 *)(in + sub * 16U) + 16 * j
+                       : (const m3_f32x4 *)&m3_minus_inf4;
+            const m3_f32x4 w = __builtin_nontemporal_load(source);
+
+            v[j] = make_float4(w[0], w[1], w[2], w[3]);
+        }
+#pragma unroll
+        for (int j = 0; j < (int)kLaneBlocks; ++j) {
+            const float t = fmaxf(fmaxf(v[j].x, v[j].y),
+                                  fmaxf(v[j].z, v[j].w));
+
+            m = fmaxf(m, t);
+            last = t != -INFINITY ? sub + 16U * j + 1U : last;
+        }
+        m = m3_row16_max(m);
+        const uint32_t length = m3_uniform_u32(m3_wave_max_u32(last));
+        const bool finite = m != INFINITY && m != -INFINITY;
+
+        if (M3_ANY_LANE(!finite)) {
+            uint32_t count = 0U;
+
+#pragma unroll
+            for (int j = 0; j < (int)kLaneBlocks; ++j) {
+                count += (v[j].x == INFINITY) + (v[j].y == INFINITY) +
+                         (v[j].z == INFINITY) + (v[j].w == INFINITY);
+            }
+            const float one_over_count = 1.0F / (float)m3_row16_sum(count);
+
+            if (!finite && present) {
+#pragma unroll
+                for (int j = 0; j < (int)kLaneBlocks; ++j) {
+                    float4 p;
+
+                    p.x = v[j].x == INFINITY ? one_over_count : 0.0F;
+                    p.y = v[j].y == INFINITY ? one_over_count : 0.0F;
+                    p.z = v[j].z == INFINITY ? one_over_count : 0.0F;
+                    p.w = v[j].w == INFINITY ? one_over_count : 0.0F;
+                    if (FULL || j < (int)kLaneBlocks / 2 ||
+                        sub * 4U + 64U * j < width) {
+                        m3_stream_store((float4 *)(out + sub * 16U) + 16 * j,
+                                        p);
+                    }
+                }
+            }
+        }
+        /* e_j against a finite maximum (what the other rows get is not
+         * used). Each block's four exponentials are completed in place
+         * before the next block's start (the empty asm statement): left to
+         * itself the scheduler interleaves the start of every block's expf
+         * with the end of others and spills. */
+        const float shift = finite ? m : 0.0F;
+
+#pragma unroll
+        for (int j = 0; j < (int)kLaneBlocks; ++j) {
+            v[j].x = m3_expf_with_table(v[j].x - shift, exp_table);
+            v[j].y = m3_expf_with_table(v[j].y - shift, exp_table);
+            v[j].z = m3_expf_with_table(v[j].z - shift, exp_table);
+            v[j].w = m3_expf_with_table(v[j].w - shift, exp_table);
+            asm volatile(""
+                         : "+v"(v[j].x), "+v"(v[j].y), "+v"(v[j].z),
+                           "+v"(v[j].w));
+        }
+        float sum = 0.0F;
+
+#pragma unroll
+        for (int j = 0; j < (int)kLaneBlocks; ++j) {
+            if (16U * j < length) {
+                sum = m3_block_sum(sum, v[j],
+                                   std::make_integer_sequence<int, 16>());
+            }
+        }
+        if (finite && present) {
+            const double inverse = 1.0 / (double)sum;
+
+#pragma unroll
+            for (int j = 0; j < (int)kLaneBlocks; ++j) {
+                if (FULL || j < (int)kLaneBlocks / 2 ||
+                    sub * 4U + 64U * j < width) {
+                    m3_stream_store((float4 *)(out + sub * 16U) + 16 * j,
+                                    m3_softmax_scale4(v[j], inverse));
+                }
+            }
+        }
+    }
+}
+
 /* The full 256-column left-to-right sum of an LDS line, continuing s, in
  * eight groups of 32 columns: each group's reads are issued before the
  * previous group's dependent additions, so 32 additions cover the LDS
@@ -1106,6 +1307,14 @@ void m3_launch_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                           args);
 }
 
+template <bool FULL>
+void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
+                         hipEvent_t stop, m3_softmax_args args)
+{
+    hipExtLaunchKernelGGL((m3_softmax_lane_rows_kernel<FULL>), grid,
+                          dim3(kThreads), 0, stream, start, stop, 0U, args);
+}
+
 template <bool F32IO, bool VEC>
 void m3_launch_stream(dim3 grid, hipStream_t stream, hipEvent_t start,
                       hipEvent_t stop, m3_softmax_args args)
@@ -1312,6 +1521,24 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
                                      (4U * in_size) ==
                                  0U;
             }
+        }
+        /* F32 rows of 513..1024 columns: the lane-row kernel (its 16-bit
+         * instances would spill, so other dtypes take the rows kernel). */
+        if (vec && f32 && width > kLaneRowWidth / 2U &&
+            width <= kLaneRowWidth) {
+            const uint64_t tasks = (rows + 3U) / 4U;
+            const uint64_t blocks = (tasks + kWaves - 1U) / kWaves;
+            const dim3 grid((uint32_t)(blocks < kMaxGrid ? blocks : kMaxGrid));
+            const m3_softmax_launcher launcher =
+                width == kLaneRowWidth ? &m3_launch_lane_rows<true>
+                                       : &m3_launch_lane_rows<false>;
+
+            return m3_hip_launch(
+                device, "m3_softmax_rows",
+                [&](hipEvent_t start, hipEvent_t stop) {
+                    launcher(grid, device->stream, start, stop, args);
+                },
+                message, capacity);
         }
         for (const m3_rows_variant &variant : m3_rows_variants) {
             if (width > kChunk * variant.vectors_per_lane) {

@@ -426,6 +426,46 @@ def test_softmax_strided_and_in_place(hip):
              ViewSpec(1, m3.F32, (4, 32, 1024))], "softmax rank 3")
 
 
+@pytest.mark.parametrize("width", [516, 768, 1000, 1020, 1024])
+@pytest.mark.parametrize("rows", [1, 2, 7, 258])
+def test_softmax_lane_rows(hip, width, rows):
+    """F32 rows of 513..1024 columns, four to a wave, one per 16 lanes:
+    partial last waves (rows not a multiple of 4), widths that end inside
+    a lane's block, and special rows (all -inf, +inf entries, all zero,
+    subnormal) at every position within a wave next to ordinary rows."""
+    rng = np.random.default_rng(19000 + width * 7 + rows)
+    logits = softmax_logits(rng, rows, width, specials=False)
+    special = [lambda r: r.fill(-np.inf),
+               lambda r: r.__setitem__(slice(None, None, 5), np.inf),
+               lambda r: r.fill(0.0),
+               lambda r: r.fill(np.float32(1e-40))]
+    for k in range(min(rows, 40)):
+        if k % 3 == 1:
+            special[(k // 3) % 4](logits[k])
+    if rows > 20:
+        logits[17, :] = -np.inf
+        logits[17, width - 1] = np.inf  # one +inf, last column
+        logits[18, :] = -np.inf
+        logits[18, width - 1] = 2.5  # a finite maximum in the last column
+    out = np.zeros(logits.nbytes, np.uint8)
+    compare(hip, m3.OP_SOFTMAX, [as_bytes(logits), out],
+            [ViewSpec(0, m3.F32, (rows, width)),
+             ViewSpec(1, m3.F32, (rows, width))],
+            "softmax lane rows w=%d rows=%d" % (width, rows))
+    if rows == 258:
+        # uneven row starts: outer axes (2, 129) read from (129, 2, width)
+        stack = logits.reshape(129, 2, width)
+        compare(hip, m3.OP_SOFTMAX, [as_bytes(stack), out],
+                [ViewSpec(0, m3.F32, (2, 129, width),
+                          (width * 4, 2 * width * 4, 4)),
+                 ViewSpec(1, m3.F32, (2, 129, width))],
+                "softmax lane rows uneven w=%d" % width)
+        compare(hip, m3.OP_SOFTMAX, [as_bytes(logits)],
+                [ViewSpec(0, m3.F32, (rows, width)),
+                 ViewSpec(0, m3.F32, (rows, width))],
+                "softmax lane rows in place w=%d" % width)
+
+
 # ---- snake1d -------------------------------------------------------------------
 
 @pytest.mark.parametrize("shape", [(2, 16, 1024), (1, 3, 5), (3, 7, 12),
