@@ -63,7 +63,6 @@ constexpr uint32_t kChunk = 256U;         /* columns per LDS chunk */
 constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
 constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
 constexpr uint32_t kStreamRows = 4U; /* rows per workgroup, streamed kernel */
-constexpr uint32_t kChainLanes = 16U; /* lanes of the streamed chains */
 
 /* Four F32 -inf: what a load past the end of a row reads instead. Never
  * written; not const, so that it is in the global address space like the
@@ -189,21 +188,31 @@ __device__ __forceinline__ float4 m3_widen4(uint32_t lo, uint32_t hi,
         m3_bits_f32(m3_load_as_f32_bits(hi >> 16U, dtype)));
 }
 
+/* A load that is nontemporal (data read once) or ordinary (data read
+ * again soon, which the caches may keep). */
+template <bool NT, typename T>
+__device__ __forceinline__ T m3_softmax_read(const T *p)
+{
+    if (NT) {
+        return __builtin_nontemporal_load(p);
+    }
+    return *p;
+}
+
 /* Four consecutive row elements starting at column c, as F32, from an
- * aligned row (16 bytes for F32, 8 for 16-bit dtypes). The rows are read
- * once, so the loads are nontemporal. */
-template <bool F32IO>
+ * aligned row (16 bytes for F32, 8 for 16-bit dtypes); nontemporal unless
+ * NT is false. */
+template <bool F32IO, bool NT = true>
 __device__ __forceinline__ float4 m3_softmax_load4(const uint8_t *row,
                                                    uint64_t c, uint32_t dtype)
 {
     if (F32IO || dtype == M3N_F32) {
         const m3_f32x4 w =
-            __builtin_nontemporal_load((const m3_f32x4 *)(row + c * 4U));
+            m3_softmax_read<NT>((const m3_f32x4 *)(row + c * 4U));
 
         return make_float4(w[0], w[1], w[2], w[3]);
     }
-    const m3_u32x2 h =
-        __builtin_nontemporal_load((const m3_u32x2 *)(row + c * 2U));
+    const m3_u32x2 h = m3_softmax_read<NT>((const m3_u32x2 *)(row + c * 2U));
 
     return m3_widen4(h[0], h[1], dtype);
 }
@@ -281,7 +290,7 @@ __device__ __forceinline__ void m3_softmax_store4_masked(
  * always valid (m3_minus_inf4, or the row's first columns) and the result
  * is replaced, so the compiler can wait for each load alone instead of
  * for every load in flight. */
-template <bool F32IO, bool VEC>
+template <bool F32IO, bool VEC, bool NT = true>
 __device__ __forceinline__ float4 m3_softmax_get4(const uint8_t *row,
                                                   uint32_t c, uint32_t width,
                                                   uint32_t dtype)
@@ -295,11 +304,12 @@ __device__ __forceinline__ float4 m3_softmax_get4(const uint8_t *row,
         const m3_f32x4 *source =
             inside ? (const m3_f32x4 *)(row + (uint64_t)c * 4U)
                    : (const m3_f32x4 *)&m3_minus_inf4;
-        const m3_f32x4 w = __builtin_nontemporal_load(source);
+        const m3_f32x4 w = m3_softmax_read<NT>(source);
 
         return make_float4(w[0], w[1], w[2], w[3]);
     }
-    const float4 x = m3_softmax_load4<F32IO>(row, inside ? c : 0U, dtype);
+    const float4 x =
+        m3_softmax_load4<F32IO, NT>(row, inside ? c : 0U, dtype);
 
     return inside ? x
                   : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
@@ -998,35 +1008,38 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
     }
 }
 
-/* The full 256-column left-to-right sum of an LDS line, continuing s, in
- * eight groups of 32 columns: each group's reads are issued before the
- * previous group's dependent additions, so 32 additions cover the LDS
- * latency. An empty asm statement that takes the running sum and clobbers
- * memory ends each group and keeps that shape; without it the compiler
- * hoists all 64 reads ahead of the chain (256 registers), and a loop
- * would copy the look-ahead registers each iteration. */
-__device__ __forceinline__ float m3_chunk_sum_full(float s, const float *line)
+/* Float4 slot, in a line of the streamed kernel's ring, of the chunk's
+ * float4 f = 4i + q (columns 16i + 4q .. +3): the summing lane i reads
+ * slots 4i..4i+3, rotated by (i >> 1) + (i >> 3) so that the 16-byte reads
+ * of the lanes that the LDS serves together fall on distinct banks. The
+ * producers write through the same map. */
+__device__ __forceinline__ uint32_t m3_ring_slot(uint32_t f)
 {
-    float4 group[2][8];
+    const uint32_t i = f >> 2U;
 
+    return (i << 2U) | (((f & 3U) + (i >> 1U) + (i >> 3U)) & 3U);
+}
+
+/* Continues the left-to-right sum over one 256-column chunk of a ring line.
+ * Lane i of each 16-lane DPP row holds columns 16i..16i+15 (e, in order),
+ * and the running sum passes from lane to lane: step g, the same four
+ * instructions in every lane, takes lane g - 1's sum (row_ror:1; lane 0
+ * takes lane 15's, the end of the previous chunk) and adds lane g's
+ * sixteen columns. Only lane g's result is the in-order sum after step g;
+ * after the chunk lane 15 holds it. One DPP addition per sixteen columns:
+ * a dependent DPP addition costs about three plain ones. */
+__device__ __forceinline__ float m3_pass_along_sum(float s, const float4 (&e)[4])
+{
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        group[0][i] = *(const float4 *)(line + 4 * i);
-    }
+    for (int g = 0; g < 16; ++g) {
+        s = m3_dpp_f32<0x121>(0.0F, s) + e[0].x;
+        s = s + e[0].y;
+        s = s + e[0].z;
+        s = s + e[0].w;
 #pragma unroll
-    for (int g = 0; g < 8; ++g) {
-        if (g + 1 < 8) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                group[(g + 1) & 1][i] =
-                    *(const float4 *)(line + 32 * (g + 1) + 4 * i);
-            }
+        for (int q = 1; q < 4; ++q) {
+            s = m3_add4(s, e[q]);
         }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            s = m3_add4(s, group[g & 1][i]);
-        }
-        asm volatile("" : "+v"(s) : : "memory");
     }
     return s;
 }
@@ -1055,14 +1068,15 @@ __device__ __forceinline__ float4 m3_exp4(float4 v, float m,
  * at columns 4l..4l+3 of a chunk:
  *   pass 1  wave w takes the chunks w, w+4, ...: maximum, +inf count and
  *           last column that is not -inf, combined through LDS;
- *   pass 2  the in-order sums. One wave runs the chains (every lane l
- *           continues the left-to-right sum of row l % R) while the other
- *           three produce the e_j of the next chunks into an LDS ring, one
- *           chunk each per step: the chain, a serial sum of width terms per
- *           row, is the critical path, and the exponentials run beside it
- *           on other SIMDs instead of in front of it;
+ *   pass 2  the in-order sums. One wave runs the chains (DPP row k of its
+ *           lanes sums row k, m3_pass_along_sum) while the other three
+ *           produce the e_j of the next chunks into an LDS ring, one chunk
+ *           each per step: the exponentials run beside the chains on other
+ *           SIMDs instead of in front of them;
  *   pass 3  wave w takes the chunks w, w+4, ... again: e_j (the same
  *           function of the same input), scaled, rounded and stored.
+ * The rows are read with ordinary loads, not nontemporal ones, so that the
+ * caches may serve a pass's reads of lines the previous pass fetched.
  * The sums stop after the last column holding something other than -inf
  * in a row with a finite maximum (later terms are +0). Rows past the end
  * of the tensor repeat the task's first row and store its values again.
@@ -1121,7 +1135,7 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
             for (int k = 0; k < R; ++k) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    x[k][h] = m3_softmax_get4<F32IO, VEC>(
+                    x[k][h] = m3_softmax_get4<F32IO, VEC, false>(
                         rows[k], (j + h * kWaves) * kChunk + lane * 4U, width,
                         in_dtype);
                 }
@@ -1195,7 +1209,7 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int k = 0; k < R; ++k) {
-                x[h][k] = m3_softmax_get4<F32IO, VEC>(
+                x[h][k] = m3_softmax_get4<F32IO, VEC, false>(
                     rows[k], (h * P + producer) * kChunk + lane * 4U, seen,
                     in_dtype);
             }
@@ -1211,13 +1225,14 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
                 for (int k = 0; k < R; ++k) {
                     const float4 v = (step & 1U) != 0U ? x[1][k] : x[0][k];
 
-                    *(float4 *)(slot + k * kLine + lane * 4U) = m3_keep4(
-                        m3_exp4(v, maximum[k], exp_table), finite[k]);
+                    *(float4 *)(slot + k * kLine + m3_ring_slot(lane) * 4U) =
+                        m3_keep4(m3_exp4(v, maximum[k], exp_table),
+                                 finite[k]);
                     __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int k = 0; k < R; ++k) {
-                    const float4 v = m3_softmax_get4<F32IO, VEC>(
+                    const float4 v = m3_softmax_get4<F32IO, VEC, false>(
                         rows[k], ahead * kChunk + lane * 4U, seen, in_dtype);
 
                     if ((step & 1U) != 0U) {
@@ -1226,25 +1241,33 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
                         x[0][k] = v;
                     }
                 }
-            } else if (step > 0U && lane < kChainLanes) {
-                /* consumer: the chunks of the previous step, in order, on
-                 * 16 lanes (R rows, each summed by 16 / R lanes): the LDS
-                 * reads of a full wave would take four times the LDS
-                 * bandwidth that the chains of a CU can use */
+            } else if (step > 0U) {
+                /* consumer: the chunks of the previous step, in order; the
+                 * 16 lanes of DPP row k sum row k, each reading its sixteen
+                 * columns of a chunk once */
                 const uint32_t first = (step - 1U) * P;
+                const uint32_t i = lane & 15U;
 
 #pragma unroll 1
-                for (uint32_t i = 0U; i < P && first + i < sum_chunks; ++i) {
-                    sum = m3_chunk_sum_full(
-                        sum, &ring[((step - 1U) & 1U) * P + i][0][0] +
-                                 (lane % (uint32_t)R) * kLine);
+                for (uint32_t c = 0U; c < P && first + c < sum_chunks; ++c) {
+                    const float *line =
+                        &ring[((step - 1U) & 1U) * P + c][lane >> 4U][0];
+                    float4 e[4];
+
+#pragma unroll
+                    for (uint32_t q = 0U; q < 4U; ++q) {
+                        e[q] = *(const float4 *)(line +
+                                                 m3_ring_slot(4U * i + q) * 4U);
+                    }
+                    sum = m3_pass_along_sum(sum, e);
                 }
             }
             __syncthreads();
         }
-        /* the sums reach the other waves through LDS */
-        if (wave == consumer && lane < (uint32_t)R) {
-            part_max[0][lane] = sum;
+        /* the sums (lane 15 of each DPP row) reach the other waves
+         * through LDS */
+        if (wave == consumer && (lane & 15U) == 15U) {
+            part_max[0][lane >> 4U] = sum;
         }
         __syncthreads();
         double inverse[R];
@@ -1262,7 +1285,7 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
 
 #pragma unroll
             for (int k = 0; k < R; ++k) {
-                x[k] = m3_softmax_get4<F32IO, VEC>(
+                x[k] = m3_softmax_get4<F32IO, VEC, false>(
                     rows[k], j * kChunk + lane * 4U, width, in_dtype);
             }
 #pragma unroll
