@@ -1127,16 +1127,25 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
             infinities[k] = 0U;
             last[k] = 0U;
         }
-        /* pass 1: two chunks per iteration keep 2R loads in flight */
+        /* pass 1, last chunk first (pass 2 then starts on the chunks read
+         * most recently, pass 3 ends there): two chunks per iteration keep
+         * 2R loads in flight; a chunk index past the row reads -inf */
         for (uint32_t j = wave; j < chunks; j += 2U * kWaves) {
             float4 x[R][2];
+            uint32_t chunk[2];
 
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t t = j + (uint32_t)h * kWaves;
+
+                chunk[h] = t < chunks ? chunks - 1U - t : chunks;
+            }
 #pragma unroll
             for (int k = 0; k < R; ++k) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     x[k][h] = m3_softmax_get4<F32IO, VEC, false>(
-                        rows[k], (j + h * kWaves) * kChunk + lane * 4U, width,
+                        rows[k], chunk[h] * kChunk + lane * 4U, width,
                         in_dtype);
                 }
             }
@@ -1151,8 +1160,7 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
                     infinities[k] += (e.x == INFINITY) + (e.y == INFINITY) +
                                      (e.z == INFINITY) + (e.w == INFINITY);
                     last[k] = t != -INFINITY
-                                  ? max(last[k], (j + h * kWaves) * 64U +
-                                                     lane + 1U)
+                                  ? max(last[k], chunk[h] * 64U + lane + 1U)
                                   : last[k];
                 }
             }
@@ -1279,8 +1287,9 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
             one_over_count[k] =
                 maximum[k] == INFINITY ? 1.0F / (float)infinities[k] : 0.0F;
         }
-        /* pass 3 */
-        for (uint32_t j = wave; j < chunks; j += kWaves) {
+        /* pass 3, last chunk first, where pass 2 ended */
+        for (uint32_t t = wave; t < chunks; t += kWaves) {
+            const uint32_t j = chunks - 1U - t;
             float4 x[R];
 
 #pragma unroll
