@@ -62,6 +62,7 @@ constexpr uint32_t kPad = 4U;
 constexpr uint32_t kChunk = 256U;         /* columns per LDS chunk */
 constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
 constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
+constexpr uint64_t kMaxLaneGrid = 0x7fffffffU; /* grid x limit */
 constexpr uint32_t kStreamRows = 4U; /* rows per workgroup, streamed kernel */
 
 /* Four F32 -inf: what a load past the end of a row reads instead. Never
@@ -901,13 +902,15 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
     const uint32_t width = a.width;
     const uint64_t out_pitch = (uint64_t)width * 4U;
     const uint64_t tasks = (a.rows + 3U) / 4U;
+    /* one task per wave: the grid covers them all (a loop over tasks took
+     * 30 more VGPRs and ran slower) */
+    const uint64_t task = (uint64_t)blockIdx.x * kWaves + wave;
 
     if (threadIdx.x < 32U) {
         exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
     }
     __syncthreads();
-    for (uint64_t task = (uint64_t)blockIdx.x * kWaves + wave; task < tasks;
-         task += (uint64_t)gridDim.x * kWaves) {
+    if (task < tasks) {
         const uint64_t row = task * 4U + (lane >> 4U);
         const bool present = row < a.rows;
         /* a row past the end of the tensor reads the task's first row */
@@ -1556,11 +1559,12 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
         }
         /* F32 rows of 513..1024 columns: the lane-row kernel (its 16-bit
          * instances would spill, so other dtypes take the rows kernel). */
+        const uint64_t lane_blocks =
+            (rows + 4U * kWaves - 1U) / (4U * kWaves);
+
         if (vec && f32 && width > kLaneRowWidth / 2U &&
-            width <= kLaneRowWidth) {
-            const uint64_t tasks = (rows + 3U) / 4U;
-            const uint64_t blocks = (tasks + kWaves - 1U) / kWaves;
-            const dim3 grid((uint32_t)(blocks < kMaxGrid ? blocks : kMaxGrid));
+            width <= kLaneRowWidth && lane_blocks <= kMaxLaneGrid) {
+            const dim3 grid((uint32_t)lane_blocks);
             const m3_softmax_launcher launcher =
                 width == kLaneRowWidth ? &m3_launch_lane_rows<true>
                                        : &m3_launch_lane_rows<false>;
