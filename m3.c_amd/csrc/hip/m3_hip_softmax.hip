@@ -22,10 +22,11 @@
  * have aligned starts and a width that is a multiple of 4 and move in 16-
  * or 8-byte accesses, other rows element by element; row starts may be
  * evenly spaced or follow several outer axes (m3_softmax_row):
- *   - F32 VEC rows of 513..1024 columns: four rows per wave, one per
- *     16-lane DPP row, the in-order sums carried in registers by additions
- *     whose addends are broadcast from lane to lane (row_newbcast), with no
- *     LDS traffic (m3_softmax_lane_rows_kernel).
+ *   - VEC rows of 513..1024 columns, and of 257..512 columns with 16-bit
+ *     input or output: four rows per wave, one per 16-lane DPP row, the
+ *     in-order sums carried in registers by additions whose addends are
+ *     broadcast from lane to lane (row_newbcast), with no LDS traffic
+ *     (m3_softmax_lane_rows_kernel).
  *   - other rows up to 2048 columns: wave-independent rows
  *     (m3_softmax_rows_kernel). A wave holds R rows in VGPRs, reduces max
  *     and k, forms e_j in place and streams 256-column chunks through a
@@ -871,27 +872,27 @@ __device__ __forceinline__ float m3_block_sum(float s, float4 e,
     return s;
 }
 
-constexpr uint32_t kLaneBlocks = 16U; /* float4 per lane, lane-row kernel */
-constexpr uint32_t kLaneRowWidth = 64U * kLaneBlocks;
-
-/* F32 rows of kLaneRowWidth / 2 + 1 .. kLaneRowWidth columns (aligned,
- * a multiple of 4 wide), with the in-order sum carried in registers. A
- * wave takes four consecutive rows, one per 16-lane DPP row (lanes
- * 16k..16k+15 hold row k); lane i of a row holds columns 4i + 64j ..
- * 4i + 64j + 3 (block j = 0..15), so each load instruction reads four runs
- * of 256 bytes. The maximum is reduced within the 16 lanes and e_j formed
- * in place; then the left-to-right sum is one dependent addition per
- * column, whose addend comes from the lane holding it (m3_add_from_lane),
- * and the four rows advance together. Against the rows kernel this
- * removes the LDS tile: there every lane group reads its row's e_j back
- * from LDS, at a bandwidth cost per CU that set the sum's pace. As there,
- * the sum stops after the wave's last float4 holding something other than
- * -inf (later terms are +0). Rows whose maximum is +-inf are written from
- * their inputs before the exponentials (zeros, or 1/k on their k +inf
- * entries) behind a wave-uniform test. FULL rows are exactly
- * kLaneRowWidth wide; otherwise blocks of the second half may lie past the
- * width, read four -inf from m3_minus_inf4 there and are not stored. */
-template <bool FULL>
+/* Rows of 32Q + 1 .. 64Q columns (VEC: aligned, a multiple of 4 wide),
+ * Q = 8 or 16, with the in-order sum carried in registers. A wave takes
+ * four consecutive rows, one per 16-lane DPP row (lanes 16k..16k+15 hold
+ * row k); lane i of a row holds columns 4i + 64j .. 4i + 64j + 3 (block
+ * j = 0..Q-1), so each load instruction reads four runs of 256 bytes (F32)
+ * or 128 bytes (16-bit). The maximum is reduced within the 16 lanes and
+ * e_j formed in place; then the left-to-right sum is one dependent
+ * addition per column, whose addend comes from the lane holding it
+ * (m3_add_from_lane), and the four rows advance together. Against the
+ * rows kernel this removes the LDS tile: there every lane group reads its
+ * row's e_j back from LDS, at a bandwidth cost per CU that set the sum's
+ * pace. As there, the sum stops after the wave's last float4 holding
+ * something other than -inf (later terms are +0). Rows whose maximum is
+ * +-inf are written from their inputs before the exponentials (zeros, or
+ * 1/k on their k +inf entries) behind a wave-uniform test. FULL rows are
+ * exactly 64Q wide; otherwise blocks of the second half may lie past the
+ * width, read -inf there and are not stored. F32IO: F32 in and out, with
+ * immediate-offset addressing; otherwise any float dtypes. One task per
+ * wave: the grid covers them all (a loop over tasks took 30 more VGPRs and
+ * ran slower). */
+template <int Q, bool FULL, bool F32IO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void m3_softmax_lane_rows_kernel(m3_softmax_args a)
 {
@@ -900,10 +901,11 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
     const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
     const uint32_t sub = lane & 15U;
     const uint32_t width = a.width;
-    const uint64_t out_pitch = (uint64_t)width * 4U;
+    const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
+    const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
+    const uint64_t out_pitch =
+        (uint64_t)width * (out_dtype == M3N_F32 ? 4U : 2U);
     const uint64_t tasks = (a.rows + 3U) / 4U;
-    /* one task per wave: the grid covers them all (a loop over tasks took
-     * 30 more VGPRs and ran slower) */
     const uint64_t task = (uint64_t)blockIdx.x * kWaves + wave;
 
     if (threadIdx.x < 32U) {
@@ -916,23 +918,33 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
         /* a row past the end of the tensor reads the task's first row */
         const uint8_t *in = m3_softmax_row(a, present ? row : task * 4U);
         uint8_t *out = a.output + row * out_pitch;
-        float4 v[kLaneBlocks];
+        float4 v[Q];
         float m = -INFINITY;
         uint32_t last = 0U; /* 1 + index of the last float4 not all -inf */
 
 #pragma unroll
-        for (int j = 0; j < (int)kLaneBlocks; ++j) {
-            const bool inside = FULL || j < (int)kLaneBlocks / 2 ||
-                                sub * 4U + 64U * j < width;
-            const m3_f32x4 *source =
-                inside ? (const m3_f32x4 *)(in + sub * 16U) + 16 * j
-                       : (const m3_f32x4 *)&m3_minus_inf4;
-            const m3_f32x4 w = __builtin_nontemporal_load(source);
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t c = sub * 4U + 64U * j;
+            const bool inside = FULL || j < Q / 2 || c < width;
 
-            v[j] = make_float4(w[0], w[1], w[2], w[3]);
+            if (F32IO) {
+                const m3_f32x4 *source =
+                    inside ? (const m3_f32x4 *)(in + sub * 16U) + 16 * j
+                           : (const m3_f32x4 *)&m3_minus_inf4;
+                const m3_f32x4 w = __builtin_nontemporal_load(source);
+
+                v[j] = make_float4(w[0], w[1], w[2], w[3]);
+            } else {
+                const float4 x =
+                    m3_softmax_load4<false>(in, inside ? c : 0U, in_dtype);
+
+                v[j] = inside ? x
+                              : make_float4(-INFINITY, -INFINITY, -INFINITY,
+                                            -INFINITY);
+            }
         }
 #pragma unroll
-        for (int j = 0; j < (int)kLaneBlocks; ++j) {
+        for (int j = 0; j < Q; ++j) {
             const float t = fmaxf(fmaxf(v[j].x, v[j].y),
                                   fmaxf(v[j].z, v[j].w));
 
@@ -942,12 +954,25 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
         m = m3_row16_max(m);
         const uint32_t length = m3_uniform_u32(m3_wave_max_u32(last));
         const bool finite = m != INFINITY && m != -INFINITY;
+        /* stores p at block j when the block is inside the row */
+        auto put = [&](int j, float4 p) {
+            const uint32_t c = sub * 4U + 64U * j;
+
+            if (!FULL && j >= Q / 2 && c >= width) {
+                return;
+            }
+            if (F32IO) {
+                m3_stream_store((float4 *)(out + sub * 16U) + 16 * j, p);
+            } else {
+                m3_softmax_store4<false>(out, c, out_dtype, p);
+            }
+        };
 
         if (M3_ANY_LANE(!finite)) {
             uint32_t count = 0U;
 
 #pragma unroll
-            for (int j = 0; j < (int)kLaneBlocks; ++j) {
+            for (int j = 0; j < Q; ++j) {
                 count += (v[j].x == INFINITY) + (v[j].y == INFINITY) +
                          (v[j].z == INFINITY) + (v[j].w == INFINITY);
             }
@@ -955,18 +980,14 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
 
             if (!finite && present) {
 #pragma unroll
-                for (int j = 0; j < (int)kLaneBlocks; ++j) {
+                for (int j = 0; j < Q; ++j) {
                     float4 p;
 
                     p.x = v[j].x == INFINITY ? one_over_count : 0.0F;
                     p.y = v[j].y == INFINITY ? one_over_count : 0.0F;
                     p.z = v[j].z == INFINITY ? one_over_count : 0.0F;
                     p.w = v[j].w == INFINITY ? one_over_count : 0.0F;
-                    if (FULL || j < (int)kLaneBlocks / 2 ||
-                        sub * 4U + 64U * j < width) {
-                        m3_stream_store((float4 *)(out + sub * 16U) + 16 * j,
-                                        p);
-                    }
+                    put(j, p);
                 }
             }
         }
@@ -978,7 +999,7 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
         const float shift = finite ? m : 0.0F;
 
 #pragma unroll
-        for (int j = 0; j < (int)kLaneBlocks; ++j) {
+        for (int j = 0; j < Q; ++j) {
             v[j].x = m3_expf_with_table(v[j].x - shift, exp_table);
             v[j].y = m3_expf_with_table(v[j].y - shift, exp_table);
             v[j].z = m3_expf_with_table(v[j].z - shift, exp_table);
@@ -990,7 +1011,7 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
         float sum = 0.0F;
 
 #pragma unroll
-        for (int j = 0; j < (int)kLaneBlocks; ++j) {
+        for (int j = 0; j < Q; ++j) {
             if (16U * j < length) {
                 sum = m3_block_sum(sum, v[j],
                                    std::make_integer_sequence<int, 16>());
@@ -1000,12 +1021,8 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
             const double inverse = 1.0 / (double)sum;
 
 #pragma unroll
-            for (int j = 0; j < (int)kLaneBlocks; ++j) {
-                if (FULL || j < (int)kLaneBlocks / 2 ||
-                    sub * 4U + 64U * j < width) {
-                    m3_stream_store((float4 *)(out + sub * 16U) + 16 * j,
-                                    m3_softmax_scale4(v[j], inverse));
-                }
+            for (int j = 0; j < Q; ++j) {
+                put(j, m3_softmax_scale4(v[j], inverse));
             }
         }
     }
@@ -1342,11 +1359,11 @@ void m3_launch_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                           args);
 }
 
-template <bool FULL>
+template <int Q, bool FULL, bool F32IO>
 void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                          hipEvent_t stop, m3_softmax_args args)
 {
-    hipExtLaunchKernelGGL((m3_softmax_lane_rows_kernel<FULL>), grid,
+    hipExtLaunchKernelGGL((m3_softmax_lane_rows_kernel<Q, FULL, F32IO>), grid,
                           dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
@@ -1557,17 +1574,34 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
                                  0U;
             }
         }
-        /* F32 rows of 513..1024 columns: the lane-row kernel (its 16-bit
-         * instances would spill, so other dtypes take the rows kernel). */
+        /* VEC rows of 513..1024 columns, and of 257..512 columns with a
+         * 16-bit input or output: the lane-row kernel, 16 or 8 float4 per
+         * lane (index: [wide][full][f32]). F32 rows of 257..512 columns
+         * measured the same or faster on the rows kernel (49.5 against
+         * 49.6 us for [65536,512], 23.4 against 22.2 us for [32768,300]);
+         * with 16-bit I/O the lane-row kernel is faster at every width
+         * (56.6 against 73.3 us for [65536,512] BF16, 38.5 against 58.1 us
+         * for [16384,1024] BF16). */
+        static const m3_softmax_launcher lane_launchers[2][2][2] = {
+            {{&m3_launch_lane_rows<8, false, false>,
+              &m3_launch_lane_rows<8, false, true>},
+             {&m3_launch_lane_rows<8, true, false>,
+              &m3_launch_lane_rows<8, true, true>}},
+            {{&m3_launch_lane_rows<16, false, false>,
+              &m3_launch_lane_rows<16, false, true>},
+             {&m3_launch_lane_rows<16, true, false>,
+              &m3_launch_lane_rows<16, true, true>}}};
         const uint64_t lane_blocks =
             (rows + 4U * kWaves - 1U) / (4U * kWaves);
+        const uint32_t lane_q = width > 1024U           ? 0U
+                                : width > 512U          ? 16U
+                                : width > 256U && !f32 ? 8U
+                                                        : 0U;
 
-        if (vec && f32 && width > kLaneRowWidth / 2U &&
-            width <= kLaneRowWidth && lane_blocks <= kMaxLaneGrid) {
+        if (vec && lane_q != 0U && lane_blocks <= kMaxLaneGrid) {
             const dim3 grid((uint32_t)lane_blocks);
             const m3_softmax_launcher launcher =
-                width == kLaneRowWidth ? &m3_launch_lane_rows<true>
-                                       : &m3_launch_lane_rows<false>;
+                lane_launchers[lane_q == 16U][width == 64U * lane_q][f32];
 
             return m3_hip_launch(
                 device, "m3_softmax_rows",

@@ -426,14 +426,9 @@ def test_softmax_strided_and_in_place(hip):
              ViewSpec(1, m3.F32, (4, 32, 1024))], "softmax rank 3")
 
 
-@pytest.mark.parametrize("width", [516, 768, 1000, 1020, 1024])
-@pytest.mark.parametrize("rows", [1, 2, 7, 258])
-def test_softmax_lane_rows(hip, width, rows):
-    """F32 rows of 513..1024 columns, four to a wave, one per 16 lanes:
-    partial last waves (rows not a multiple of 4), widths that end inside
-    a lane's block, and special rows (all -inf, +inf entries, all zero,
-    subnormal) at every position within a wave next to ordinary rows."""
-    rng = np.random.default_rng(19000 + width * 7 + rows)
+def lane_row_logits(rng, rows, width):
+    """Causal logits with special rows (all -inf, +inf entries, all zero,
+    subnormal) at every position within a wave of four rows."""
     logits = softmax_logits(rng, rows, width, specials=False)
     special = [lambda r: r.fill(-np.inf),
                lambda r: r.__setitem__(slice(None, None, 5), np.inf),
@@ -447,6 +442,18 @@ def test_softmax_lane_rows(hip, width, rows):
         logits[17, width - 1] = np.inf  # one +inf, last column
         logits[18, :] = -np.inf
         logits[18, width - 1] = 2.5  # a finite maximum in the last column
+    return logits
+
+
+@pytest.mark.parametrize("width", [516, 768, 1000, 1020, 1024])
+@pytest.mark.parametrize("rows", [1, 2, 7, 258])
+def test_softmax_lane_rows(hip, width, rows):
+    """F32 rows of 513..1024 columns, four to a wave, one per 16 lanes:
+    partial last waves (rows not a multiple of 4), widths that end inside
+    a lane's block, and special rows at every position within a wave next
+    to ordinary rows."""
+    rng = np.random.default_rng(19000 + width * 7 + rows)
+    logits = lane_row_logits(rng, rows, width)
     out = np.zeros(logits.nbytes, np.uint8)
     compare(hip, m3.OP_SOFTMAX, [as_bytes(logits), out],
             [ViewSpec(0, m3.F32, (rows, width)),
@@ -464,6 +471,25 @@ def test_softmax_lane_rows(hip, width, rows):
                 [ViewSpec(0, m3.F32, (rows, width)),
                  ViewSpec(0, m3.F32, (rows, width))],
                 "softmax lane rows in place w=%d" % width)
+
+
+@pytest.mark.parametrize("dtypes", [(m3.F16, m3.F16), (m3.BF16, m3.F32),
+                                    (m3.F32, m3.BF16)])
+@pytest.mark.parametrize("width", [260, 300, 508, 512, 700, 1020, 1024])
+@pytest.mark.parametrize("rows", [7, 258])
+def test_softmax_lane_rows_dtypes(hip, dtypes, width, rows):
+    """The lane-row kernel with 16-bit input or output, 8 float4 per lane
+    (257..512 columns) and 16 (513..1024)."""
+    rng = np.random.default_rng(21000 + width * 7 + rows + 3 * dtypes[0] +
+                                dtypes[1])
+    logits = lane_row_logits(rng, rows, width)
+    out_size = 4 if dtypes[1] == m3.F32 else 2
+    compare(hip, m3.OP_SOFTMAX,
+            [softmax_source(logits, dtypes[0]),
+             np.zeros(rows * width * out_size, np.uint8)],
+            [ViewSpec(0, dtypes[0], (rows, width)),
+             ViewSpec(1, dtypes[1], (rows, width))],
+            "softmax lane rows %s w=%d rows=%d" % (dtypes, width, rows))
 
 
 # ---- snake1d -------------------------------------------------------------------
