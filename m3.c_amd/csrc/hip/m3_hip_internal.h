@@ -42,6 +42,10 @@ struct m3_hip_device {
     uint64_t total_bytes;
     uint32_t compute_units;
     uint32_t lds_per_block; /* bytes of LDS one workgroup may use */
+    uint32_t wall_clock_khz; /* rate of s_memrealtime; 0 if unknown */
+    /* M3_HIP_SOFTMAX_LATE_US at open (negative when unset): when a wave of
+     * the lane-row softmax counts as late (m3_hip_softmax.hip) */
+    float softmax_late_us;
     /* device flags for data scans (a view's word holds the epoch of the
      * last scan that found an offending element in it), the epoch of the
      * next scan, and the flags' host mirror in coherent pinned memory */

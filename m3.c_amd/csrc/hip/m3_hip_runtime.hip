@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -262,6 +263,19 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
     device->total_bytes = (uint64_t)properties.totalGlobalMem;
     device->compute_units = (uint32_t)properties.multiProcessorCount;
     device->lds_per_block = (uint32_t)properties.sharedMemPerBlock;
+    {
+        int rate = 0;
+        const char *late = std::getenv("M3_HIP_SOFTMAX_LATE_US");
+
+        device->wall_clock_khz =
+            hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate,
+                                  ordinal) == hipSuccess && rate > 0
+                ? (uint32_t)rate
+                : 0U;
+        device->softmax_late_us =
+            late != nullptr && late[0] != '\0' ? std::strtof(late, nullptr)
+                                                : -1.0F;
+    }
     code = m3_hip_check(hipStreamCreateWithFlags(&device->stream,
                                                  hipStreamNonBlocking),
                         "hipStreamCreateWithFlags", message, capacity);

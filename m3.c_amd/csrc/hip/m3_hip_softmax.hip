@@ -48,6 +48,7 @@
 #include "m3_hip_internal.h"
 #include "m3_libm.h"
 
+#include <algorithm>
 #include <cstring>
 #include <utility>
 
@@ -64,6 +65,9 @@ constexpr uint32_t kChunk = 256U;         /* columns per LDS chunk */
 constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
 constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
 constexpr uint64_t kMaxLaneGrid = 0x7fffffffU; /* grid x limit */
+constexpr double kHbmBytesPerUs = 8.0e6; /* MI355X peak, 8 TB/s */
+constexpr double kLateFactor = 1.2;
+constexpr double kLateFloorUs = 3.0;
 constexpr uint32_t kStreamRows = 4U; /* rows per workgroup, streamed kernel */
 
 /* Four F32 -inf: what a load past the end of a row reads instead. Never
@@ -81,6 +85,9 @@ struct m3_softmax_args {
     uint32_t in_dtype;
     uint32_t out_dtype;
     uint32_t tile_rows;
+    /* lane-row kernel: s_memrealtime ticks after its start past which a
+     * wave still waiting for its rows counts as late */
+    uint32_t late_ticks;
     /* Rows whose starts are not evenly spaced (outer_rank > 1): row r
      * starts at input + sum over axes of coordinate(r, axis) * stride. */
     uint32_t outer_rank;
@@ -872,6 +879,25 @@ __device__ __forceinline__ float m3_block_sum(float s, float4 e,
     return s;
 }
 
+/* The same sum with the running value passed from lane to lane: step g,
+ * the same four instructions in every lane, takes lane g - 1's sum
+ * (row_ror:1; lane 0 takes lane 15's, the end of the previous block) and
+ * adds lane g's four columns, so that lane g holds the in-order sum after
+ * step g and lane 15 after the block. A dependent DPP addition takes about
+ * 12 cycles and a plain one 4: 6 cycles per column against 12 for
+ * m3_block_sum, whose DPP operand is the addend, not the sum. */
+__device__ __forceinline__ float m3_block_sum_passed(float s, float4 e)
+{
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+        s = m3_dpp_f32<0x121>(0.0F, s) + e.x;
+        s = s + e.y;
+        s = s + e.z;
+        s = s + e.w;
+    }
+    return s;
+}
+
 /* Rows of 32Q + 1 .. 64Q columns (VEC: aligned, a multiple of 4 wide),
  * Q = 8 or 16, with the in-order sum carried in registers. A wave takes
  * four consecutive rows, one per 16-lane DPP row (lanes 16k..16k+15 hold
@@ -891,7 +917,15 @@ __device__ __forceinline__ float m3_block_sum(float s, float4 e,
  * width, read -inf there and are not stored. F32IO: F32 in and out, with
  * immediate-offset addressing; otherwise any float dtypes. One task per
  * wave: the grid covers them all (a loop over tasks took 30 more VGPRs and
- * ran slower). */
+ * ran slower).
+ *
+ * All waves issue their loads at once, and the waves whose rows the HBM
+ * serves last decide when the kernel ends: by then most SIMDs are idle and
+ * the sum's latency is what counts. A wave whose rows arrive more than
+ * a.late_ticks after its start (s_memrealtime) therefore sums with
+ * m3_block_sum_passed, half the latency per column; the others keep
+ * m3_block_sum, which leaves more issue slots to the waves sharing their
+ * SIMD. Both perform the same additions in the same order. */
 template <int Q, bool FULL, bool F32IO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void m3_softmax_lane_rows_kernel(m3_softmax_args a)
@@ -907,6 +941,7 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
         (uint64_t)width * (out_dtype == M3N_F32 ? 4U : 2U);
     const uint64_t tasks = (a.rows + 3U) / 4U;
     const uint64_t task = (uint64_t)blockIdx.x * kWaves + wave;
+    const uint64_t start = __builtin_amdgcn_s_memrealtime();
 
     if (threadIdx.x < 32U) {
         exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
@@ -954,6 +989,11 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
         m = m3_row16_max(m);
         const uint32_t length = m3_uniform_u32(m3_wave_max_u32(last));
         const bool finite = m != INFINITY && m != -INFINITY;
+        /* every load has returned here (all were reduced); the wait makes
+         * the clock read follow them */
+        __builtin_amdgcn_s_waitcnt(0);
+        const bool late =
+            __builtin_amdgcn_s_memrealtime() - start > (uint64_t)a.late_ticks;
         /* stores p at block j when the block is inside the row */
         auto put = [&](int j, float4 p) {
             const uint32_t c = sub * 4U + 64U * j;
@@ -1010,11 +1050,21 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
         }
         float sum = 0.0F;
 
+        if (late) {
 #pragma unroll
-        for (int j = 0; j < Q; ++j) {
-            if (16U * j < length) {
-                sum = m3_block_sum(sum, v[j],
-                                   std::make_integer_sequence<int, 16>());
+            for (int j = 0; j < Q; ++j) {
+                if (16U * j < length) {
+                    sum = m3_block_sum_passed(sum, v[j]);
+                }
+            }
+            sum = m3_dpp_f32<0x15F>(0.0F, sum); /* lane 15's, to the row */
+        } else {
+#pragma unroll
+            for (int j = 0; j < Q; ++j) {
+                if (16U * j < length) {
+                    sum = m3_block_sum(sum, v[j],
+                                       std::make_integer_sequence<int, 16>());
+                }
             }
         }
         if (finite && present) {
@@ -1600,6 +1650,20 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
 
         if (vec && lane_q != 0U && lane_blocks <= kMaxLaneGrid) {
             const dim3 grid((uint32_t)lane_blocks);
+            /* late: 1.2 times the launch's reads at peak HBM bandwidth, at
+             * least 3 us (about the latency of a first load), unless
+             * M3_HIP_SOFTMAX_LATE_US sets it */
+            const double late_us =
+                device->softmax_late_us >= 0.0F
+                    ? (double)device->softmax_late_us
+                    : std::max(kLateFloorUs,
+                               kLateFactor * (double)rows * (double)width *
+                                   in_size / kHbmBytesPerUs);
+            const double ticks = late_us * device->wall_clock_khz / 1000.0;
+
+            args.late_ticks = device->wall_clock_khz == 0U || ticks >= 4.0e9
+                                  ? 0xffffffffU
+                                  : (uint32_t)ticks;
             const m3_softmax_launcher launcher =
                 lane_launchers[lane_q == 16U][width == 64U * lane_q][f32];
 

@@ -6,6 +6,7 @@ broadcast classes, strided general paths, 16-bit dtypes, aliasing). The
 bar is bit-exact output and equal status for every case, including NaN
 payloads, infinities, signed zeros and subnormals in the inputs.
 """
+import os
 import sys
 
 import numpy as np
@@ -490,6 +491,46 @@ def test_softmax_lane_rows_dtypes(hip, dtypes, width, rows):
             [ViewSpec(0, dtypes[0], (rows, width)),
              ViewSpec(1, dtypes[1], (rows, width))],
             "softmax lane rows %s w=%d rows=%d" % (dtypes, width, rows))
+
+
+@pytest.fixture(scope="module")
+def hip_late(gpu):
+    """A HIP backend on which every wave of the lane-row softmax counts as
+    late (M3_HIP_SOFTMAX_LATE_US=0, read when the device opens), so every
+    sum runs the lane-to-lane form."""
+    saved = os.environ.get("M3_HIP_SOFTMAX_LATE_US")
+    os.environ["M3_HIP_SOFTMAX_LATE_US"] = "0"
+    try:
+        fixture = HipFixture()
+    finally:
+        if saved is None:
+            del os.environ["M3_HIP_SOFTMAX_LATE_US"]
+        else:
+            os.environ["M3_HIP_SOFTMAX_LATE_US"] = saved
+    yield fixture
+    fixture.close()
+
+
+@pytest.mark.parametrize("dtypes", [(m3.F32, m3.F32), (m3.F16, m3.F16),
+                                    (m3.BF16, m3.F32)])
+@pytest.mark.parametrize("width", [300, 516, 1000, 1024])
+@pytest.mark.parametrize("rows", [7, 258])
+def test_softmax_lane_rows_late_path(hip_late, dtypes, width, rows):
+    """The lane-row kernel with every sum passed from lane to lane, the
+    form that waves whose rows arrive late take: the same bits."""
+    if dtypes == (m3.F32, m3.F32) and width <= 512:
+        width += 512  # F32 rows of 257..512 columns take the rows kernel
+    rng = np.random.default_rng(23000 + width * 7 + rows + 3 * dtypes[0] +
+                                dtypes[1])
+    logits = lane_row_logits(rng, rows, width)
+    out_size = 4 if dtypes[1] == m3.F32 else 2
+    compare(hip_late, m3.OP_SOFTMAX,
+            [softmax_source(logits, dtypes[0]),
+             np.zeros(rows * width * out_size, np.uint8)],
+            [ViewSpec(0, dtypes[0], (rows, width)),
+             ViewSpec(1, dtypes[1], (rows, width))],
+            "softmax lane rows, late path %s w=%d rows=%d" % (dtypes, width,
+                                                             rows))
 
 
 # ---- snake1d -------------------------------------------------------------------
