@@ -94,6 +94,12 @@ m3_program_load(const unsigned int *operands, unsigned int index,
             at;
 
         if (FULL) {
+            /* an array operand is read once per launch; a broadcast one
+             * (period) is read again and stays in the caches */
+            if (period == 0ULL) {
+                return __builtin_nontemporal_load(
+                    (const m3_program_global_f32x4 *)p);
+            }
             return *(const m3_program_global_f32x4 *)p;
         }
         v.x = p[0];
@@ -115,7 +121,10 @@ m3_program_load(const unsigned int *operands, unsigned int index,
     unsigned int h[4] = {0U, 0U, 0U, 0U};
 
     if (FULL) {
-        const m3_program_u32x2 w = *(const m3_program_global_u32x2 *)p;
+        const m3_program_u32x2 w =
+            period == 0ULL
+                ? __builtin_nontemporal_load((const m3_program_global_u32x2 *)p)
+                : *(const m3_program_global_u32x2 *)p;
 
         h[0] = w.x & 0xffffU;
         h[1] = w.x >> 16U;
