@@ -166,6 +166,13 @@ __device__ __forceinline__ uint2 m3_stream_load(const uint2 *p)
     return make_uint2(w.x, w.y);
 }
 
+__device__ __forceinline__ float4 m3_stream_load(const float4 *p)
+{
+    m3_f32x4 w = __builtin_nontemporal_load((const m3_f32x4 *)p);
+
+    return make_float4(w.x, w.y, w.z, w.w);
+}
+
 /* Unsigned 32-bit division by an invariant divisor d >= 1:
  * q = (umulhi(n, mul) + n) >> shift with shift = ceil(log2 d) and
  * mul = floor(2^32 (2^shift - d) / d) + 1; the sum is formed in 64 bits,

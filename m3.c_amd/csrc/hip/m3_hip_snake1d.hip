@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void m3_snake1d_vec_kernel(
 
 #pragma unroll
             for (uint32_t u = 0U; u < kUnroll; ++u) {
-                x[u] = a.input[first + u * kThreads];
+                x[u] = m3_stream_load(&a.input[first + u * kThreads]);
             }
             const float inverse = m3_snake_inverse(alpha);
 
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void m3_snake1d_vec_kernel(
                 uint32_t channel =
                     q - m3_fast_div_q(a.channels, q) * a.channels.divisor;
 
-                x[u] = a.input[g];
+                x[u] = m3_stream_load(&a.input[g]);
                 alpha[u] = *(const float *)(a.alpha +
                                             (int64_t)channel * a.alpha_stride);
             }
