@@ -66,7 +66,7 @@ constexpr uint32_t kLine = kChunk + kPad; /* LDS floats per chunk row */
 constexpr uint64_t kMaxGrid = 1U << 20;   /* workgroups; waves loop beyond */
 constexpr uint64_t kMaxLaneGrid = 0x7fffffffU; /* grid x limit */
 constexpr double kHbmBytesPerUs = 8.0e6; /* MI355X peak, 8 TB/s */
-constexpr double kLateFactor = 1.2;
+constexpr double kLateFactor = 0.85;
 constexpr double kLateFloorUs = 3.0;
 constexpr uint32_t kStreamRows = 4U; /* rows per workgroup, streamed kernel */
 
@@ -1650,8 +1650,9 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
 
         if (vec && lane_q != 0U && lane_blocks <= kMaxLaneGrid) {
             const dim3 grid((uint32_t)lane_blocks);
-            /* late: 1.2 times the launch's reads at peak HBM bandwidth, at
-             * least 3 us (about the latency of a first load), unless
+            /* late: 0.85 times the time the launch's reads take at peak
+             * HBM bandwidth (7.1 us for [16,1024,1024] F32), at least 3 us
+             * (about the latency of a first load), unless
              * M3_HIP_SOFTMAX_LATE_US sets it */
             const double late_us =
                 device->softmax_late_us >= 0.0F
