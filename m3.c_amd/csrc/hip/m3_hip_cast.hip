@@ -23,8 +23,15 @@ namespace {
 
 constexpr uint32_t kThreads = 256U;
 constexpr uint32_t kUnroll = 2U; /* groups in flight per lane, copies */
-/* groups in flight per lane of a conversion */
-constexpr uint32_t kCastUnroll = 2U;
+/* Groups in flight per lane of a conversion: 4 when it narrows (4-byte to
+ * 16-bit elements), 2 otherwise. Against 2, in bench.py alternating
+ * libraries on one box: F32 -> F16 17.4-17.5 against 17.6-17.8 us and
+ * F32 -> BF16 16.9-17.0 against 17.0-17.1 us; the widening casts measured
+ * the same or slower with 1 or 4. */
+constexpr uint32_t m3_cast_unroll(uint32_t in_size, uint32_t out_size)
+{
+    return in_size > out_size ? 4U : 2U;
+}
 /* workgroups per CU of a conversion: up to 32, so that a 16M-element
  * cast runs each lane's groups in one pass instead of a grid-stride loop
  * (measured 2% faster for F16 -> F32 than 16 per CU) */
@@ -80,15 +87,16 @@ __global__ __launch_bounds__(256) void m3_cast_vec_kernel(
     using out_io = m3_vec_io<m3_size_of(OUT)>;
     const typename in_io::type *in = (const typename in_io::type *)input;
     typename out_io::type *out = (typename out_io::type *)output;
-    const uint64_t step = (uint64_t)gridDim.x * kThreads * kCastUnroll;
+    constexpr uint32_t unroll = m3_cast_unroll(m3_size_of(IN), m3_size_of(OUT));
+    const uint64_t step = (uint64_t)gridDim.x * kThreads * unroll;
 
-    for (uint64_t first = (uint64_t)blockIdx.x * kThreads * kCastUnroll +
+    for (uint64_t first = (uint64_t)blockIdx.x * kThreads * unroll +
                           threadIdx.x;
          first < groups; first += step) {
-        uint4 v[kCastUnroll];
+        uint4 v[unroll];
 
 #pragma unroll
-        for (uint32_t u = 0U; u < kCastUnroll; ++u) {
+        for (uint32_t u = 0U; u < unroll; ++u) {
             uint64_t g = first + u * kThreads;
 
             if (g < groups) {
@@ -96,7 +104,7 @@ __global__ __launch_bounds__(256) void m3_cast_vec_kernel(
             }
         }
 #pragma unroll
-        for (uint32_t u = 0U; u < kCastUnroll; ++u) {
+        for (uint32_t u = 0U; u < unroll; ++u) {
             uint64_t g = first + u * kThreads;
 
             if (g < groups) {
@@ -300,7 +308,9 @@ int m3_launch_unary(m3_hip_device *device, const m3_hip_view *input,
             uint64_t groups = count / 4U;
             uint32_t blocks = m3_grid_blocks(device,
                                              groups == 0U ? 1U : groups,
-                                             kThreads * kCastUnroll,
+                                             kThreads * m3_cast_unroll(
+                                                 in_align / 4U,
+                                                 out_align / 4U),
                                              kCastBlocksPerCu);
 
             return m3_hip_launch(
