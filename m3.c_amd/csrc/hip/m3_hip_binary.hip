@@ -116,15 +116,15 @@ __device__ __forceinline__ uint4 m3_operand_load4(const m3_bin_operand &o,
                              : f - m3_fast_div_q(o.period, f) *
                                        o.period.divisor;
 
-        /* a full F32 operand is read once per launch with 16-byte
-         * accesses: streamed; a trailing broadcast operand is reread by
-         * every row: cached (8-byte streaming loads measured slower) */
+        /* a full operand is read once per launch: streamed; a trailing
+         * broadcast operand is reread by every row: cached */
         if (dtype == M3N_F32) {
             const uint4 *p = (const uint4 *)(o.base + (uint64_t)index * 4U);
 
             return o.mode == M3_BIN_FULL ? m3_stream_load(p) : *p;
         }
-        uint2 half = *(const uint2 *)(o.base + (uint64_t)index * 2U);
+        const uint2 *h = (const uint2 *)(o.base + (uint64_t)index * 2U);
+        const uint2 half = o.mode == M3_BIN_FULL ? m3_stream_load(h) : *h;
 
         return make_uint4(m3_load_as_f32_bits(half.x & 0xffffU, dtype),
                           m3_load_as_f32_bits(half.x >> 16U, dtype),

@@ -50,12 +50,14 @@ struct m3_vec_io<4U> {
     __device__ static type pack(uint4 v) { return v; }
 };
 
-/* Four 2-byte elements: one 8-byte access, read with an ordinary load
- * (8-byte streaming loads measured slower on gfx950). */
+/* Four 2-byte elements: one 8-byte access, read with a streaming load
+ * (F16 -> F32 17.8-18.0 against 18.3-18.5 us with an ordinary one, BF16 ->
+ * F32 17.8-18.0 against 18.3-18.5 us; bench.py alternating libraries on
+ * one box). */
 template <>
 struct m3_vec_io<2U> {
     using type = uint2;
-    __device__ static type load(const type *p) { return *p; }
+    __device__ static type load(const type *p) { return m3_stream_load(p); }
     __device__ static uint4 unpack(type v)
     {
         return make_uint4(v.x & 0xffffU, v.x >> 16U, v.y & 0xffffU,
