@@ -4,9 +4,13 @@
  *
  * Storage. With the GPU provider allowed (allow_metal, or the neural
  * engine option, which here means "any provider") the storage is the HIP
- * device's; a missing device is an error (UNSUPPORTED), never a silent
- * move to the CPU. With only the CPU provider allowed the storage is host
- * memory (m3_host_backend.c).
+ * device's. When the HIP backend cannot be made because there is no usable
+ * device (its constructor says UNSUPPORTED) and the CPU provider is
+ * allowed, the storage is host memory (m3_host_backend.c) and every list
+ * runs on the CPU provider, as the reference falls back from Metal
+ * (src/m3_provider.c:46-58); any other failure of the constructor is
+ * returned as it is. With only the CPU provider allowed the storage is
+ * host memory.
  *
  * Lists. A list goes to the GPU provider when the GPU is allowed, the
  * storage is the device's and the GPU takes every kind in it; otherwise to
@@ -19,9 +23,9 @@
  * reads it once, when it is created.
  *
  * This is the reference's scheduling (src/m3_provider.c:35-129) with HIP
- * in the place of Metal. It differs where the reference would use its
- * CPU provider because the GPU is missing, or for kinds outside this
- * library: here both are UNSUPPORTED.
+ * in the place of Metal. It differs for kinds outside this library, which
+ * the reference's CPU provider would run: here such a list is
+ * UNSUPPORTED.
  *
  * m3_provider_set_gpu_factory replaces the GPU backend's constructor;
  * tests use it to compile sessions against a recording backend on
@@ -100,7 +104,15 @@ m3_status m3_backend_create_preferred(bool allow_gpu, bool allow_cpu,
     }
     status = m3_gpu_factory != NULL ? m3_gpu_factory(backend, error)
                                     : m3_backend_create_hip(backend, error);
-    if (status == M3_STATUS_UNSUPPORTED) {
+    if (status != M3_STATUS_UNSUPPORTED) {
+        return status;
+    }
+    *backend = NULL;
+    if (allow_cpu) {
+        /* No usable device: host storage and the CPU provider. */
+        return m3_backend_create_host(backend, error);
+    }
+    {
         char cause[M3_ERROR_MESSAGE_CAPACITY] = "";
 
         if (error != NULL) {
@@ -108,12 +120,9 @@ m3_status m3_backend_create_preferred(bool allow_gpu, bool allow_cpu,
             cause[sizeof(cause) - 1U] = '\0';
         }
         return m3_error_set(error, M3_STATUS_UNSUPPORTED,
-                            "no HIP device: %s%s", cause,
-                            allow_cpu ? " (allow_metal = false selects the "
-                                        "CPU provider)"
-                                      : "");
+                            "no HIP device and the CPU provider is not "
+                            "allowed: %s", cause);
     }
-    return status;
 }
 
 m3_status m3_provider_select_regular(const m3_backend *storage_backend,

@@ -42,6 +42,9 @@ static int g_decreasing;
  * (write/read hooks, which copy and count): the session then runs CPU
  * provider nodes on host mirrors, as it does over HIP memory. */
 static int g_device_memory;
+/* When nonzero, the constructor makes nothing and returns this status, as
+ * a GPU backend does on a machine without a usable device. */
+static int g_create_status;
 static size_t g_host_to_device;
 static size_t g_device_to_host;
 
@@ -54,6 +57,7 @@ size_t oracle_backend_programs(void);
 size_t oracle_backend_periodic(void);
 void oracle_backend_set_program_order(int decreasing);
 void oracle_backend_set_device_memory(int on);
+void oracle_backend_set_create_status(int status);
 size_t oracle_backend_transfers(int to_device);
 m3_status oracle_backend_create(m3_backend **backend, m3_error *error);
 
@@ -68,6 +72,12 @@ void oracle_backend_reset(void)
     g_periodic = 0U;
     g_host_to_device = 0U;
     g_device_to_host = 0U;
+    g_create_status = 0;
+}
+
+void oracle_backend_set_create_status(int status)
+{
+    g_create_status = status;
 }
 
 void oracle_backend_set_program_order(int decreasing)
@@ -477,9 +487,15 @@ m3_status oracle_backend_create(m3_backend **backend, m3_error *error)
     const m3_backend_vtable *chosen =
         g_device_memory ? &device_vtable : &host_vtable;
     m3_backend_info info;
-    oracle_backend_context *context = calloc(1U, sizeof(*context));
+    oracle_backend_context *context;
     m3_status status;
 
+    if (g_create_status != 0) {
+        return m3_error_set(error, (m3_status)g_create_status,
+                            "test backend: made to fail with status %d",
+                            g_create_status);
+    }
+    context = calloc(1U, sizeof(*context));
     if (context == NULL) {
         return m3_error_set(error, M3_STATUS_OUT_OF_MEMORY, "no memory");
     }

@@ -54,6 +54,7 @@ def backend_lib():
     fake.oracle_backend_programs.restype = ctypes.c_size_t
     fake.oracle_backend_periodic.restype = ctypes.c_size_t
     fake.oracle_backend_set_program_order.argtypes = [ctypes.c_int]
+    fake.oracle_backend_set_create_status.argtypes = [ctypes.c_int]
     factory = ctypes.cast(fake.oracle_backend_create, ctypes.c_void_p)
     lib.m3_provider_set_gpu_factory.argtypes = [ctypes.c_void_p]
     lib.m3_provider_set_gpu_factory(factory)
@@ -253,6 +254,49 @@ def test_provider_options(fake):
     # Neural Engine alone gives GPU storage but no provider for regular
     # nodes, as in the reference (src/m3_provider.c:62-99).
     assert _session_status(g, (True, False, False))[0] == m3.UNSUPPORTED
+    g.free()
+
+
+def test_no_gpu_falls_back_to_the_cpu_provider(fake):
+    """src/m3_provider.c:46-58 of the reference: when the GPU backend cannot
+    be made (UNSUPPORTED, no device) and the CPU provider is allowed, the
+    session gets host storage and every node runs on the CPU provider. The
+    default options (NULL) take this path. Without the CPU provider the
+    session is UNSUPPORTED; any other constructor failure is returned as it
+    is, whatever the options."""
+    fake.oracle_backend_set_create_status(m3.UNSUPPORTED)
+    g, x, y, constant = reference_graph()
+    for options in (None, (True, True, True), (False, True, True),
+                    (True, False, True)):
+        status, made, text = _session_status(g, options)
+        assert status == m3.OK and made, (options, text)
+    assert fake.oracle_backend_reserved() == 0
+    session = m3.Session(g)
+    assert [session.provider(i) for i in range(4)] == [m3.PROVIDER_CPU] * 4
+    data = np.array([1.0, 2.0, -3.0, 0.25], np.float32)
+    session.write(x, data)
+    session.run()
+    out = session.read(y, np.zeros(4, np.float32))
+    session.free()
+    # tests/test_graph_runtime.c:139-146 of the reference, tolerance zero
+    expected = ((c_tanhf(data + constant) * constant).astype(np.float32)
+                + data).astype(np.float32)
+    assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
+    assert log_of(fake) == ([], [])
+    status, made, text = _session_status(g, (False, True, False))
+    assert status == m3.UNSUPPORTED and not made, text
+    assert "test backend: made to fail" in text
+    # The Neural Engine option allows host storage (src/m3_graph_compile.c
+    # :506-507 of the reference) but not the CPU provider for regular
+    # nodes (:412-413), so the list finds no provider.
+    status, made, text = _session_status(g, (True, True, False))
+    assert status == m3.UNSUPPORTED and not made, text
+    fake.oracle_backend_set_create_status(m3.INTERNAL)
+    for options in (None, (False, True, True), (False, True, False)):
+        status, made, text = _session_status(g, options)
+        assert status == m3.INTERNAL and not made, (options, text)
+    fake.oracle_backend_set_create_status(0)
+    assert _session_status(g)[0] == m3.OK
     g.free()
 
 
