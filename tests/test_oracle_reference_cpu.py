@@ -7,9 +7,9 @@ included. Inputs mix normal values with the special classes (signed zeros,
 infinities, NaNs with random payloads and signs, subnormals, overflow edges)
 and, for the NaN rules of two-operand ops, with inputs where most elements
 of both operands are NaN. Layouts cover contiguous, strided, offset,
-broadcast and aliased views. SUB and DIV have no reference counterpart and
-are pinned by their closed form in test_oracle_golden.py's cases and
-test_graph_cpu.py.
+broadcast and aliased views. SUB and DIV have no reference counterpart;
+test_oracle_subdiv_cpu.py pins them to IEEE-754 subtraction and division
+(numpy float32) and to the stated NaN payload rule.
 """
 import numpy as np
 import pytest
