@@ -95,10 +95,14 @@ class CpuBaseline:
             return self.harness.run_ref(kind, storages, views)
         return self.harness.run_oracle(kind, storages, views)
 
-    def timed(self, kind, storages, views):
-        start = time.perf_counter()
-        status, out = self.run(kind, storages, views)
-        return status, out, time.perf_counter() - start
+    def timed(self, kind, storages, views, runs=3):
+        """The result and the median wall time of `runs` runs."""
+        seconds = []
+        for _ in range(runs):
+            start = time.perf_counter()
+            status, out = self.run(kind, storages, views)
+            seconds.append(time.perf_counter() - start)
+        return status, out, float(np.median(seconds))
 
 
 def cpu_model():
@@ -214,6 +218,11 @@ class Workload:
             for _ in range(visits):
                 session.run()
             session.timing_reset()
+        # runs of this workload before the event-timed pass (warm-up,
+        # wall-clock pass, event pool warm-up): a kernel trace of the
+        # process finds the timed pass's dispatches after as many runs
+        self.runs_before_timed = (max(warmup, len(self.sessions)) + steps +
+                                  visits * len(self.sessions))
         for i in range(steps):
             self.sessions[i % len(self.sessions)].run()
         per_kernel = {}
@@ -532,6 +541,8 @@ def result_entry(name, workload, wall_ms, kernel_us, launches, bytes_total,
             kernel_bytes / (median_us * 1e-6) / 1e9 / PEAK_GBPS, 4)
         entry["kernel_us_min_max"] = [round(min(runs), 3),
                                       round(max(runs), 3)]
+        entry["kernel_us_runs"] = [round(u, 2) for u in runs]
+        entry["runs_before_timed_pass"] = workload.runs_before_timed
     if cpu_seconds is not None:
         entry["cpu_GBps"] = round(cpu_bytes / cpu_seconds / 1e9, 4)
     return entry
@@ -588,8 +599,10 @@ def main():
             cpu_line = {"value": round(nbytes / cpu_seconds / 1e9, 4),
                         "unit": "GB/s", "cores": 1, "kind": cpu.kind,
                         "model": cpu_model(),
-                        "sample": "the full [16,1024,1024] softmax, one "
-                                  "run of the single-threaded CPU provider"}
+                        "runs": 3,
+                        "sample": "the full [16,1024,1024] softmax, median "
+                                  "of 3 runs of the single-threaded CPU "
+                                  "provider"}
         results["softmax"] = result_entry("softmax", w, wall, kus, launches,
                                           nbytes, nbytes, parity, cpu_seconds,
                                           nbytes)

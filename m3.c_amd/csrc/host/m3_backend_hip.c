@@ -583,8 +583,8 @@ static m3_status m3_hip_scan_failure(uint32_t kind, m3_error *error)
 {
     return m3_error_set(error, M3_STATUS_OUT_OF_RANGE,
                         kind == M3_HIP_SCAN_NAN
-                            ? "softmax input contains NaN"
-                            : "float-to-I32 cast value is invalid");
+                            ? "a softmax input element is NaN"
+                            : "a value cast to I32 is NaN, infinite or outside [-2^31, 2^31)");
 }
 
 /* The list-atomic part of the data preflight: every checked input that no

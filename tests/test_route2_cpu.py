@@ -2,7 +2,8 @@
 reference tree (CPU; needs the reference, so it is skipped elsewhere).
 
 tests/route2_patch.py applies the route's header edits to copies of the
-reference headers in tests/_build/route2; m3.c_amd/csrc/host/
+reference headers in a temporary directory outside the repository (pytest's
+tmp_path); m3.c_amd/csrc/host/
 m3_backend_hip.c, include/m3_hip.h and include/m3_backend_hip.h are
 copied beside them, and gcc -fsyntax-only must accept the backend against
 the patched reference headers alone. Against the unpatched headers it must
@@ -24,10 +25,8 @@ pytestmark = pytest.mark.skipif(
     reason="the reference tree is not present here")
 
 
-def _compile(patched):
-    out = os.path.join(ROOT, "tests", "_build",
-                       "route2" if patched else "route2_unpatched")
-    shutil.rmtree(out, ignore_errors=True)
+def _compile(patched, tmp_path):
+    out = str(tmp_path / ("route2" if patched else "route2_unpatched"))
     apply_patch(REFERENCE, out, edits=EDITS if patched else [])
     ours = os.path.join(out, "ours")
     os.makedirs(ours)
@@ -42,12 +41,12 @@ def _compile(patched):
         capture_output=True, text=True)
 
 
-def test_hip_backend_compiles_against_the_patched_reference():
-    result = _compile(patched=True)
+def test_hip_backend_compiles_against_the_patched_reference(tmp_path):
+    result = _compile(True, tmp_path)
     assert result.returncode == 0, result.stderr
 
 
-def test_hip_backend_needs_the_patch():
-    result = _compile(patched=False)
+def test_hip_backend_needs_the_patch(tmp_path):
+    result = _compile(False, tmp_path)
     assert result.returncode != 0
     assert "M3_BACKEND_HIP" in result.stderr or "write" in result.stderr
