@@ -45,6 +45,10 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PEAK_GBPS = 8000.0
 CACHE_DEFEAT_BYTES = 512 << 20  # input bytes between two runs of a session
+# --no-events: the timed pass waits on the stream after each run as usual
+# but attaches no timing events, for runs under an external kernel
+# profiler (whose trace then gives the kernel durations)
+EVENTS = True
 METRIC = ("achieved HBM GB/s (% of MI355X peak) per op class; "
           "ms per m3_session_run")
 
@@ -213,8 +217,9 @@ class Workload:
         # launch that has to create its events reads a microsecond or two
         # long).
         visits = -(-steps // len(self.sessions))
+        mode = True if EVENTS else "stream"
         for session in self.sessions:
-            session.timing_enable(True)
+            session.timing_enable(mode)
             for _ in range(visits):
                 session.run()
             session.timing_reset()
@@ -520,6 +525,7 @@ def as_bytes(array):
 
 def result_entry(name, workload, wall_ms, kernel_us, launches, bytes_total,
                  kernel_bytes, parity, cpu_seconds=None, cpu_bytes=None):
+    launches = launches if EVENTS else None
     kernel_gbps = kernel_bytes / (kernel_us * 1e-6) / 1e9 if kernel_us else 0
     entry = {
         "op_class": name,
@@ -542,6 +548,7 @@ def result_entry(name, workload, wall_ms, kernel_us, launches, bytes_total,
         entry["kernel_us_min_max"] = [round(min(runs), 3),
                                       round(max(runs), 3)]
         entry["kernel_us_runs"] = [round(u, 2) for u in runs]
+    if hasattr(workload, "runs_before_timed"):
         entry["runs_before_timed_pass"] = workload.runs_before_timed
     if cpu_seconds is not None:
         entry["cpu_GBps"] = round(cpu_bytes / cpu_seconds / 1e9, 4)
@@ -560,7 +567,12 @@ def main():
                         help="comma-separated op classes to run")
     parser.add_argument("--no-cpu", action="store_true",
                         help="skip the CPU baseline and CPU parity check")
+    parser.add_argument("--no-events", action="store_true",
+                        help="no timing events in the timed pass (run it "
+                             "under a kernel profiler for the durations)")
     args = parser.parse_args()
+    global EVENTS
+    EVENTS = not args.no_events
     if args.gpus != 1:
         print("bench.py measures one GPU: this provider has no multi-GPU "
               "path (each op shards with zero exchange; see the design "
@@ -954,7 +966,7 @@ def main():
         print(json.dumps({"metric": METRIC, "op_classes": results}))
         return 0
     rotation, wall, kus, nbytes = headline
-    achieved = nbytes / (kus * 1e-6) / 1e9
+    achieved = nbytes / (kus * 1e-6) / 1e9 if kus else 0.0
     line = {
         "metric": METRIC,
         "value": round(nbytes / (wall * 1e-3) / 1e9, 1),

@@ -298,9 +298,12 @@ int m3_hip_scan_views_static(m3_hip_device *device, const uint32_t *kinds,
 int m3_hip_synchronize(m3_hip_device *device, char *message,
                        size_t capacity);
 
-/* Measurement support: when enabled, every launch is bracketed by HIP events
- * on the device stream; m3_hip_timing_read synchronizes, folds completed
- * event pairs into per-kernel totals, and copies up to `capacity` entries. */
+/* Measurement support: with `enabled` 1, every launch is bracketed by HIP
+ * events on the device stream and each run waits on the stream (not on the
+ * completion word); with 2, runs wait on the stream the same way but no
+ * events are attached, for runs under an external kernel profiler; with 0,
+ * neither. m3_hip_timing_read synchronizes, folds completed event pairs
+ * into per-kernel totals, and copies up to `capacity` entries. */
 int m3_hip_timing_enable(m3_hip_device *device, int enabled);
 int m3_hip_timing_reset(m3_hip_device *device);
 int m3_hip_timing_read(m3_hip_device *device, m3_hip_kernel_time *entries,

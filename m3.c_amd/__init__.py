@@ -464,7 +464,10 @@ class Session:
         return self.lib.m3_backend_hip_device(backend)
 
     def timing_enable(self, enabled):
-        self.hip.m3_hip_timing_enable(self.hip_device(), 1 if enabled else 0)
+        """True: events on every launch; "stream": the same stream waits
+        without events (for an external profiler); False: off."""
+        mode = 2 if enabled == "stream" else 1 if enabled else 0
+        self.hip.m3_hip_timing_enable(self.hip_device(), mode)
 
     def timing_reset(self):
         self.hip.m3_hip_timing_reset(self.hip_device())

@@ -46,6 +46,9 @@ struct m3_hip_device {
     /* M3_HIP_SOFTMAX_LATE_US at open (negative when unset): when a wave of
      * the lane-row softmax counts as late (m3_hip_softmax.hip) */
     float softmax_late_us;
+    /* M3_HIP_SOFTMAX_HOLD_US at open (negative when unset): how long after
+     * its start a wave of the lane-row softmax holds its stores */
+    float softmax_hold_us;
     /* device flags for data scans (a view's word holds the epoch of the
      * last scan that found an offending element in it), the epoch of the
      * next scan, and the flags' host mirror in coherent pinned memory */
@@ -66,6 +69,10 @@ struct m3_hip_device {
     uint32_t unchecked_polls; /* polled completions since the last query
                                * of the stream's error state */
     bool timing;
+    /* timing mode 1 attaches events to every launch; mode 2 only retires
+     * each run on the stream, as mode 1 does, so that an external profiler
+     * sees the same dispatch pattern without the events */
+    bool timing_events;
     std::vector<m3_hip_pending_time> pending;
     std::vector<hipEvent_t> spare_events;
     std::vector<m3_hip_time_total> totals;

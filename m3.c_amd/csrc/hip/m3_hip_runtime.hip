@@ -266,6 +266,7 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
     {
         int rate = 0;
         const char *late = std::getenv("M3_HIP_SOFTMAX_LATE_US");
+        const char *hold = std::getenv("M3_HIP_SOFTMAX_HOLD_US");
 
         device->wall_clock_khz =
             hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate,
@@ -274,6 +275,9 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
                 : 0U;
         device->softmax_late_us =
             late != nullptr && late[0] != '\0' ? std::strtof(late, nullptr)
+                                                : -1.0F;
+        device->softmax_hold_us =
+            hold != nullptr && hold[0] != '\0' ? std::strtof(hold, nullptr)
                                                 : -1.0F;
     }
     code = m3_hip_check(hipStreamCreateWithFlags(&device->stream,
@@ -1117,7 +1121,7 @@ int m3_hip_time_begin(m3_hip_device *device, const char *name,
     slot->name = name;
     slot->start = nullptr;
     slot->stop = nullptr;
-    if (!device->timing) {
+    if (!device->timing || !device->timing_events) {
         return M3_HIP_OK;
     }
     if (m3_hip_take_event(device, &slot->start) != M3_HIP_OK) {
@@ -1147,6 +1151,7 @@ extern "C" int m3_hip_timing_enable(m3_hip_device *device, int enabled)
         return M3_HIP_INVALID;
     }
     device->timing = enabled != 0;
+    device->timing_events = enabled == 1;
     return M3_HIP_OK;
 }
 

@@ -68,6 +68,8 @@ constexpr uint64_t kMaxLaneGrid = 0x7fffffffU; /* grid x limit */
 constexpr double kHbmBytesPerUs = 8.0e6; /* MI355X peak, 8 TB/s */
 constexpr double kLateFactor = 0.85;
 constexpr double kLateFloorUs = 3.0;
+constexpr double kHoldFactor = 1.19;
+constexpr uint32_t kLaneRowWavesPerSimd = 4U; /* amdgpu_waves_per_eu */
 constexpr uint32_t kStreamRows = 4U; /* rows per workgroup, streamed kernel */
 
 /* Four F32 -inf: what a load past the end of a row reads instead. Never
@@ -88,6 +90,9 @@ struct m3_softmax_args {
     /* lane-row kernel: s_memrealtime ticks after its start past which a
      * wave still waiting for its rows counts as late */
     uint32_t late_ticks;
+    /* lane-row kernel: s_memrealtime ticks after its start before which a
+     * wave does not store its results (0: no hold) */
+    uint32_t hold_ticks;
     /* Rows whose starts are not evenly spaced (outer_rank > 1): row r
      * starts at input + sum over axes of coordinate(r, axis) * stride. */
     uint32_t outer_rank;
@@ -1077,6 +1082,14 @@ void m3_softmax_lane_rows_kernel(m3_softmax_args a)
                 }
             }
         }
+        /* A wave whose rows arrived early waits, up to a.hold_ticks after
+         * its start, before it stores: its writes then do not compete with
+         * the reads still in flight for other waves. Bounded by the clock,
+         * so every wave goes on. */
+        while (__builtin_amdgcn_s_memrealtime() - start <
+               (uint64_t)a.hold_ticks) {
+            __builtin_amdgcn_s_sleep(2);
+        }
         if (finite && present) {
             const double inverse = 1.0 / (double)sum;
 
@@ -1675,6 +1688,25 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
             args.late_ticks = device->wall_clock_khz == 0U || ticks >= 4.0e9
                                   ? 0xffffffffU
                                   : (uint32_t)ticks;
+            /* hold: 1.19 times the time the launch's reads take at peak
+             * HBM bandwidth (10.0 us for [16,1024,1024] F32), when every
+             * wave of the launch is resident at once so that all its reads
+             * are issued at the start; otherwise none. M3_HIP_SOFTMAX_HOLD_US
+             * sets it. */
+            const uint64_t resident = (uint64_t)device->compute_units * 4U *
+                                      kLaneRowWavesPerSimd;
+            const double hold_us =
+                device->softmax_hold_us >= 0.0F
+                    ? (double)device->softmax_hold_us
+                : (rows + 3U) / 4U <= resident
+                    ? kHoldFactor * (double)rows * (double)width * in_size /
+                          kHbmBytesPerUs
+                    : 0.0;
+            const double hold = hold_us * device->wall_clock_khz / 1000.0;
+
+            args.hold_ticks = device->wall_clock_khz == 0U || hold >= 4.0e9
+                                  ? 0U
+                                  : (uint32_t)hold;
             const m3_softmax_launcher launcher =
                 lane_launchers[lane_q == 16U][width == 64U * lane_q][f32];
 
