@@ -300,6 +300,25 @@ def build_softmax(s):
     return build
 
 
+def build_attention(scores, causal):
+    def build():
+        shape = scores.shape
+        graph = m3.Graph()
+        vs = graph.add_value(m3.INPUT, m3.F32, shape)
+        vscale = graph.add_value(m3.CONSTANT, m3.F32, (1,))
+        vmask = graph.add_value(m3.CONSTANT, m3.F32, causal.shape)
+        graph.set_constant(vscale, np.array([0.125], np.float32))
+        graph.set_constant(vmask, causal)
+        t0 = graph.add_value(m3.TEMPORARY, m3.F32, shape)
+        graph.add_node(m3.OP_MUL, [vs, vscale], [t0])
+        t1 = graph.add_value(m3.TEMPORARY, m3.F32, shape)
+        graph.add_node(m3.OP_ADD, [t0, vmask], [t1])
+        vy = graph.add_value(m3.OUTPUT, m3.F32, shape)
+        graph.add_node(m3.OP_SOFTMAX, [t1], [vy])
+        return graph, [(vs, scores)], (vy, shape, np.float32)
+    return build
+
+
 def build_mul(x, c):
     def build():
         graph = m3.Graph()
@@ -562,8 +581,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--rotate", type=int, default=4)
     parser.add_argument("--classes",
-                        default="softmax,softmax_wide,mul,cast,copy,snake,"
-                                "tanh,gated_silu,euler,executor",
+                        default="softmax,attention,softmax_wide,mul,cast,"
+                                "copy,snake,tanh,gated_silu,euler,executor",
                         help="comma-separated op classes to run")
     parser.add_argument("--no-cpu", action="store_true",
                         help="skip the CPU baseline and CPU parity check")
@@ -629,6 +648,54 @@ def main():
         headline = (w.rotate, wall, kus, nbytes)
         w.free()
         log("softmax:", json.dumps(results["softmax"]))
+
+    if "attention" in classes:
+        # scores * scale + causal mask -> SOFTMAX in one run: the softmax
+        # input is produced inside the run (by the fused scale-and-mask
+        # program) and checked for NaN on the device before the softmax,
+        # with one host wait per run
+        log("attention: generating [16,1024,1024] scores")
+        shape = (16, 1024, 1024)
+        scores = m3.rng_fill("normal", int(np.prod(shape)), seed=0,
+                             a=8.0).reshape(shape)
+        causal = np.where(np.triu(np.ones(shape[1:], bool), 1), -np.inf,
+                          0.0).astype(np.float32)
+        unique = 2 * scores.nbytes + causal.nbytes
+        w = Workload("attention", build_attention(scores, causal),
+                     [scores], unique, ["m3_softmax_rows"], args.rotate, cpu)
+        wall, kus, launches, kernels, run_kernel_ms = w.measure(
+            args.steps, args.warmup)
+        parity = None
+        if cpu is not None:
+            out = w.read_output()
+            f = np.float32
+            logits = ((scores * f(0.125)).astype(f) + causal).astype(f)
+            status, storages = cpu.run(
+                m3.OP_SOFTMAX, [as_bytes(logits),
+                                np.zeros(logits.nbytes, np.uint8)],
+                [spec(0, m3.F32, shape), spec(1, m3.F32, shape)])
+            ref = storages[1].view(np.float32).reshape(shape)
+            mismatches = int(np.count_nonzero(ref.view(np.uint32) !=
+                                              out.view(np.uint32)))
+            parity = ("bit-exact vs float32 scale and mask, then the CPU "
+                      "provider's softmax" if mismatches == 0 else
+                      "%d of %d elements differ" % (mismatches, scores.size))
+        # host waits of one plain run (the completion-word path)
+        session = w.sessions[0]
+        before = session.host_waits()
+        session.run()
+        waits_per_run = session.host_waits() - before
+        entry = result_entry("attention", w, wall, kus, launches, unique,
+                             2 * scores.nbytes, parity)
+        entry["kernels"] = {k: v[1] / max(v[0], 1) * 1000
+                            for k, v in kernels.items()}
+        entry["kernel_time_per_run_ms"] = round(run_kernel_ms, 4)
+        entry["host_waits_per_run"] = waits_per_run
+        entry["hbm_bytes_per_run"] = (3 * scores.nbytes + causal.nbytes +
+                                      3 * scores.nbytes)
+        results["attention"] = entry
+        w.free()
+        log("attention:", json.dumps(results["attention"]))
 
     if "softmax_wide" in classes:
         log("softmax_wide: generating [4096,16384] logits")

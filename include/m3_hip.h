@@ -298,6 +298,39 @@ int m3_hip_scan_views_static(m3_hip_device *device, const uint32_t *kinds,
 int m3_hip_synchronize(m3_hip_device *device, char *message,
                        size_t capacity);
 
+/* How many times the host has waited for the device's stream (stream
+ * synchronizations and completion polls, data-scan readbacks, blocking
+ * copies) since the device was opened; for tests and measurement. No
+ * counterpart in the reference. */
+int m3_hip_host_waits(const m3_hip_device *device, uint64_t *waits);
+
+/* Device-side gating of the rest of a command list, so that a list whose
+ * checked input (a softmax input, a float-to-I32 cast input) an earlier
+ * command of the same list produces runs with one host wait, at its end.
+ * The reference's Metal provider rejects such a list
+ * (src/m3_backend_metal_basic.m:274-302) and its CPU provider checks the
+ * input right before the command (src/m3_op_execute_host.c:5-60); these
+ * calls give the CPU provider's order without a mid-list wait:
+ *   m3_hip_gate_open   every command kernel launched from here until
+ *                      m3_hip_gate_close returns at its start, touching no
+ *                      tensor, once a check of this gate has failed;
+ *                      idempotent while open;
+ *   m3_hip_gate_check  queues, in stream order, the data scan of `view`
+ *                      for `kind` (M3_HIP_SCAN_NAN, M3_HIP_SCAN_I32_RANGE)
+ *                      and closes the gate when it finds an offending
+ *                      element; the first failing check of a gate is the
+ *                      one kept;
+ *   m3_hip_gate_close  waits for the stream once and ends the gating;
+ *                      *failed_kind receives 0 when every check passed,
+ *                      else 1 + the kind of the first failing check.
+ * No counterpart in the reference's backend interface. */
+int m3_hip_gate_open(m3_hip_device *device, char *message, size_t capacity);
+int m3_hip_gate_check(m3_hip_device *device, uint32_t kind,
+                      const m3_hip_view *view, char *message,
+                      size_t capacity);
+int m3_hip_gate_close(m3_hip_device *device, uint32_t *failed_kind,
+                      char *message, size_t capacity);
+
 /* Measurement support: with `enabled` 1, every launch is bracketed by HIP
  * events on the device stream and each run waits on the stream (not on the
  * completion word); with 2, runs wait on the stream the same way but no

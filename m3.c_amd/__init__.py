@@ -201,6 +201,8 @@ EXPORTS_HIP = [
     "m3_hip_launch_program", "m3_hip_launch_tanh", "m3_hip_launch_gated_silu",
     "m3_hip_prepare_program", "m3_hip_scan_views_static",
     "m3_hip_scan_views_begin", "m3_hip_scan_views_collect",
+    "m3_hip_gate_open", "m3_hip_gate_check", "m3_hip_gate_close",
+    "m3_hip_host_waits",
 ]
 
 _LIB = None
@@ -304,6 +306,7 @@ def load():
              P(ctypes.c_float), sz, P(sz), ctypes.c_char_p, sz)
     _declare(hip, "m3_hip_stream", vp, vp)
     _declare(hip, "m3_hip_synchronize", st, vp, ctypes.c_char_p, sz)
+    _declare(hip, "m3_hip_host_waits", st, vp, P(ctypes.c_uint64))
     _declare(hip, "m3_hip_launch_program", st, vp, P(ctypes.c_uint32), vp,
              sz, ctypes.c_char_p, sz)
     _LIB, _HIP = lib, hip
@@ -462,6 +465,15 @@ class Session:
     def hip_device(self):
         backend = self.lib.m3_session_backend(self.handle)
         return self.lib.m3_backend_hip_device(backend)
+
+    def host_waits(self):
+        """How many times the host has waited for this session's stream."""
+        waits = ctypes.c_uint64(0)
+        check_hip = self.hip.m3_hip_host_waits(self.hip_device(),
+                                               ctypes.byref(waits))
+        if check_hip != 0:
+            raise M3Error(INTERNAL, "m3_hip_host_waits failed")
+        return waits.value
 
     def timing_enable(self, enabled):
         """True: events on every launch; "stream": the same stream waits

@@ -121,10 +121,14 @@ struct m3_tanh_vec_args {
     uint8_t *output;
     uint32_t groups; /* count / 4 */
     uint32_t tail;   /* count % 4 */
+    m3_hip_gate list_gate;
 };
 
 __global__ __launch_bounds__(256) void m3_tanh_vec_kernel(m3_tanh_vec_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint32_t step = gridDim.x * kThreads * kTanhUnroll;
 
     for (uint32_t first = blockIdx.x * kThreads * kTanhUnroll + threadIdx.x;
@@ -171,6 +175,7 @@ struct m3_activation_general_args {
     uint64_t count;
     uint64_t shape[M3_HIP_MAX_RANK];
     int64_t strides[2][M3_HIP_MAX_RANK];
+    m3_hip_gate list_gate;
 };
 
 __device__ __forceinline__ void m3_general_offsets(
@@ -194,6 +199,9 @@ __device__ __forceinline__ void m3_general_offsets(
 __global__ __launch_bounds__(256) void m3_tanh_general_kernel(
     m3_activation_general_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
 
     for (uint64_t f = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -215,6 +223,7 @@ struct m3_silu_vec_args {
     uint8_t *output;
     uint32_t groups;
     uint32_t tail;
+    m3_hip_gate list_gate;
 };
 
 /* Four GATED_SILU elements with a gate of dtype D, as F32 bits; `table`
@@ -306,6 +315,9 @@ __device__ __forceinline__ uint32_t m3_silu_table_lookup(
 __global__ __launch_bounds__(256) void m3_gated_silu_bf16_kernel(
     m3_silu_vec_args a, const uint4 *source)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint32_t step = gridDim.x * kThreads * kUnroll;
     __shared__ uint16_t table[kSiluTableEntries];
     __shared__ uint64_t exp_table[32];
@@ -400,6 +412,9 @@ template <uint32_t D>
 __global__ __launch_bounds__(256) void m3_gated_silu_vec_kernel(
     m3_silu_vec_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint32_t step = gridDim.x * kThreads * kUnroll;
     constexpr uint32_t size = D == M3N_F32 ? 4U : 2U;
     __shared__ uint64_t table[32];
@@ -446,6 +461,9 @@ __global__ __launch_bounds__(256) void m3_gated_silu_vec_kernel(
 __global__ __launch_bounds__(256) void m3_gated_silu_general_kernel(
     m3_activation_general_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
     const uint64_t out_size = a.dtypes[0] == M3N_F32 ? 4U : 2U;
 
@@ -591,6 +609,7 @@ extern "C" int m3_hip_launch_tanh(m3_hip_device *device,
         count < (1ULL << 32U)) {
         m3_tanh_vec_args args;
 
+        args.list_gate = device->gate;
         args.input = (const uint8_t *)input->base + input->byte_offset;
         args.output = (uint8_t *)output->base + output->byte_offset;
         args.groups = (uint32_t)(count / 4U);
@@ -611,6 +630,7 @@ extern "C" int m3_hip_launch_tanh(m3_hip_device *device,
     m3_activation_general_args args;
 
     m3_general_args(output, input, nullptr, &args);
+    args.list_gate = device->gate;
     uint32_t blocks = m3_grid_blocks(device, count, 256U, 16U);
 
     return m3_hip_launch(
@@ -651,6 +671,7 @@ extern "C" int m3_hip_launch_gated_silu(m3_hip_device *device,
         count < (1ULL << 32U)) { /* 32-bit group indices, as for TANH */
         m3_silu_vec_args args;
 
+        args.list_gate = device->gate;
         args.gate = (const uint8_t *)gate->base + gate->byte_offset;
         args.up = (const uint8_t *)up->base + up->byte_offset;
         args.output = (uint8_t *)output->base + output->byte_offset;
@@ -678,6 +699,7 @@ extern "C" int m3_hip_launch_gated_silu(m3_hip_device *device,
     m3_activation_general_args args;
 
     m3_general_args(output, gate, up, &args);
+    args.list_gate = device->gate;
     uint32_t blocks = m3_grid_blocks(device, count, 256U, 16U);
 
     return m3_hip_launch(

@@ -59,6 +59,7 @@ struct m3_bin_vec_args {
     uint32_t out_dtype;
     uint32_t count;  /* elements, < 2^32 */
     uint32_t groups; /* count / 4 */
+    m3_hip_gate list_gate;
 };
 
 constexpr uint32_t kThreads = 256U;
@@ -162,6 +163,9 @@ __device__ __forceinline__ void m3_store4(uint8_t *out, uint32_t dtype,
 template <int OP, bool F32ONLY, int UNROLL = (int)kUnroll>
 __global__ __launch_bounds__(256) void m3_binary_vec_kernel(m3_bin_vec_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint32_t out_dtype = F32ONLY ? (uint32_t)M3N_F32 : a.out_dtype;
     const uint32_t step = gridDim.x * kThreads * UNROLL;
 
@@ -222,12 +226,16 @@ struct m3_bin_general_args {
     uint64_t shape[M3_HIP_MAX_RANK];
     int64_t left_strides[M3_HIP_MAX_RANK];
     int64_t right_strides[M3_HIP_MAX_RANK];
+    m3_hip_gate list_gate;
 };
 
 template <int OP>
 __global__ __launch_bounds__(256) void m3_binary_general_kernel(
     m3_bin_general_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     const uint32_t out_size = a.out_dtype == M3N_F32 ? 4U : 2U;
 
@@ -341,6 +349,7 @@ int m3_launch_binary_op(m3_hip_device *device, const m3_hip_view *left,
 
     m3_plan_index_space(output, operands, 3U, &plan);
     std::memset(&vec, 0, sizeof(vec));
+    vec.list_gate = device->gate;
     if (output->element_count < (1ULL << 32U) &&
         ((uintptr_t)out % out_bytes) == 0U &&
         m3_classify_operand(plan, 1U, left, &vec.left) &&
@@ -380,6 +389,7 @@ int m3_launch_binary_op(m3_hip_device *device, const m3_hip_view *left,
     m3_bin_general_args general;
 
     std::memset(&general, 0, sizeof(general));
+    general.list_gate = device->gate;
     general.left = (const uint8_t *)left->base + left->byte_offset;
     general.right = (const uint8_t *)right->base + right->byte_offset;
     general.out = out;

@@ -83,8 +83,12 @@ __device__ __forceinline__ uint32_t m3_convert(uint32_t raw)
 
 template <uint32_t IN, uint32_t OUT>
 __global__ __launch_bounds__(256) void m3_cast_vec_kernel(
-    const uint8_t *input, uint8_t *output, uint64_t count, uint64_t groups)
+    const uint8_t *input, uint8_t *output, uint64_t count, uint64_t groups,
+    m3_hip_gate gate)
 {
+    if (m3_gate_closed(gate)) {
+        return; /* a check earlier in the list failed */
+    }
     using in_io = m3_vec_io<m3_size_of(IN)>;
     using out_io = m3_vec_io<m3_size_of(OUT)>;
     const typename in_io::type *in = (const typename in_io::type *)input;
@@ -143,12 +147,16 @@ struct m3_strided_args {
     uint64_t count;
     uint64_t shape[M3_HIP_MAX_RANK];
     int64_t strides[M3_HIP_MAX_RANK];
+    m3_hip_gate list_gate;
 };
 
 /* Strided input, contiguous output; `convert` false copies raw elements. */
 __global__ __launch_bounds__(256) void m3_cast_strided_kernel(
     m3_strided_args a, bool convert)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
     const uint32_t in_size = m3_size_of(a.in_dtype);
     const uint32_t out_size = m3_size_of(a.out_dtype);
@@ -184,8 +192,11 @@ __global__ __launch_bounds__(256) void m3_cast_strided_kernel(
 /* Contiguous byte copy with 16-byte words; `tail` bytes finish it. */
 __global__ __launch_bounds__(256) void m3_copy_bytes_kernel(
     const uint4 *input, uint4 *output, uint64_t words, const uint8_t *tail_in,
-    uint8_t *tail_out, uint32_t tail)
+    uint8_t *tail_out, uint32_t tail, m3_hip_gate gate)
 {
+    if (m3_gate_closed(gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint64_t step = (uint64_t)gridDim.x * kThreads * kUnroll;
 
     for (uint64_t first = (uint64_t)blockIdx.x * kThreads * kUnroll +
@@ -222,7 +233,7 @@ void m3_launch_cast_vec(m3_hip_device *device, const uint8_t *input,
 {
     hipExtLaunchKernelGGL((m3_cast_vec_kernel<IN, OUT>), dim3(blocks),
                           dim3(kThreads), 0, device->stream, start, stop, 0U,
-                          input, output, count, count / 4U);
+                          input, output, count, count / 4U, device->gate);
 }
 
 typedef void (*m3_cast_launcher)(m3_hip_device *, const uint8_t *, uint8_t *,
@@ -295,7 +306,7 @@ int m3_launch_unary(m3_hip_device *device, const m3_hip_view *input,
                                       dim3(kThreads), 0, device->stream, start,
                                       stop, 0U, (const uint4 *)in,
                                       (uint4 *)out, words, in + words * 16U,
-                                      out + words * 16U, tail);
+                                      out + words * 16U, tail, device->gate);
             },
             message, capacity);
     }
@@ -326,6 +337,7 @@ int m3_launch_unary(m3_hip_device *device, const m3_hip_view *input,
     m3_strided_args args;
 
     std::memset(&args, 0, sizeof(args));
+    args.list_gate = device->gate;
     args.input = in;
     args.output = out;
     args.in_dtype = input->dtype;

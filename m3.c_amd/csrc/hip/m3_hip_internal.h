@@ -35,6 +35,25 @@ struct m3_hip_time_total {
 /* Launch durations kept per kernel name between two timing resets. */
 constexpr size_t kTimingSamples = 4096U;
 
+/* The device-side gate of a command list. After a command whose checked
+ * input (a softmax input, a float-to-I32 cast input) an earlier command of
+ * the same list produced, every command kernel of the list is launched
+ * with the list's gate; it returns at its start, before touching any
+ * tensor, when the gate word holds the gate's epoch, which a failed check
+ * stores there (m3_hip_gate_check). word == nullptr: no gate, one uniform
+ * branch on a kernel argument. */
+struct m3_hip_gate {
+    const uint32_t *word;
+    uint32_t epoch;
+};
+
+__device__ __forceinline__ bool m3_gate_closed(const m3_hip_gate &gate)
+{
+    return gate.word != nullptr &&
+           __hip_atomic_load(gate.word, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) == gate.epoch;
+}
+
 struct m3_hip_device {
     int ordinal;
     hipStream_t stream;
@@ -60,6 +79,19 @@ struct m3_hip_device {
     uint32_t async_ticket;
     uint32_t async_sequence;
     uint32_t async_count;
+    /* the gate that launches carry (no word outside m3_hip_gate_open ..
+     * m3_hip_gate_close); device words: [0] the epoch of the last closed
+     * gate, [1] the flag of the gate's scans; pinned words: [0] the epoch
+     * of the last closed gate, [1] the kind of its failed check; the epoch
+     * of the last gate opened */
+    m3_hip_gate gate;
+    uint32_t *gate_words;
+    uint32_t *host_gate;
+    uint32_t gate_epoch;
+    uint32_t gate_scan_epoch;
+    /* how many times the host has waited for the stream (synchronize,
+     * scan readback, blocking copies) since the device was opened */
+    uint64_t host_waits;
     /* the device address of the static scan scratch (m3_hip_runtime.hip) */
     uint32_t *static_scratch;
     /* completion word in coherent pinned host memory (may be null) and the

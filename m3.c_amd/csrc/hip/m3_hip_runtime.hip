@@ -329,6 +329,12 @@ extern "C" void m3_hip_device_close(m3_hip_device *device)
     if (device->scan_flags != nullptr) {
         (void)hipFree(device->scan_flags);
     }
+    if (device->gate_words != nullptr) {
+        (void)hipFree(device->gate_words);
+    }
+    if (device->host_gate != nullptr) {
+        (void)hipHostFree(device->host_gate);
+    }
     if (device->host_flags != nullptr) {
         (void)hipHostFree(device->host_flags);
     }
@@ -339,6 +345,16 @@ extern "C" void m3_hip_device_close(m3_hip_device *device)
         (void)hipStreamDestroy(device->stream);
     }
     delete device;
+}
+
+extern "C" int m3_hip_host_waits(const m3_hip_device *device,
+                                 uint64_t *waits)
+{
+    if (device == nullptr || waits == nullptr) {
+        return M3_HIP_INVALID;
+    }
+    *waits = device->host_waits;
+    return M3_HIP_OK;
 }
 
 extern "C" int m3_hip_device_properties(const m3_hip_device *device,
@@ -516,6 +532,7 @@ extern "C" int m3_hip_copy_h2d(m3_hip_device *device,
                                        byte_count, hipMemcpyHostToDevice,
                                        device->stream),
                         "hipMemcpyAsync(host to device)", message, capacity);
+    device->host_waits += 1U;
     if (code == M3_HIP_OK) {
         code = m3_hip_check(hipStreamSynchronize(device->stream),
                             "hipStreamSynchronize", message, capacity);
@@ -542,6 +559,7 @@ extern "C" int m3_hip_copy_d2h(m3_hip_device *device, void *host_destination,
                                        byte_count, hipMemcpyDeviceToHost,
                                        device->stream),
                         "hipMemcpyAsync(device to host)", message, capacity);
+    device->host_waits += 1U;
     if (code == M3_HIP_OK) {
         code = m3_hip_check(hipStreamSynchronize(device->stream),
                             "hipStreamSynchronize", message, capacity);
@@ -634,6 +652,7 @@ extern "C" int m3_hip_synchronize(m3_hip_device *device, char *message,
      * next launch, and the timing events of the next launch read the
      * kernel's own duration (they read about 2 us long when the runtime
      * has not yet retired the previous work). */
+    device->host_waits += 1U;
     if (device->done_word != nullptr && !device->timing) {
         const uint32_t sequence = device->done_sequence + 1U;
 
@@ -705,17 +724,43 @@ __device__ __forceinline__ uint32_t m3_scan_offends(uint32_t bits,
                : 1U;
 }
 
+/* A scan that also closes a command list's gate when it finds an
+ * offending element (m3_hip_gate_check): words[0] is the gate word, `host`
+ * the pinned report (epoch of the closed gate, kind of the check). No
+ * words: a plain scan. */
+struct m3_scan_gate {
+    uint32_t *words;
+    uint32_t *host;
+    uint32_t epoch;
+    uint32_t kind;
+};
+
 /* The lanes that found an offending element store the epoch (all store
- * the same word, so their order does not matter). */
+ * the same word, so their order does not matter), and close the gate of
+ * a gated scan unless an earlier check of the same gate closed it (the
+ * waves of one scan store the same values, so their races are benign;
+ * checks of one gate run in list order on the stream). */
 __device__ __forceinline__ void m3_scan_mark(uint32_t found, uint32_t *flag,
-                                             uint32_t epoch)
+                                             uint32_t epoch,
+                                             const m3_scan_gate &gate)
 {
     if (__any(found != 0U) && found != 0U) {
         *flag = epoch;
+        if (gate.words != nullptr &&
+            __hip_atomic_load(&gate.words[0], __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT) != gate.epoch) {
+            __hip_atomic_store(&gate.words[0], gate.epoch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&gate.host[1], gate.kind, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(&gate.host[0], gate.epoch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+            __threadfence_system();
+        }
     }
 }
 
-__global__ void m3_scan_kernel(m3_scan_args args)
+__global__ void m3_scan_kernel(m3_scan_args args, m3_scan_gate gate)
 {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     uint32_t found = 0U;
@@ -735,7 +780,7 @@ __global__ void m3_scan_kernel(m3_scan_args args)
         found |= m3_scan_offends(m3_scan_load(args.base + offset, args.dtype),
                                  args.kind);
     }
-    m3_scan_mark(found, args.flag, args.epoch);
+    m3_scan_mark(found, args.flag, args.epoch, gate);
 }
 
 /* Contiguous F32 scan: 16-byte loads. */
@@ -744,7 +789,8 @@ __global__ void m3_scan_f32_contiguous_kernel(const uint4 *data,
                                               const uint32_t *tail,
                                               uint32_t tail_count,
                                               uint32_t kind, uint32_t *flag,
-                                              uint32_t epoch)
+                                              uint32_t epoch,
+                                              m3_scan_gate gate)
 {
     uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     uint32_t found = 0U;
@@ -759,7 +805,7 @@ __global__ void m3_scan_f32_contiguous_kernel(const uint4 *data,
     if (blockIdx.x == 0U && threadIdx.x < tail_count) {
         found |= m3_scan_offends(tail[threadIdx.x], kind);
     }
-    m3_scan_mark(found, flag, epoch);
+    m3_scan_mark(found, flag, epoch, gate);
 }
 
 /* Zeroes `count` flag words (one wave). */
@@ -791,6 +837,67 @@ __global__ __launch_bounds__(64) void m3_scan_publish_kernel(
     }
 }
 
+/* Queues the scan of one view for `kind`: a wave that finds an offending
+ * element stores `epoch` into *flag and closes `gate` when it has words. */
+static int m3_hip_scan_launch(m3_hip_device *device, uint32_t *flag,
+                              uint32_t epoch, uint32_t kind,
+                              const m3_hip_view *view,
+                              const m3_scan_gate &gate, char *message,
+                              size_t capacity)
+{
+    if (view->element_count == 0U) {
+        return M3_HIP_OK;
+    }
+    const m3_hip_view *operands[1] = {view};
+    m3_index_plan plan;
+    const uint8_t *base = (const uint8_t *)view->base + view->byte_offset;
+
+    m3_plan_index_space(view, operands, 1U, &plan);
+    if (view->dtype == M3_HIP_F32 && plan.rank == 1U &&
+        plan.strides[0][0] == 4 && ((uintptr_t)base & 15U) == 0U) {
+        uint64_t quads = view->element_count / 4U;
+        uint32_t tail = (uint32_t)(view->element_count % 4U);
+        uint32_t blocks = m3_grid_blocks(device, quads == 0U ? 1U : quads,
+                                         256U, 8U);
+
+        return m3_hip_launch(
+            device, "m3_scan_f32",
+            [&](hipEvent_t start, hipEvent_t stop) {
+                hipExtLaunchKernelGGL(m3_scan_f32_contiguous_kernel,
+                                      dim3(blocks), dim3(256), 0,
+                                      device->stream, start, stop, 0U,
+                                      (const uint4 *)base, quads,
+                                      (const uint32_t *)base + quads * 4U,
+                                      tail, kind, flag, epoch, gate);
+            },
+            message, capacity);
+    }
+    m3_scan_args args;
+
+    std::memset(&args, 0, sizeof(args));
+    args.base = base;
+    args.count = view->element_count;
+    args.rank = plan.rank;
+    args.dtype = view->dtype;
+    args.kind = kind;
+    args.epoch = epoch;
+    args.flag = flag;
+    for (uint32_t axis = 0U; axis < plan.rank; ++axis) {
+        args.shape[axis] = plan.shape[axis];
+        args.strides[axis] = plan.strides[0][axis];
+    }
+    uint32_t blocks = m3_grid_blocks(device, view->element_count, 256U, 8U);
+
+    return m3_hip_launch(
+        device, "m3_scan_strided",
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL(m3_scan_kernel, dim3(blocks), dim3(256), 0,
+                                  device->stream, start, stop, 0U, args,
+                                  gate);
+        },
+        message, capacity);
+}
+
 /* Queues the scan of views[0, count) into the flag words `flags` with
  * `epoch` and the publication of one flag per view into the pinned words
  * `published`; *sequence receives the completion sequence that follows
@@ -808,64 +915,10 @@ static int m3_hip_scan_queue(m3_hip_device *device, uint32_t *flags,
     const bool was_timing = device->timing;
 
     device->timing = device->timing && timed;
-
     for (size_t i = 0U; code == M3_HIP_OK && i < count; ++i) {
-        const m3_hip_view *view = &views[i];
-        uint32_t *flag = flags + i;
-
-        if (view->element_count == 0U) {
-            continue;
-        }
-        const m3_hip_view *operands[1] = {view};
-        m3_index_plan plan;
-        const uint8_t *base = (const uint8_t *)view->base + view->byte_offset;
-
-        m3_plan_index_space(view, operands, 1U, &plan);
-        if (view->dtype == M3_HIP_F32 && plan.rank == 1U &&
-            plan.strides[0][0] == 4 && ((uintptr_t)base & 15U) == 0U) {
-            uint64_t quads = view->element_count / 4U;
-            uint32_t tail = (uint32_t)(view->element_count % 4U);
-            uint32_t blocks = m3_grid_blocks(device, quads == 0U ? 1U : quads,
-                                             256U, 8U);
-
-            code = m3_hip_launch(
-                device, "m3_scan_f32",
-                [&](hipEvent_t start, hipEvent_t stop) {
-                    hipExtLaunchKernelGGL(m3_scan_f32_contiguous_kernel,
-                                          dim3(blocks), dim3(256), 0,
-                                          device->stream, start, stop, 0U,
-                                          (const uint4 *)base, quads,
-                                          (const uint32_t *)base + quads * 4U,
-                                          tail, kinds[i], flag, epoch);
-                },
-                message, capacity);
-        } else {
-            m3_scan_args args;
-
-            std::memset(&args, 0, sizeof(args));
-            args.base = base;
-            args.count = view->element_count;
-            args.rank = plan.rank;
-            args.dtype = view->dtype;
-            args.kind = kinds[i];
-            args.epoch = epoch;
-            args.flag = flag;
-            for (uint32_t axis = 0U; axis < plan.rank; ++axis) {
-                args.shape[axis] = plan.shape[axis];
-                args.strides[axis] = plan.strides[0][axis];
-            }
-            uint32_t blocks = m3_grid_blocks(device, view->element_count,
-                                             256U, 8U);
-
-            code = m3_hip_launch(
-                device, "m3_scan_strided",
-                [&](hipEvent_t start, hipEvent_t stop) {
-                    hipExtLaunchKernelGGL(m3_scan_kernel, dim3(blocks),
-                                          dim3(256), 0, device->stream, start,
-                                          stop, 0U, args);
-                },
-                message, capacity);
-        }
+        code = m3_hip_scan_launch(device, flags + i, epoch, kinds[i],
+                                  &views[i], m3_scan_gate{}, message,
+                                  capacity);
     }
     if (code == M3_HIP_OK) {
         sequence += 1U;
@@ -899,6 +952,7 @@ static int m3_hip_scan_wait(m3_hip_device *device, uint32_t sequence,
 {
     int code;
 
+    device->host_waits += 1U;
     if (device->done_word != nullptr && !device->timing &&
         m3_hip_poll_done(device, sequence)) {
         code = m3_hip_stream_errors(device, message, capacity);
@@ -1101,6 +1155,135 @@ extern "C" int m3_hip_scan_views_static(m3_hip_device *device,
     }
     return m3_hip_scan_into(device, device->static_scratch, 1U, kinds, views,
                             count, flags, false, message, capacity);
+}
+
+/* ---- device-side gating of a command list ------------------------------ */
+
+/* Zeroes gate words [first, first + count) on the stream. */
+static int m3_hip_gate_clear(m3_hip_device *device, uint32_t first,
+                             uint32_t count, char *message, size_t capacity)
+{
+    return m3_hip_launch(
+        device, "m3_scan_clear",
+        [&](hipEvent_t start, hipEvent_t stop) {
+            hipExtLaunchKernelGGL(m3_scan_clear_kernel, dim3(1), dim3(64), 0,
+                                  device->stream, start, stop, 0U,
+                                  device->gate_words + first, count);
+        },
+        message, capacity);
+}
+
+extern "C" int m3_hip_gate_open(m3_hip_device *device, char *message,
+                                size_t capacity)
+{
+    int code = M3_HIP_OK;
+
+    if (device == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "device is null");
+    }
+    if (device->gate.word != nullptr) {
+        return M3_HIP_OK; /* already open: the list keeps its gate */
+    }
+    if (device->gate_words == nullptr) {
+        code = m3_hip_check(hipMalloc((void **)&device->gate_words,
+                                      2U * sizeof(uint32_t)),
+                            "hipMalloc(gate words)", message, capacity);
+        if (code == M3_HIP_OK) {
+            code = m3_hip_gate_clear(device, 0U, 2U, message, capacity);
+        }
+        if (code != M3_HIP_OK) {
+            (void)hipFree(device->gate_words);
+            device->gate_words = nullptr;
+            return code;
+        }
+    }
+    if (device->host_gate == nullptr) {
+        code = m3_hip_check(hipHostMalloc((void **)&device->host_gate,
+                                          2U * sizeof(uint32_t),
+                                          hipHostMallocCoherent),
+                            "hipHostMalloc(gate report)", message, capacity);
+        if (code != M3_HIP_OK) {
+            device->host_gate = nullptr;
+            return code;
+        }
+        device->host_gate[0] = 0U;
+        device->host_gate[1] = 0U;
+    }
+    /* 0 is what a cleared gate word holds and is never an epoch; when the
+     * epochs wrap the words are cleared again */
+    device->gate_epoch += 1U;
+    if (device->gate_epoch == 0U) {
+        device->gate_epoch = 1U;
+        code = m3_hip_gate_clear(device, 0U, 2U, message, capacity);
+        if (code != M3_HIP_OK) {
+            return code;
+        }
+        __atomic_store_n(&device->host_gate[0], 0U, __ATOMIC_RELEASE);
+    }
+    device->gate.word = device->gate_words;
+    device->gate.epoch = device->gate_epoch;
+    return M3_HIP_OK;
+}
+
+extern "C" int m3_hip_gate_check(m3_hip_device *device, uint32_t kind,
+                                 const m3_hip_view *view, char *message,
+                                 size_t capacity)
+{
+    int code;
+
+    if (device == nullptr || view == nullptr || !m3_view_is_valid(view) ||
+        kind > M3_HIP_SCAN_I32_RANGE) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "gate check arguments are incomplete or "
+                           "malformed");
+    }
+    if (device->gate.word == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "no gate is open on this device");
+    }
+    device->gate_scan_epoch += 1U;
+    if (device->gate_scan_epoch == 0U) {
+        device->gate_scan_epoch = 1U;
+        code = m3_hip_gate_clear(device, 1U, 1U, message, capacity);
+        if (code != M3_HIP_OK) {
+            return code;
+        }
+    }
+    const m3_scan_gate gate = {device->gate_words, device->host_gate,
+                               device->gate.epoch, kind};
+
+    return m3_hip_scan_launch(device, device->gate_words + 1U,
+                              device->gate_scan_epoch, kind, view, gate,
+                              message, capacity);
+}
+
+extern "C" int m3_hip_gate_close(m3_hip_device *device,
+                                 uint32_t *failed_kind, char *message,
+                                 size_t capacity)
+{
+    if (device == nullptr || failed_kind == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "gate close arguments are incomplete");
+    }
+    *failed_kind = 0U;
+    if (device->gate.word == nullptr) {
+        return M3_HIP_OK;
+    }
+    const uint32_t epoch = device->gate.epoch;
+
+    device->gate.word = nullptr;
+    device->gate.epoch = 0U;
+    int code = m3_hip_synchronize(device, message, capacity);
+
+    if (code != M3_HIP_OK) {
+        return code;
+    }
+    if (__atomic_load_n(&device->host_gate[0], __ATOMIC_ACQUIRE) == epoch) {
+        *failed_kind = 1U + __atomic_load_n(&device->host_gate[1],
+                                            __ATOMIC_ACQUIRE);
+    }
+    return M3_HIP_OK;
 }
 
 /* ---- timing ------------------------------------------------------------- */

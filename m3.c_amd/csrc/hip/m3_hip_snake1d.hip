@@ -97,11 +97,15 @@ struct m3_snake_vec_args {
     uint32_t groups;      /* elements / 4 */
     m3_fast_div length_in_groups; /* L / 4 */
     m3_fast_div channels;
+    m3_hip_gate list_gate;
 };
 
 __global__ __launch_bounds__(256) void m3_snake1d_vec_kernel(
     m3_snake_vec_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint32_t step = gridDim.x * kThreads * kUnroll;
 
     for (uint32_t first = blockIdx.x * kThreads * kUnroll + threadIdx.x;
@@ -172,11 +176,15 @@ struct m3_snake_general_args {
     uint64_t shape[3];
     int64_t input_strides[3];
     int64_t alpha_stride;
+    m3_hip_gate list_gate;
 };
 
 __global__ __launch_bounds__(256) void m3_snake1d_general_kernel(
     m3_snake_general_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
 
     for (uint64_t f = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -235,6 +243,7 @@ extern "C" int m3_hip_launch_snake1d(m3_hip_device *device,
         m3_snake_vec_args args;
 
         std::memset(&args, 0, sizeof(args));
+        args.list_gate = device->gate;
         args.input = (const float4 *)in;
         args.alpha = al;
         args.alpha_stride = alpha_stride;
@@ -258,6 +267,7 @@ extern "C" int m3_hip_launch_snake1d(m3_hip_device *device,
     m3_snake_general_args general;
 
     std::memset(&general, 0, sizeof(general));
+    general.list_gate = device->gate;
     general.input = in;
     general.alpha = al;
     general.output = (float *)out;

@@ -98,6 +98,7 @@ struct m3_softmax_args {
     uint32_t outer_rank;
     uint64_t outer_shape[M3_HIP_MAX_RANK];
     int64_t outer_strides[M3_HIP_MAX_RANK];
+    m3_hip_gate list_gate;
 };
 
 /* Start of input row `row`. */
@@ -467,6 +468,9 @@ template <bool F32IO>
 __global__ __launch_bounds__(256) void m3_softmax_tiled_kernel(
     m3_softmax_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     extern __shared__ float lds[];
     __shared__ m3_row_state state[kMaxTileRows];
     __shared__ uint64_t exp_table[32];
@@ -825,6 +829,9 @@ template <int VPL, int R, int DEPTH, bool F32IO, bool VEC>
 __global__ __launch_bounds__(256) void m3_softmax_rows_kernel(
     m3_softmax_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     m3_softmax_rows<VPL, R, DEPTH, F32IO, VEC>(a);
 }
 
@@ -935,6 +942,9 @@ template <int Q, bool FULL, bool F32IO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void m3_softmax_lane_rows_kernel(m3_softmax_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     __shared__ uint64_t exp_table[32];
     const uint32_t lane = threadIdx.x & 63U;
     const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
@@ -1179,6 +1189,9 @@ __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
     m3_softmax_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     constexpr int R = (int)kStreamRows;
     constexpr int P = (int)kWaves - 1; /* producer waves */
     __shared__ float ring[2 * P][R][kLine];
@@ -1487,6 +1500,7 @@ struct m3_softmax_general_args {
     int64_t column_stride;
     uint64_t outer_shape[M3_HIP_MAX_RANK];
     int64_t outer_strides[M3_HIP_MAX_RANK];
+    m3_hip_gate list_gate;
 };
 
 __device__ __forceinline__ float m3_general_load(const uint8_t *p,
@@ -1502,6 +1516,9 @@ __device__ __forceinline__ float m3_general_load(const uint8_t *p,
 __global__ __launch_bounds__(64) void m3_softmax_general_kernel(
     m3_softmax_general_args a)
 {
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
     const uint32_t out_size = a.out_dtype == M3N_F32 ? 4U : 2U;
     const uint64_t step = (uint64_t)gridDim.x * blockDim.x;
 
@@ -1627,6 +1644,7 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
             input->dtype == M3_HIP_F32 && output->dtype == M3_HIP_F32;
 
         std::memset(&args, 0, sizeof(args));
+        args.list_gate = device->gate;
         args.input = in;
         args.output = out;
         args.rows = rows;
@@ -1791,6 +1809,7 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
     m3_softmax_general_args general;
 
     std::memset(&general, 0, sizeof(general));
+    general.list_gate = device->gate;
     general.input = in;
     general.output = out;
     general.rows = rows;

@@ -68,6 +68,16 @@ __device__ __forceinline__ float m3_program_scalar(
         m3_load_as_f32_bits((unsigned int)*(constant_u16)address, D));
 }
 
+/* True when the command list's gate is closed: a data check earlier in
+ * the list failed and the program must not run (word 0: no gate). */
+__device__ __forceinline__ bool m3_program_gate_closed(
+    const unsigned int *word, unsigned int epoch)
+{
+    return word != 0 &&
+           __hip_atomic_load(word, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) == epoch;
+}
+
 __device__ __forceinline__ m3_program_f32x4 m3_program_splat(float v)
 {
     m3_program_f32x4 r = {v, v, v, v};

@@ -13,16 +13,18 @@
  *
  * Execution of a command list (reference: m3_metal_execute_in_pool,
  * src/m3_backend_metal.m:178-217, and m3_metal_preflight_basic,
- * src/m3_backend_metal_basic.m:274-302). The list is atomic with respect
- * to data checks: before any kernel is enqueued,
- *   1. a SOFTMAX, or a CAST from a float dtype to I32, whose input storage
- *      is written by an earlier command of the same list is rejected with
- *      M3_STATUS_UNSUPPORTED (the data would only exist after commit);
- *   2. the remaining such inputs are scanned on the device (NaN for
- *      SOFTMAX, finite and inside [-2^31, 2^31) for the cast) with one
- *      flag readback for the whole list;
- * and the first command in list order that fails either check decides the
- * status (OUT_OF_RANGE for data), with no output modified. A view that
+ * src/m3_backend_metal_basic.m:274-302). Checked inputs (a SOFTMAX input,
+ * the input of a CAST from a float dtype to I32) that no command of the
+ * list writes are scanned on the device (NaN for SOFTMAX, finite and
+ * inside [-2^31, 2^31) for the cast) before any kernel is enqueued, with
+ * one flag readback for the whole list, and the first failing one in list
+ * order fails the list with no output modified (OUT_OF_RANGE). A checked
+ * input that an earlier command of the list writes, which Metal rejects,
+ * is checked as the reference CPU provider does, right before its command:
+ * the scan is queued after its producers and a failure closes the list's
+ * device-side gate, so that the command and every later one return
+ * without running; the list then waits once, at its end, for the verdict
+ * (the commands before the failing one have run). A view that
  * passed its check is remembered until its storage is written (host write,
  * kernel output) or freed, so an unchanged input is not scanned again.
  * Views the preflight has scanned are also watched: a host write to their
@@ -79,6 +81,9 @@ typedef struct {
     bool started_valid[M3_HIP_WATCHED_VIEWS];
     size_t started_count;
     uint32_t started_ticket;
+    /* true when nothing was queued since the last list waited for its
+     * produced checks' verdict: m3_hip_finish has nothing to wait for */
+    bool settled;
 } m3_hip_backend_context;
 
 static bool m3_hip_same_view(const m3_hip_view *a, const m3_hip_view *b)
@@ -247,6 +252,7 @@ static m3_status m3_hip_reserve(void *opaque, size_t byte_count,
     void *base = NULL;
     int code;
 
+    context->settled = false;
     if (context->arena_count == M3_HIP_MAX_ARENAS) {
         return m3_error_set(error, M3_STATUS_OUT_OF_RANGE,
                             "HIP backend arena table is full");
@@ -297,6 +303,7 @@ static m3_status m3_hip_allocate(void *opaque, size_t byte_count,
     void *base = NULL;
     int code;
 
+    context->settled = false;
     *handle = NULL;
     *data = NULL;
     if (byte_count == 0U) {
@@ -361,6 +368,7 @@ static m3_status m3_hip_write(void *opaque, void *data, size_t byte_offset,
     m3_status status;
     int code;
 
+    context->settled = false;
     m3_hip_forget_storage(context, data);
     code = m3_hip_copy_h2d(context->device, (uint8_t *)data + byte_offset,
                                source, byte_count, message, sizeof(message));
@@ -411,6 +419,7 @@ static m3_status m3_hip_read(void *opaque, const void *data,
                                (const uint8_t *)data + byte_offset,
                                byte_count, message, sizeof(message));
 
+    context->settled = false;
     return code == M3_HIP_OK ? M3_STATUS_OK
                              : m3_hip_status(code, message, error);
 }
@@ -584,15 +593,15 @@ static m3_status m3_hip_scan_failure(uint32_t kind, m3_error *error)
     return m3_error_set(error, M3_STATUS_OUT_OF_RANGE,
                         kind == M3_HIP_SCAN_NAN
                             ? "a softmax input element is NaN"
-                            : "a value cast to I32 is NaN, infinite or outside [-2^31, 2^31)");
+                            : "invalid value for a cast to I32: NaN, infinite or outside [-2^31, 2^31)");
 }
 
 /* The list-atomic part of the data preflight: every checked input that no
  * earlier command of the list writes is scanned before anything runs, and
  * the first failing one in list order fails the whole list with nothing
  * executed (the Metal contract, src/m3_backend_metal_basic.m:274-302).
- * Checked inputs that an earlier command writes are scanned later, when
- * their producers have run (m3_hip_scan_produced). */
+ * Checked inputs that an earlier command writes are checked on the
+ * device after their producers (m3_hip_check_produced). */
 static m3_status m3_hip_preflight(m3_hip_backend_context *context,
                                   const m3_command *commands, size_t count,
                                   m3_error *error)
@@ -652,40 +661,43 @@ static m3_status m3_hip_preflight(m3_hip_backend_context *context,
     return M3_STATUS_OK;
 }
 
-/* Scans the checked input of commands[index] when an earlier command of
- * the list writes it. The scan runs on the stream after every command
- * enqueued so far and its flag is read back, so it sees the produced
- * values. On failure the commands before `index` have run and it and the
- * rest do not: the reference CPU provider's order, preflight right before
- * each command (src/m3_op_execute_host.c:5-60), where Metal rejects such a
- * list outright. */
-static m3_status m3_hip_scan_produced(m3_hip_backend_context *context,
-                                      const m3_command *commands,
-                                      size_t index, m3_error *error)
+/* Queues the check of the input of commands[index] when it is a checked
+ * input (softmax, float-to-I32 cast) that an earlier command of the list
+ * writes: the scan runs on the stream after the commands enqueued so far,
+ * so it sees the produced values, and a failing scan closes the list's
+ * gate, so that this command and every later one return without running
+ * (m3_hip_gate_open .. m3_hip_gate_close). The commands before `index`
+ * have then run and it and the rest have not: the reference CPU provider's
+ * order, preflight right before each command (src/m3_op_execute_host.c
+ * :5-60), where Metal rejects such a list outright. *gated records that the
+ * gate is open. */
+static m3_status m3_hip_check_produced(m3_hip_backend_context *context,
+                                       const m3_command *commands,
+                                       size_t index, bool *gated,
+                                       m3_error *error)
 {
     uint32_t kind = 0U;
-    uint32_t flag = 0U;
     const m3_tensor_view *input = m3_hip_checked_input(&commands[index],
                                                        &kind);
     char message[M3_HIP_MESSAGE] = "";
     m3_hip_view view;
-    int code;
+    int code = M3_HIP_OK;
 
     if (input == NULL || input->metadata.element_count == 0U ||
         !m3_hip_written_before(commands, index, input->storage)) {
         return M3_STATUS_OK;
     }
-    m3_hip_view_of(input, &view);
-    code = m3_hip_scan_views(context->device, &kind, &view, 1U, &flag,
-                             message, sizeof(message));
-    if (code != M3_HIP_OK) {
-        return m3_hip_status(code, message, error);
+    if (!*gated) {
+        code = m3_hip_gate_open(context->device, message, sizeof(message));
+        *gated = code == M3_HIP_OK;
     }
-    if (flag != 0U) {
-        return m3_hip_scan_failure(kind, error);
+    if (code == M3_HIP_OK) {
+        m3_hip_view_of(input, &view);
+        code = m3_hip_gate_check(context->device, kind, &view, message,
+                                 sizeof(message));
     }
-    m3_hip_remember_clean(context, &view, kind);
-    return M3_STATUS_OK;
+    return code == M3_HIP_OK ? M3_STATUS_OK
+                             : m3_hip_status(code, message, error);
 }
 
 static int m3_hip_enqueue(m3_hip_backend_context *context,
@@ -772,24 +784,48 @@ static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
     m3_status status;
     size_t i;
     int code = M3_HIP_OK;
+    bool gated = false;
 
     (void)scratch;
+    context->settled = false;
     status = m3_hip_preflight(context, commands, count, error);
     if (status != M3_STATUS_OK) {
         return status;
     }
     for (i = 0U; i < count && code == M3_HIP_OK; ++i) {
-        status = m3_hip_scan_produced(context, commands, i, error);
+        status = m3_hip_check_produced(context, commands, i, &gated, error);
         if (status != M3_STATUS_OK) {
-            return status;
+            break;
         }
         m3_hip_forget_outputs(context, &commands[i]);
         code = m3_hip_enqueue(context, &commands[i], message,
                               sizeof(message));
     }
+    if (gated) {
+        /* the list's one host wait: the verdict of its produced checks */
+        uint32_t failed = 0U;
+        char close_message[M3_HIP_MESSAGE] = "";
+        const int closed = m3_hip_gate_close(context->device, &failed,
+                                             close_message,
+                                             sizeof(close_message));
+
+        if (status == M3_STATUS_OK && code == M3_HIP_OK) {
+            if (closed != M3_HIP_OK) {
+                return m3_hip_status(closed, close_message, error);
+            }
+            if (failed != 0U) {
+                return m3_hip_scan_failure(failed - 1U, error);
+            }
+            context->settled = true;
+        }
+    }
+    if (status != M3_STATUS_OK) {
+        (void)m3_hip_synchronize(context->device, NULL, 0U);
+        return status;
+    }
     if (code == M3_HIP_OK) {
-        /* queued; m3_hip_finish, a storage read or write, a data scan or
-         * destroy waits for it */
+        /* queued (or, with produced checks, complete); m3_hip_finish, a
+         * storage read or write, a data scan or destroy waits for it */
         m3_error_reset(error);
         return M3_STATUS_OK;
     }
@@ -801,7 +837,12 @@ static m3_status m3_hip_finish(void *opaque, m3_error *error)
 {
     m3_hip_backend_context *context = opaque;
     char message[M3_HIP_MESSAGE] = "";
-    int code = m3_hip_synchronize(context->device, message, sizeof(message));
+    int code;
+
+    if (context->settled) {
+        return M3_STATUS_OK; /* the last list already waited */
+    }
+    code = m3_hip_synchronize(context->device, message, sizeof(message));
 
     return code == M3_HIP_OK ? M3_STATUS_OK
                              : m3_hip_status(code, message, error);

@@ -1,0 +1,200 @@
+"""Checked inputs produced inside a command list, gated on the device (GPU).
+
+A softmax input, or the input of a float-to-I32 cast, that an earlier
+command of the same list writes is checked as the reference CPU provider
+checks it, right before its command (src/m3_op_execute_host.c:5-60): the
+commands before it run, it and every later command do not, and the list
+fails with OUT_OF_RANGE. The HIP provider queues the check on the device
+after the producers and lets a failed check close the list's gate, so the
+list waits for the host once, at its end. These tests hold the order
+semantics (every earlier output written, every later one untouched, the
+first failing check decides) and the single wait per run.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import m3
+from harness import HipFixture, ViewSpec, as_bytes, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def f32(values):
+    return np.asarray(values, dtype=np.float32)
+
+
+@pytest.fixture()
+def hip(gpu):
+    fixture = HipFixture()
+    yield fixture
+    fixture.close()
+
+
+def values(hip, handle, count, dtype=np.float32):
+    return hip.download([handle], [np.empty(count, dtype=dtype)])[0]
+
+
+def softmax_oracle(row):
+    views = [ViewSpec(0, m3.F32, (row.size,)),
+             ViewSpec(1, m3.F32, (row.size,))]
+    status, out = run_oracle(m3.OP_SOFTMAX, [as_bytes(row),
+                                             np.zeros(row.nbytes, np.uint8)],
+                             views)
+    assert status == m3.OK
+    return out[1].view(np.float32)
+
+
+def test_nan_produced_mid_list_stops_the_rest(hip):
+    print("gpu case gate nan_produced_mid_list", file=sys.stderr, flush=True)
+    sentinel = f32([-9, -9, -9])
+    arrays = [f32([3, 4, 5]), f32([2, 2, 2]), f32([1, math.nan, 1])] + \
+        [sentinel.copy() for _ in range(6)]
+    h = hip.upload(arrays)
+    a, b, c, t1, y1, t2, u, y2, z = hip.views(
+        h, [ViewSpec(i, m3.F32, (3,)) for i in range(9)])
+    commands = [(m3.OP_ADD, [a, b, t1]),       # produces a clean input
+                (m3.OP_SOFTMAX, [t1, y1]),     # its check passes
+                (m3.OP_MUL, [c, b, t2]),       # produces a NaN
+                (m3.OP_ADD, [a, a, u]),        # before the failing check
+                (m3.OP_SOFTMAX, [t2, y2]),     # its check fails
+                (m3.OP_MUL, [a, b, z])]        # after it: must not run
+    status, message = hip.execute(commands)
+    assert status == m3.OUT_OF_RANGE and "NaN" in message, message
+    assert list(values(hip, h[3], 3)) == [5, 6, 7]
+    assert np.array_equal(values(hip, h[4], 3).view(np.uint32),
+                          softmax_oracle(f32([5, 6, 7])).view(np.uint32))
+    got = values(hip, h[5], 3)
+    assert got[0] == 2 and math.isnan(got[1]) and got[2] == 2
+    assert list(values(hip, h[6], 3)) == [6, 8, 10]
+    assert list(values(hip, h[7], 3)) == [-9, -9, -9]
+    assert list(values(hip, h[8], 3)) == [-9, -9, -9]
+    # The next list on the same device is not gated by the failed one.
+    status, message = hip.execute([(m3.OP_MUL, [a, b, z])])
+    assert status == m3.OK, message
+    assert list(values(hip, h[8], 3)) == [6, 8, 10]
+
+
+def test_first_failing_check_decides(hip):
+    """Two produced checks that both fail: the first one in list order is
+    reported (a NaN softmax input before an invalid I32 cast input), and
+    the command between them does not run."""
+    print("gpu case gate first_failing_check", file=sys.stderr, flush=True)
+    arrays = [f32([1, math.nan, 2, 3]), f32([1, 1, 1, 1]),
+              f32([7, 7, 7, 7]), f32([7, 7, 7, 7]), f32([7, 7, 7, 7]),
+              np.array([5, 5, 5, 5], np.int32)]
+    h = hip.upload(arrays)
+    x, one, t, y, w = hip.views(h[:5], [ViewSpec(i, m3.F32, (4,))
+                                        for i in range(5)])
+    (i32,) = hip.views([h[5]], [ViewSpec(0, m3.I32, (4,))])
+    status, message = hip.execute([(m3.OP_MUL, [x, one, t]),
+                                   (m3.OP_SOFTMAX, [t, y]),
+                                   (m3.OP_COPY, [x, w]),
+                                   (m3.OP_CAST, [w, i32])])
+    assert status == m3.OUT_OF_RANGE and "NaN" in message, message
+    assert list(values(hip, h[3], 4)) == [7, 7, 7, 7]
+    assert list(values(hip, h[4], 4)) == [7, 7, 7, 7]
+    assert list(values(hip, h[5], 4, np.int32)) == [5, 5, 5, 5]
+    # Only the cast's input is produced and invalid: the cast is reported.
+    status, message = hip.execute([(m3.OP_COPY, [x, w]),
+                                   (m3.OP_CAST, [w, i32]),
+                                   (m3.OP_MUL, [one, one, y])])
+    assert status == m3.OUT_OF_RANGE and "I32" in message, message
+    got = values(hip, h[4], 4)
+    assert got[0] == 1 and math.isnan(got[1])
+    assert list(values(hip, h[5], 4, np.int32)) == [5, 5, 5, 5]
+    assert list(values(hip, h[3], 4)) == [7, 7, 7, 7]
+
+
+def attention_graph(shape):
+    """scores * scale + mask -> SOFTMAX: the scaled, causally masked scores
+    of attention, produced and checked inside one run."""
+    rows, width = shape[-2], shape[-1]
+    g = m3.Graph()
+    scores = g.add_value(m3.INPUT, m3.F32, shape)
+    scale = g.add_value(m3.CONSTANT, m3.F32, (1,))
+    mask = g.add_value(m3.CONSTANT, m3.F32, (rows, width))
+    g.set_constant(scale, np.array([0.125], np.float32))
+    causal = np.where(np.triu(np.ones((rows, width), bool), 1), -np.inf,
+                      0.0).astype(np.float32)
+    g.set_constant(mask, causal)
+    t0 = g.add_inferred(m3.OP_MUL, [scores, scale], m3.TEMPORARY, m3.F32)
+    g.add_node(m3.OP_MUL, [scores, scale], [t0])
+    t1 = g.add_inferred(m3.OP_ADD, [t0, mask], m3.TEMPORARY, m3.F32)
+    g.add_node(m3.OP_ADD, [t0, mask], [t1])
+    y = g.add_inferred(m3.OP_SOFTMAX, [t1], m3.OUTPUT, m3.F32)
+    g.add_node(m3.OP_SOFTMAX, [t1], [y])
+    return g, scores, y, causal
+
+
+def attention_oracle(scores, causal):
+    shape = scores.shape
+    f = np.float32
+    logits = ((scores * f(0.125)).astype(f) + causal).astype(f)
+    views = [ViewSpec(0, m3.F32, shape), ViewSpec(1, m3.F32, shape)]
+    status, out = run_oracle(m3.OP_SOFTMAX, [as_bytes(logits),
+                                             np.zeros(logits.nbytes,
+                                                      np.uint8)], views)
+    assert status == m3.OK
+    return out[1].view(np.float32).reshape(shape)
+
+
+def test_attention_pattern_waits_once_per_run(gpu):
+    """The fused scale-and-mask program produces the softmax input; the
+    run waits for the host once, the result equals the oracle bit for bit
+    (MUL and ADD are single IEEE operations, which numpy float32 fixes), and
+    a NaN made by the program (inf * 0 is not reachable with a fixed scale,
+    so an inf score plus a -inf mask entry) fails the run with OUT_OF_RANGE
+    and leaves the output as it was."""
+    print("gpu case gate attention_waits_once", file=sys.stderr, flush=True)
+    shape = (2, 64, 96)
+    rng = np.random.default_rng(3)
+    scores = rng.standard_normal(shape).astype(np.float32) * 3
+    g, vin, vout, causal = attention_graph(shape)
+    session = m3.Session(g)
+    g.free()
+    assert all(session.provider(i) == m3.PROVIDER_HIP for i in range(3))
+    session.write(vin, scores)
+    session.run()
+    before = session.host_waits()
+    for _ in range(3):
+        session.run()
+    assert session.host_waits() - before == 3
+    out = session.read(vout, np.zeros(shape, np.float32))
+    assert np.array_equal(out.view(np.uint32),
+                          attention_oracle(scores, causal).view(np.uint32))
+    bad = scores.copy()
+    bad[1, 5, 70] = np.inf  # column 70 > row 5: the mask adds -inf there
+    session.write(vin, bad)
+    with pytest.raises(m3.M3Error) as failure:
+        session.run()
+    assert failure.value.status == m3.OUT_OF_RANGE
+    assert "NaN" in failure.value.message
+    again = session.read(vout, np.zeros(shape, np.float32))
+    assert np.array_equal(again.view(np.uint32), out.view(np.uint32))
+    # a clean input afterwards runs again
+    session.write(vin, scores)
+    session.run()
+    out2 = session.read(vout, np.zeros(shape, np.float32))
+    assert np.array_equal(out2.view(np.uint32), out.view(np.uint32))
+    session.free()
+
+
+def test_attention_pattern_full_size(gpu):
+    """[16, 1024, 1024] causal attention scores through the same graph,
+    every element against the oracle."""
+    print("gpu case gate attention_full_size", file=sys.stderr, flush=True)
+    shape = (16, 1024, 1024)
+    scores = m3.rng_fill("normal", int(np.prod(shape)), seed=4,
+                         a=3.0).reshape(shape)
+    g, vin, vout, causal = attention_graph(shape)
+    session = m3.Session(g)
+    g.free()
+    session.write(vin, scores)
+    session.run()
+    out = session.read(vout, np.zeros(shape, np.float32))
+    session.free()
+    expected = attention_oracle(scores, causal)
+    assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
