@@ -703,7 +703,7 @@ def main():
             4096, 16384)
         nbytes = 2 * s.nbytes
         w = Workload("softmax_wide", build_softmax(s), [s], nbytes,
-                     ["m3_softmax_rows_streamed"], args.rotate, cpu)
+                     ["m3_softmax_rows_wide", "m3_softmax_rows_streamed"], args.rotate, cpu)
         wall, kus, launches, kernels, _ = w.measure(args.steps, args.warmup)
         parity = None
         cpu_seconds = None

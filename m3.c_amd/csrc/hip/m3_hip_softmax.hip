@@ -1433,6 +1433,401 @@ __attribute__((amdgpu_waves_per_eu(4))) void m3_softmax_stream_kernel(
     }
 }
 
+/* ---- long rows: one read, the in-order sum in parallel ------------------ */
+
+/* Sum of a float over the 16 lanes of each DPP row (any order: the value
+ * is an estimate), in every lane of the row. */
+__device__ __forceinline__ float m3_row16_sum_f32(float t)
+{
+    t = t + m3_dpp_f32<0xB1>(0.0F, t);
+    t = t + m3_dpp_f32<0x4E>(0.0F, t);
+    t = t + m3_dpp_f32<0x141>(0.0F, t);
+    return t + m3_dpp_f32<0x140>(0.0F, t);
+}
+
+/* The left-to-right F32 sum continued over 64 consecutive values of LDS
+ * starting at `line` (16-byte aligned): lane i of the first DPP row reads
+ * values 4i..4i+3 and the running value passes from lane to lane
+ * (row_ror:1), so that lane 15 holds the sum after the 64 values. The
+ * other rows of the wave perform the same instructions on the same values;
+ * only lane 15's result is read. */
+__device__ __forceinline__ uint32_t m3_segment_sum_sequential(
+    uint32_t s_bits, const float *line)
+{
+    const float4 e = *(const float4 *)(line + 4U * (threadIdx.x & 15U));
+    float t = m3_bits_f32(s_bits);
+
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+        t = m3_dpp_f32<0x121>(0.0F, t) + e.x;
+        t = t + e.y;
+        t = t + e.z;
+        t = t + e.w;
+    }
+    return (uint32_t)__builtin_amdgcn_readlane((int)m3_f32_bits(t), 15);
+}
+
+/* Inclusive prefix sum over the 64 lanes of a wave (lane l gets the sum of
+ * lanes 0..l): row_shr within the 16-lane rows, then row_bcast:15 and
+ * row_bcast:31 across them. */
+__device__ __forceinline__ uint32_t m3_wave_scan_u32(uint32_t x)
+{
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF,
+                                               false); /* row_shr:1 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF,
+                                               false); /* row_shr:2 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF,
+                                               false); /* row_shr:4 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF,
+                                               false); /* row_shr:8 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF,
+                                               false); /* row_bcast:15 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF,
+                                               false); /* row_bcast:31 */
+    return x;
+}
+
+/* Rows of up to 1024Q columns (VEC: aligned, a multiple of 4 wide), read
+ * once: a workgroup of four waves holds one row in VGPRs, wave w the
+ * contiguous quarter of columns [256Qw, 256Q(w+1)); lane l of a wave holds
+ * columns 256j + 4l .. +3 of that quarter in block j (j < Q), and DPP row
+ * r of the wave (lanes 16r..16r+15) holds the 64 columns 256j + 64r .. of
+ * block j, a "segment". Columns past the width read -inf and give e = +0.
+ *
+ * The reference's in-order sum s_{c+1} = RN(s_c + e_c) (src/m3_op_execute_
+ * basic.c:124-180) is computed exactly without a chain of `width`
+ * dependent additions. While s stays inside one binade [2^k, 2^(k+1)), an
+ * F32 value there is K ulp_k with K an integer in [2^23, 2^24) (ulp_k =
+ * 2^(k-23); the binade "k = -126" is [0, 2^-125) with K in [0, 2^24), zero
+ * and the subnormals included), and for e >= 0
+ *     RN(K ulp_k + e) = (K + r) ulp_k,  r = RN_int(e / ulp_k)
+ * as long as K + r < 2^24 and e / ulp_k is not an exact half-integer (a tie,
+ * whose rounding would depend on the parity of K). Within a binade the sum
+ * is therefore K plus an integer sum of the r, which any order computes.
+ * For each segment the kernel guesses the binade of s at its start from an
+ * estimate of the running sum (F32 totals of the segments before it) and
+ * forms R = sum of r over its 64 columns, marking the segment when a
+ * column is a tie or its r reaches 2^24. Then a walk over the segments in
+ * column order (wave 0's, then 1's, ..., handed on through LDS) keeps the
+ * exact s as bits: a segment whose guess matches the binade of s, is not
+ * marked and ends inside the binade advances s by R in integer arithmetic;
+ * any other segment (the first one, which starts at s = 0; one where s
+ * crosses a power of two; a tie; a wrong guess) is summed column by column
+ * in order (m3_row_sum_sequential). Both give the reference's bits; the
+ * guesses only decide how often the second form runs (about 3% of the
+ * segments for softmax rows of 16,384 normal logits).
+ *
+ * The maximum, the count of +inf and the last column that is not -inf are
+ * reduced across the workgroup first; blocks past that column skip the
+ * exponentials. Rows whose maximum is +-inf are written from their inputs
+ * (zeros, or 1/k on their k +inf entries). p = e / sum as in the other
+ * kernels (m3_softmax_scale4), stored once. */
+/* Loads one row's block j of this lane as F32 (columns past the width
+ * read -inf). */
+template <bool F32IO>
+__device__ __forceinline__ float4 m3_wide_load(const uint8_t *in, uint32_t c,
+                                               uint32_t width,
+                                               uint32_t in_dtype)
+{
+    if (F32IO) {
+        const m3_f32x4 *source =
+            c < width ? (const m3_f32x4 *)(in + 4U * (uint64_t)c)
+                      : (const m3_f32x4 *)&m3_minus_inf4;
+        const m3_f32x4 w = __builtin_nontemporal_load(source);
+
+        return make_float4(w[0], w[1], w[2], w[3]);
+    }
+    const float4 x = m3_softmax_load4<false>(in, c < width ? c : 0U, in_dtype);
+
+    return c < width ? x
+                     : make_float4(-INFINITY, -INFINITY, -INFINITY,
+                                   -INFINITY);
+}
+
+template <int Q, int NW, bool F32IO>
+__global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
+    m3_softmax_args a)
+{
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
+    __shared__ uint64_t exp_table[32];
+    __shared__ float part_max[NW];
+    __shared__ uint32_t part_inf[NW];
+    __shared__ uint32_t part_last[NW];
+    __shared__ float segments[NW][Q][4];
+    __shared__ uint32_t words[NW * Q * 4];
+    __shared__ uint32_t carry;
+    extern __shared__ float values[]; /* e of the row, 256 NW Q floats */
+    const uint32_t lane = threadIdx.x & 63U;
+    const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
+    const uint32_t drow = lane >> 4U;
+    const uint32_t width = a.width;
+    const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
+    const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
+    const uint64_t out_pitch =
+        (uint64_t)width * (out_dtype == M3N_F32 ? 4U : 2U);
+    /* first column of this lane in block 0 */
+    uint32_t first = wave * 256U * Q + 4U * lane;
+    uint64_t row = blockIdx.x;
+    float4 ahead[Q]; /* the next row's columns, loading */
+
+    if (threadIdx.x < 32U) {
+        exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
+    }
+    {
+        const uint8_t *in = m3_softmax_row(a, row);
+
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            ahead[j] = m3_wide_load<F32IO>(in, first + 256U * j, width,
+                                           in_dtype);
+        }
+    }
+    while (row < a.rows) {
+        /* the per-block columns are recomputed each row, not kept live
+         * across the loop */
+        asm volatile("" : "+v"(first));
+        float4 v[Q];
+
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            v[j] = ahead[j];
+        }
+        const uint64_t next = row + gridDim.x;
+
+        /* the next row's loads go out now and arrive while this row is
+         * computed */
+        if (next < a.rows) {
+            const uint8_t *in = m3_softmax_row(a, next);
+
+#pragma unroll
+            for (int j = 0; j < Q; ++j) {
+                ahead[j] = m3_wide_load<F32IO>(in, first + 256U * j, width,
+                                               in_dtype);
+            }
+        }
+        uint8_t *out = a.output + row * out_pitch;
+        /* maximum, +inf count, 1 + the last column that is not -inf */
+        float m = -INFINITY;
+        uint32_t infinities = 0U;
+        uint32_t last = 0U;
+
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const float t = fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w));
+
+            m = fmaxf(m, t);
+            infinities += (v[j].x == INFINITY) + (v[j].y == INFINITY) +
+                          (v[j].z == INFINITY) + (v[j].w == INFINITY);
+            last = t != -INFINITY ? first + 256U * j + 4U : last;
+        }
+        m = m3_wave_max(m);
+        infinities = m3_wave_sum(infinities);
+        last = m3_wave_max_u32(last);
+        if (lane == 0U) {
+            part_max[wave] = m;
+            part_inf[wave] = infinities;
+            part_last[wave] = last;
+        }
+        __syncthreads();
+        m = part_max[0];
+        infinities = part_inf[0];
+        last = part_last[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            m = fmaxf(m, part_max[w]);
+            infinities += part_inf[w];
+            last = max(last, part_last[w]);
+        }
+        m = m3_uniform_f32(m);
+        infinities = m3_uniform_u32(infinities);
+        last = m3_uniform_u32(last);
+        if (m == INFINITY || m == -INFINITY) {
+            /* zeros, or 1/k on the k +inf entries */
+            const float one_over_count =
+                m == INFINITY ? 1.0F / (float)infinities : 0.0F;
+
+#pragma unroll
+            for (int j = 0; j < Q; ++j) {
+                const uint32_t c = first + 256U * j;
+                float4 p;
+
+                p.x = v[j].x == INFINITY ? one_over_count : 0.0F;
+                p.y = v[j].y == INFINITY ? one_over_count : 0.0F;
+                p.z = v[j].z == INFINITY ? one_over_count : 0.0F;
+                p.w = v[j].w == INFINITY ? one_over_count : 0.0F;
+                if (c < width) {
+                    m3_softmax_store4<F32IO>(out, c, out_dtype, p);
+                }
+            }
+            __syncthreads(); /* the part_* words are reused */
+            row = next;
+            continue;
+        }
+        /* e_j; blocks wholly past the last column that is not -inf are
+         * zero */
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            if (wave * 256U * Q + 256U * j < last) {
+                v[j].x = m3_expf_with_table(v[j].x - m, exp_table);
+                v[j].y = m3_expf_with_table(v[j].y - m, exp_table);
+                v[j].z = m3_expf_with_table(v[j].z - m, exp_table);
+                v[j].w = m3_expf_with_table(v[j].w - m, exp_table);
+            } else {
+                v[j] = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+            }
+        }
+        /* e in LDS, in column order, for the segments the walk sums column
+         * by column; estimates: the F32 total of each segment (any
+         * order) */
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            *(float4 *)(values + first + 256U * j) = v[j];
+            const float t = m3_row16_sum_f32(((v[j].x + v[j].y) + v[j].z) +
+                                             v[j].w);
+
+            if ((lane & 15U) == 0U) {
+                segments[wave][j][drow] = t;
+            }
+        }
+        __syncthreads();
+        /* the estimated running sum at this wave's first column */
+        float before = 0.0F;
+
+        for (uint32_t i = lane; i < wave * Q * 4U; i += 64U) {
+            before += (&segments[0][0][0])[i];
+        }
+        before = m3_bits_f32(m3_wave_reduce(
+            m3_f32_bits(before), 0U, [](uint32_t x, uint32_t y) {
+                return m3_f32_bits(m3_bits_f32(x) + m3_bits_f32(y));
+            }));
+        /* per segment: the guessed binade (as the clamped exponent field
+         * E of s) and R, packed as (E << 24) | R; R = 0xFFFFFF marks a
+         * segment that must be summed column by column. The lanes of a DPP
+         * row form the same estimate from the same values. */
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const float s0 = segments[wave][j][0];
+            const float s1 = segments[wave][j][1];
+            const float s2 = segments[wave][j][2];
+            const float s3 = segments[wave][j][3];
+            float estimate = before;
+
+            estimate = drow > 0U ? estimate + s0 : estimate;
+            estimate = drow > 1U ? estimate + s1 : estimate;
+            estimate = drow > 2U ? estimate + s2 : estimate;
+            before = ((before + s0) + s1 + s2) + s3;
+            const uint32_t field = m3_f32_bits(estimate) >> 23U;
+            const uint32_t E = field < 1U ? 1U : field;
+            const int shift = 150 - (int)E;
+            const float f[4] = {__builtin_ldexpf(v[j].x, shift),
+                                __builtin_ldexpf(v[j].y, shift),
+                                __builtin_ldexpf(v[j].z, shift),
+                                __builtin_ldexpf(v[j].w, shift)};
+            /* r = RN_int(f) summed as F32 (exact below 2^24; a sum at or
+             * above 2^24 stays there and ends the segment's fast form); a
+             * tie (f - r = +-1/2) marks the segment */
+            float R = 0.0F;
+            bool mark = E > 150U;
+
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float r = __builtin_rintf(f[q]);
+
+                mark = mark || __builtin_fabsf(f[q] - r) == 0.5F;
+                R += r;
+            }
+            R = m3_row16_sum_f32(R);
+            const uint64_t marks = __ballot(mark);
+
+            mark = ((marks >> (16U * drow)) & 0xFFFFULL) != 0ULL ||
+                   !(R < 16777215.0F);
+            if ((lane & 15U) == 0U) {
+                words[wave * Q * 4U + 4U * j + drow] =
+                    (E << 24U) | (mark ? 0xFFFFFFU : (uint32_t)R);
+            }
+        }
+        __syncthreads();
+        /* The walk, by wave 0, over the 16 Q segments in column order (the
+         * segment t holds columns 64t .. 64t+63), 64 at a time, lane l
+         * holding segment 64 c + l. From the exact s, the segments whose
+         * guess matches s's binade and that are not marked form a run;
+         * prefix sums of their R give K at every segment end, and the run
+         * advances s in one step up to the first segment where K would
+         * reach 2^24. That segment, or the first one not in the run, is
+         * summed column by column; the next run starts after it. */
+        if (wave == 0U) {
+            uint32_t s = 0U;
+
+            /* the walk is the row's critical path: it goes first on its
+             * SIMD */
+            __builtin_amdgcn_s_setprio(3);
+
+            for (uint32_t chunk = 0U; chunk < (uint32_t)(NW * Q) / 16U;
+                 ++chunk) {
+                const uint32_t word = words[64U * chunk + lane];
+                const uint32_t guess = word >> 24U;
+                const uint32_t R = word & 0xFFFFFFU;
+                uint32_t t0 = 0U;
+
+                while (t0 < 64U) {
+                    const uint32_t field = s >> 23U;
+                    const uint32_t E = field < 1U ? 1U : field;
+                    const uint32_t base = (E - 1U) << 23U;
+                    const uint32_t K = s - base;
+                    const uint64_t from = ~0ULL << t0;
+                    const uint64_t good =
+                        __ballot(guess == E && R != 0xFFFFFFU) & from;
+                    const uint64_t bad = ~good & from;
+                    const uint32_t stop =
+                        bad != 0ULL ? (uint32_t)__builtin_ctzll(bad) : 64U;
+                    const uint32_t P = m3_wave_scan_u32(
+                        lane >= t0 && lane < stop ? R : 0U);
+                    const uint64_t over =
+                        __ballot(lane >= t0 && lane < stop &&
+                                 K + P >= 0x1000000U);
+                    const uint32_t cross =
+                        over != 0ULL ? (uint32_t)__builtin_ctzll(over) : stop;
+
+                    if (cross > t0) {
+                        s = base + K +
+                            (uint32_t)__builtin_amdgcn_readlane(
+                                (int)P, (int)(cross - 1U));
+                    }
+                    if (cross < 64U) {
+                        s = m3_segment_sum_sequential(
+                            s, values + 64U * (64U * chunk + cross));
+                        t0 = cross + 1U;
+                    } else {
+                        t0 = 64U;
+                    }
+                }
+            }
+            if (lane == 0U) {
+                carry = s;
+            }
+            __builtin_amdgcn_s_setprio(0);
+        }
+        __syncthreads();
+        const float sum = m3_bits_f32(m3_uniform_u32(carry));
+        const double inverse = 1.0 / (double)sum;
+
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t c = first + 256U * j;
+
+            if (c < width) {
+                m3_softmax_store4<F32IO>(out, c, out_dtype,
+                                         m3_softmax_scale4(v[j], inverse));
+            }
+        }
+        /* carry, segments and part_* are reused by the next row */
+        __syncthreads();
+        row = next;
+    }
+}
+
 typedef void (*m3_softmax_launcher)(dim3, hipStream_t, hipEvent_t,
                                     hipEvent_t, m3_softmax_args);
 
@@ -1452,6 +1847,51 @@ void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
     hipExtLaunchKernelGGL((m3_softmax_lane_rows_kernel<Q, FULL, F32IO>), grid,
                           dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
+
+/* The wide kernel's shape: NW waves per workgroup, Q float4 per lane; a
+ * row of up to 256 NW Q columns per workgroup. */
+constexpr int kWideWaves = 8;
+
+/* Workgroups of the wide kernel that one CU holds at once (from its
+ * register and LDS use), asked of the runtime once per instance. */
+template <int Q, bool F32IO>
+uint32_t m3_wide_per_cu()
+{
+    static const uint32_t blocks = [] {
+        constexpr uint32_t lds = 1024U * kWideWaves * Q;
+        int n = 0;
+
+        if (lds > 65536U) {
+            (void)hipFuncSetAttribute(
+                (const void *)m3_softmax_wide_kernel<Q, kWideWaves, F32IO>,
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        }
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, m3_softmax_wide_kernel<Q, kWideWaves, F32IO>,
+                64 * kWideWaves, lds) != hipSuccess ||
+            n < 1) {
+            (void)hipGetLastError();
+            n = 1;
+        }
+        return (uint32_t)n;
+    }();
+    return blocks;
+}
+
+/* The wide kernel's grid is what the device holds at once (each workgroup
+ * then loops over rows, the next row's loads in flight while it computes
+ * one), at most one workgroup per row. */
+template <int Q, bool F32IO>
+void m3_launch_wide(dim3 grid, hipStream_t stream, hipEvent_t start,
+                    hipEvent_t stop, m3_softmax_args args)
+{
+    hipExtLaunchKernelGGL((m3_softmax_wide_kernel<Q, kWideWaves, F32IO>),
+                          grid, dim3(64 * kWideWaves),
+                          1024U * kWideWaves * Q, stream, start, stop, 0U,
+                          args);
+}
+
+typedef uint32_t (*m3_wide_occupancy)();
 
 template <bool F32IO, bool VEC>
 void m3_launch_stream(dim3 grid, hipStream_t stream, hipEvent_t start,
@@ -1748,6 +2188,40 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
 
             return m3_hip_launch(
                 device, "m3_softmax_rows",
+                [&](hipEvent_t start, hipEvent_t stop) {
+                    launcher(grid, device->stream, start, stop, args);
+                },
+                message, capacity);
+        }
+        /* VEC rows of 2049..32768 columns: a workgroup per row at a time,
+         * each row read once, the in-order sum in parallel. */
+        if (vec && width > 2048U && width <= 32768U) {
+            /* Q float4 per lane, even, the smallest whose 2048 Q columns
+             * hold the row */
+#define M3_WIDE_ENTRY(Q)                                                      \
+    {{&m3_launch_wide<Q, false>, &m3_launch_wide<Q, true>},                   \
+     {&m3_wide_per_cu<Q, false>, &m3_wide_per_cu<Q, true>}}
+            static const struct {
+                m3_softmax_launcher launch[2];
+                m3_wide_occupancy occupancy[2];
+            } wide[] = {M3_WIDE_ENTRY(2),  M3_WIDE_ENTRY(4),
+                        M3_WIDE_ENTRY(6),  M3_WIDE_ENTRY(8),
+                        M3_WIDE_ENTRY(10), M3_WIDE_ENTRY(12),
+                        M3_WIDE_ENTRY(16)};
+#undef M3_WIDE_ENTRY
+            static const uint32_t wide_q[] = {2U, 4U, 6U, 8U, 10U, 12U, 16U};
+            uint32_t which = 0U;
+
+            while (2048U * wide_q[which] < width) {
+                ++which;
+            }
+            const uint64_t resident = (uint64_t)device->compute_units *
+                                      wide[which].occupancy[f32]();
+            const dim3 grid((uint32_t)(rows < resident ? rows : resident));
+            const m3_softmax_launcher launcher = wide[which].launch[f32];
+
+            return m3_hip_launch(
+                device, "m3_softmax_rows_wide",
                 [&](hipEvent_t start, hipEvent_t stop) {
                     launcher(grid, device->stream, start, stop, args);
                 },
