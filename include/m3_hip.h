@@ -298,6 +298,11 @@ int m3_hip_scan_views_static(m3_hip_device *device, const uint32_t *kinds,
 int m3_hip_synchronize(m3_hip_device *device, char *message,
                        size_t capacity);
 
+/* How many device and pinned host allocations this library has made in
+ * the process (every hipMalloc and hipHostMalloc it calls), for tests that
+ * show an entry point allocates nothing. No counterpart in the reference. */
+int m3_hip_allocation_count(uint64_t *count);
+
 /* How many times the host has waited for the device's stream (stream
  * synchronizations and completion polls, data-scan readbacks, blocking
  * copies) since the device was opened; for tests and measurement. No

@@ -563,7 +563,7 @@ void m3_launch_silu_vec(m3_hip_device *device, const m3_silu_vec_args &args,
 int m3_silu_table_build(m3_hip_device *device, char *message,
                         size_t capacity)
 {
-    int code = m3_hip_check(hipMalloc((void **)&device->silu_bf16_table,
+    int code = m3_hip_check((hipError_t)m3_hip_malloc((void **)&device->silu_bf16_table,
                                       kSiluTableEntries * sizeof(uint16_t)),
                             "hipMalloc(GATED_SILU table)", message, capacity);
 

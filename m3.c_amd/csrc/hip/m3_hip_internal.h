@@ -7,6 +7,7 @@
 
 #include "m3_hip.h"
 #include "m3_numeric.h"
+#include "m3_scratch_guard.h"
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
@@ -124,6 +125,11 @@ void m3_program_cache_release(m3_hip_device *device);
 int m3_silu_table_build(m3_hip_device *device, char *message,
                         size_t capacity);
 void m3_silu_table_release(m3_hip_device *device);
+
+/* hipMalloc and hipHostMalloc, counted (m3_hip_allocation_count); the
+ * hipError_t as an int. */
+int m3_hip_malloc(void **memory, size_t bytes);
+int m3_hip_host_malloc(void **memory, size_t bytes, unsigned int flags);
 
 /* Writes a formatted message into a caller buffer (which may be NULL). */
 int m3_hip_fail(char *message, size_t capacity, int code, const char *format,

@@ -182,6 +182,41 @@ constexpr int kScratchOrdinals = 64;
 /* scratch's address on device ordinal i, looked up at the first open of
  * that device (with the device current) */
 static void *m3_scratch_address[kScratchOrdinals];
+/* one m3_hip_scan_views_static call at a time per device */
+static m3_scratch_guard<kScratchOrdinals> m3_scratch_in_use;
+
+/* Device and pinned host allocations made by this library, counted so that
+ * tests can show an entry point allocates nothing. */
+static std::atomic<uint64_t> m3_allocations{0};
+
+int m3_hip_malloc(void **memory, size_t bytes)
+{
+    const hipError_t status = hipMalloc(memory, bytes);
+
+    if (status == hipSuccess) {
+        m3_allocations.fetch_add(1U, std::memory_order_relaxed);
+    }
+    return (int)status;
+}
+
+int m3_hip_host_malloc(void **memory, size_t bytes, unsigned int flags)
+{
+    const hipError_t status = hipHostMalloc(memory, bytes, flags);
+
+    if (status == hipSuccess) {
+        m3_allocations.fetch_add(1U, std::memory_order_relaxed);
+    }
+    return (int)status;
+}
+
+extern "C" int m3_hip_allocation_count(uint64_t *count)
+{
+    if (count == nullptr) {
+        return M3_HIP_INVALID;
+    }
+    *count = m3_allocations.load(std::memory_order_relaxed);
+    return M3_HIP_OK;
+}
 
 extern "C" int m3_hip_device_count(int *count, char *message,
                                    size_t capacity)
@@ -284,10 +319,11 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
                                                  hipStreamNonBlocking),
                         "hipStreamCreateWithFlags", message, capacity);
     if (code == M3_HIP_OK) {
-        code = m3_hip_check(hipHostMalloc((void **)&device->host_flags,
-                                          2U * kScanViews * sizeof(uint32_t),
-                                          hipHostMallocCoherent),
-                            "hipHostMalloc", message, capacity);
+        code = m3_hip_check(
+            (hipError_t)m3_hip_host_malloc((void **)&device->host_flags,
+                                           2U * kScanViews * sizeof(uint32_t),
+                                           hipHostMallocCoherent),
+            "hipHostMalloc", message, capacity);
     }
     if (code == M3_HIP_OK) {
         code = m3_silu_table_build(device, message, capacity);
@@ -297,8 +333,8 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
         return code;
     }
     /* optional: without it m3_hip_synchronize waits on the stream alone */
-    if (hipHostMalloc((void **)&device->done_word, 64U,
-                      hipHostMallocCoherent) == hipSuccess) {
+    if (m3_hip_host_malloc((void **)&device->done_word, 64U,
+                           hipHostMallocCoherent) == (int)hipSuccess) {
         __atomic_store_n(device->done_word, 0U, __ATOMIC_RELEASE);
     } else {
         (void)hipGetLastError();
@@ -450,7 +486,8 @@ extern "C" int m3_hip_arena_reserve(m3_hip_device *device, size_t byte_count,
     if (byte_count == 0U) {
         return M3_HIP_OK;
     }
-    code = m3_hip_check(hipMalloc(&memory, byte_count), "hipMalloc", message,
+    code = m3_hip_check((hipError_t)m3_hip_malloc(&memory, byte_count),
+                        "hipMalloc", message,
                         capacity);
     if (code != M3_HIP_OK) {
         return code;
@@ -1024,7 +1061,7 @@ static int m3_hip_scan_epoch(m3_hip_device *device, char *message,
     bool fresh = false;
 
     if (device->scan_flags == nullptr) {
-        code = m3_hip_check(hipMalloc((void **)&device->scan_flags,
+        code = m3_hip_check((hipError_t)m3_hip_malloc((void **)&device->scan_flags,
                                       kScanViews * sizeof(uint32_t)),
                             "hipMalloc(scan flags)", message, capacity);
         fresh = true;
@@ -1143,6 +1180,12 @@ extern "C" int m3_hip_scan_views_static(m3_hip_device *device,
                            "no static scan scratch on device %d",
                            device->ordinal);
     }
+    if (!m3_scratch_in_use.acquire(device->ordinal)) {
+        return m3_hip_fail(message, capacity, M3_HIP_UNSUPPORTED,
+                           "the static scan scratch of device %d is in use "
+                           "by another call",
+                           device->ordinal);
+    }
     /* other handles on this GPU share the words: start from zero, and
      * mark with epoch 1 */
     hipLaunchKernelGGL(m3_scan_clear_kernel, dim3(1), dim3(64), 0,
@@ -1150,11 +1193,13 @@ extern "C" int m3_hip_scan_views_static(m3_hip_device *device,
                        (uint32_t)count);
     code = m3_hip_check(hipGetLastError(), "m3_scan_clear", message,
                         capacity);
-    if (code != M3_HIP_OK) {
-        return code;
+    if (code == M3_HIP_OK) {
+        code = m3_hip_scan_into(device, device->static_scratch, 1U, kinds,
+                                views, count, flags, false, message,
+                                capacity);
     }
-    return m3_hip_scan_into(device, device->static_scratch, 1U, kinds, views,
-                            count, flags, false, message, capacity);
+    m3_scratch_in_use.release(device->ordinal);
+    return code;
 }
 
 /* ---- device-side gating of a command list ------------------------------ */
@@ -1186,7 +1231,7 @@ extern "C" int m3_hip_gate_open(m3_hip_device *device, char *message,
         return M3_HIP_OK; /* already open: the list keeps its gate */
     }
     if (device->gate_words == nullptr) {
-        code = m3_hip_check(hipMalloc((void **)&device->gate_words,
+        code = m3_hip_check((hipError_t)m3_hip_malloc((void **)&device->gate_words,
                                       2U * sizeof(uint32_t)),
                             "hipMalloc(gate words)", message, capacity);
         if (code == M3_HIP_OK) {
@@ -1199,9 +1244,9 @@ extern "C" int m3_hip_gate_open(m3_hip_device *device, char *message,
         }
     }
     if (device->host_gate == nullptr) {
-        code = m3_hip_check(hipHostMalloc((void **)&device->host_gate,
-                                          2U * sizeof(uint32_t),
-                                          hipHostMallocCoherent),
+        code = m3_hip_check((hipError_t)m3_hip_host_malloc(
+                                (void **)&device->host_gate,
+                                2U * sizeof(uint32_t), hipHostMallocCoherent),
                             "hipHostMalloc(gate report)", message, capacity);
         if (code != M3_HIP_OK) {
             device->host_gate = nullptr;
