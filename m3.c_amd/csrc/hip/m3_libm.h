@@ -611,7 +611,7 @@ M3_HD float m3_expm1f_tanh(float v)
  * wherever its result is used (numerator 2 or at least 2^-54 in
  * magnitude, denominator in [1.1, 2^64)). Same bits as m3_tanhf for every
  * input. */
-M3_HD float m3_tanhf_uniform(float x)
+M3_HD float m3_tanhf_straight(float x)
 {
     const uint32_t jx = m3_f32_bits(x);
     const uint32_t ix = jx & 0x7fffffffU;
@@ -639,6 +639,100 @@ M3_HD float m3_tanhf_uniform(float x)
         if (ix > 0x7f800000U) {
             z = m3_bits_f32(jx | 0x00400000U);
         }
+    }
+    return z;
+}
+
+/* tanhf on its common domain, 2^-55 <= |x| < 0x1.f310e4p+2, where the
+ * expm1f argument v = +-2|x| reduces with k <= 22: (v in [2, 15.6) for
+ * |x| >= 1, k in [3, 22]; v in (-2, -2^-54] below, k in [-3, 0]).
+ * The same operations as m3_tanhf_straight, arranged to share work:
+ *   - k is round(v / ln2) as expm1f forms it for |v| >= 1.5 ln2, for every
+ *     v here; on the ranges where expm1f fixes k = 0 or k = -1 instead,
+ *     the rounded form gives the same k (and, at the one v, -0x1.62e43p-2,
+ *     where it gives -1 for 0, the k = -1 reconstruction gives the same
+ *     bits), so no selection of k is needed;
+ *   - k ln2_hi is exact (ln2_hi has 17 significant bits, |k| < 64), so
+ *     v - k ln2_hi is one fused operation with the same result;
+ *   - with c = 0 (k = 0) expm1f's x * (e - c) - c - hxs is x * e - hxs,
+ *     so its k = 0 result x - (x * e - hxs) is d = x - f, the value every
+ *     other reconstruction starts from: 0.5 (x - f) - 0.5 (k = -1, with
+ *     0.5 d exact, one fused operation), 1 - (f - x) = 1 + d (k <= -2,
+ *     then scaled by 2^k and less 1) and (1 - 2^-k) - (f - x) (3 <= k <=
+ *     22, then scaled by 2^k).
+ * Every input of the domain gives m3_tanhf's bits (checked against the C
+ * library on all of them on the host, and on the device with the one-step
+ * divisions, whose operands here are m3_tanhf_straight's). */
+M3_HD float m3_tanhf_common(float x)
+{
+    const float ln2_hi = 6.9313812256e-01F;
+    const float ln2_lo = 9.0580006145e-06F;
+    const float invln2 = 1.4426950216e+00F;
+    const float q1 = -3.3333335072e-02F;
+    const float q2 = 1.5873016091e-03F;
+    const float q3 = -7.9365076090e-05F;
+    const float q4 = 4.0082177293e-06F;
+    const float q5 = -2.0109921195e-07F;
+    const uint32_t jx = m3_f32_bits(x);
+    const uint32_t ix = jx & 0x7fffffffU;
+    const int big = ix >= 0x3f800000U;
+    /* |x| clamped at 22 on its bits, so that the lanes outside the domain
+     * (their results are replaced) keep k in range */
+    const float magnitude = m3_bits_f32(ix < 0x41b00000U ? ix : 0x41b00000U);
+    const float v = (big ? 2.0F : -2.0F) * magnitude;
+    /* +-0.5 with v's sign */
+    const float half = m3_bits_f32(0x3f000000U | (m3_f32_bits(v) &
+                                                  0x80000000U));
+    const int32_t k = (int32_t)(invln2 * v + half);
+    const float kf = (float)k;
+    const float hi = fmaf(-kf, ln2_hi, v);
+    const float lo = kf * ln2_lo;
+    const float r = hi - lo;
+    const float c = (hi - r) - lo;
+    const float hfx = 0.5F * r;
+    const float hxs = r * hfx;
+    const float r1 =
+        1.0F + hxs * (q1 + hxs * (q2 + hxs * (q3 + hxs * (q4 + hxs * q5))));
+    const float t = 3.0F - r1 * hfx;
+    const float e = hxs * m3_div_one_step(r1 - t, 6.0F - r * t);
+    float f = r * (e - c) - c;
+
+    f -= hxs;
+    const float d = r - f;
+    /* 1 - 2^-k for k >= 3 and 1 for k <= -2 (the shift by 32 + k leaves
+     * nothing; k = 0 and k = -1 do not use it), scaled by 2^k on the
+     * bits */
+    const float base =
+        m3_bits_f32(0x3f800000U - (0x1000000U >> ((uint32_t)k & 31U)));
+    const float scaled =
+        m3_bits_f32(m3_f32_bits(base + d) + ((uint32_t)k << 23U));
+    const float outer = scaled - 1.0F;
+    const float em1 = big ? scaled
+                      : k < -1 ? outer
+                      : k == -1 ? fmaf(0.5F, d, -0.5F)
+                                : d;
+    const float q = m3_div_one_step(big ? 2.0F : -em1, em1 + 2.0F);
+    const float z = big ? 1.0F - q : q; /* +0 or positive */
+
+    /* z's magnitude with x's sign, as one bit-field insert */
+    return m3_bits_f32((m3_f32_bits(z) & 0x7fffffffU) |
+                       (jx & 0x80000000U));
+}
+
+/* The C library's tanhf for every input: m3_tanhf_common, and
+ * m3_tanhf_straight for the inputs outside its domain (|x| from 7.8 on,
+ * infinities and NaN, |x| below 2^-55), formed only in a wave that has
+ * such an input. */
+M3_HD float m3_tanhf_uniform(float x)
+{
+    const uint32_t ix = m3_f32_bits(x) & 0x7fffffffU;
+    const int rare = ix - 0x24000000U >= 0x40f98872U - 0x24000000U;
+    float z = m3_tanhf_common(x);
+
+    if (M3_ANY_LANE(rare)) {
+        const float straight = m3_tanhf_straight(x);
+
+        z = rare ? straight : z;
     }
     return z;
 }

@@ -25,7 +25,8 @@
  *       domain; sinf on all floats), the magnitude of
  *       m3_sinf_medium_magnitude with that of sinf where |x| < 120, and
  *       m3_expf_any, m3_expm1f, m3_tanhf and m3_tanhf_uniform with expf,
- *       expm1f and tanhf on all floats, and m3_gated_silu_bits (F32 gate)
+ *       expm1f and tanhf on the same floats and on the edges of
+ *       m3_tanhf_common's domain (m3_tanhf_common there too), and m3_gated_silu_bits (F32 gate)
  *       and m3_silu_quotient_fast (its quotient alone, NaN as a class)
  *       with the same statements in C on every stride-th gate, each with
  *       one of eight non-NaN up values (the product then has at most one
@@ -415,6 +416,41 @@ static int libm(uint64_t stride)
                                      ? !isnan(fast)
                                      : memcmp(&fast, &quotient,
                                               sizeof(fast)) != 0;
+            }
+        }
+    }
+    /* the edges of m3_tanhf_common's domain and of its choice of k (each
+     * with both signs and its neighbours): 2^-55, the first |x| with
+     * k >= 23, 1 (the two expm1f arguments), the one argument where the
+     * rounded k is -1 and expm1f's own is 0 (|x| = 0x1.62e43p-3), the end
+     * of expm1f's k = -1 range (|x| = 1.5 ln2 / 2), and 22 */
+    {
+        static const uint32_t edges[] = {0x24000000U, 0x40f98872U,
+                                         0x3f800000U, 0x3e317218U,
+                                         0x3e317219U, 0x3f051592U,
+                                         0x41b00000U};
+        unsigned e;
+
+        for (e = 0U; e < sizeof(edges) / sizeof(edges[0]); ++e) {
+            uint32_t d;
+
+            for (d = 0U; d < 6U; ++d) {
+                uint32_t b = (edges[e] + d - 2U) | ((d & 1U) << 31U);
+                float x;
+                float got;
+                float want;
+
+                memcpy(&x, &b, sizeof(x));
+                got = m3_tanhf_uniform(x);
+                want = tanhf(x);
+                other_checked += 1U;
+                tanhf_uniform_bad += memcmp(&got, &want, sizeof(got)) != 0;
+                if ((b & 0x7fffffffU) >= 0x24000000U &&
+                    (b & 0x7fffffffU) < 0x40f98872U) {
+                    got = m3_tanhf_common(x);
+                    tanhf_uniform_bad +=
+                        memcmp(&got, &want, sizeof(got)) != 0;
+                }
             }
         }
     }
