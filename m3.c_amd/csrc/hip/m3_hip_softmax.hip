@@ -1487,12 +1487,12 @@ __device__ __forceinline__ uint32_t m3_wave_scan_u32(uint32_t x)
     return x;
 }
 
-/* Rows of up to 1024Q columns (VEC: aligned, a multiple of 4 wide), read
- * once: a workgroup of four waves holds one row in VGPRs, wave w the
- * contiguous quarter of columns [256Qw, 256Q(w+1)); lane l of a wave holds
- * columns 256j + 4l .. +3 of that quarter in block j (j < Q), and DPP row
- * r of the wave (lanes 16r..16r+15) holds the 64 columns 256j + 64r .. of
- * block j, a "segment". Columns past the width read -inf and give e = +0.
+/* Rows of up to 256 NW Q columns (VEC: aligned, a multiple of 4 wide),
+ * read once: a workgroup of NW waves holds one row in VGPRs, wave w the
+ * contiguous columns [256Qw, 256Q(w+1)); lane l of a wave holds columns
+ * 256j + 4l .. +3 of them in block j (j < Q), and DPP row r of the wave
+ * (lanes 16r..16r+15) holds the 64 columns 256j + 64r .. of block j, a
+ * "segment". Columns past the width read -inf and give e = +0.
  *
  * The reference's in-order sum s_{c+1} = RN(s_c + e_c) (src/m3_op_execute_
  * basic.c:124-180) is computed exactly without a chain of `width`
@@ -1513,7 +1513,7 @@ __device__ __forceinline__ uint32_t m3_wave_scan_u32(uint32_t x)
  * marked and ends inside the binade advances s by R in integer arithmetic;
  * any other segment (the first one, which starts at s = 0; one where s
  * crosses a power of two; a tie; a wrong guess) is summed column by column
- * in order (m3_row_sum_sequential). Both give the reference's bits; the
+ * in order (m3_segment_sum_sequential). Both give the reference's bits; the
  * guesses only decide how often the second form runs (about 3% of the
  * segments for softmax rows of 16,384 normal logits).
  *

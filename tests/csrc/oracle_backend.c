@@ -45,6 +45,11 @@ static int g_device_memory;
 /* When nonzero, the constructor makes nothing and returns this status, as
  * a GPU backend does on a machine without a usable device. */
 static int g_create_status;
+/* When nonzero, the list with this number (1 = the first one executed
+ * after the reset) runs its commands and then fails with g_fail_status, as
+ * a device error that surfaces when the list's completion is awaited. */
+static size_t g_fail_list_at;
+static int g_fail_status;
 static size_t g_host_to_device;
 static size_t g_device_to_host;
 
@@ -58,6 +63,7 @@ size_t oracle_backend_periodic(void);
 void oracle_backend_set_program_order(int decreasing);
 void oracle_backend_set_device_memory(int on);
 void oracle_backend_set_create_status(int status);
+void oracle_backend_fail_list_at(size_t list, int status);
 size_t oracle_backend_transfers(int to_device);
 m3_status oracle_backend_create(m3_backend **backend, m3_error *error);
 
@@ -73,11 +79,19 @@ void oracle_backend_reset(void)
     g_host_to_device = 0U;
     g_device_to_host = 0U;
     g_create_status = 0;
+    g_fail_list_at = 0U;
+    g_fail_status = 0;
 }
 
 void oracle_backend_set_create_status(int status)
 {
     g_create_status = status;
+}
+
+void oracle_backend_fail_list_at(size_t list, int status)
+{
+    g_fail_list_at = list;
+    g_fail_status = status;
 }
 
 void oracle_backend_set_program_order(int decreasing)
@@ -452,6 +466,12 @@ static m3_status execute(void *context, const m3_command *commands,
         }
     }
     g_list_count += 1U;
+    if (g_fail_list_at != 0U && g_list_count == g_fail_list_at) {
+        return m3_error_set(error, (m3_status)g_fail_status,
+                            "test backend: the device reported an error "
+                            "after list %zu",
+                            g_list_count);
+    }
     return M3_STATUS_OK;
 }
 

@@ -55,6 +55,8 @@ def backend_lib():
     fake.oracle_backend_periodic.restype = ctypes.c_size_t
     fake.oracle_backend_set_program_order.argtypes = [ctypes.c_int]
     fake.oracle_backend_set_create_status.argtypes = [ctypes.c_int]
+    fake.oracle_backend_fail_list_at.argtypes = [ctypes.c_size_t,
+                                                 ctypes.c_int]
     factory = ctypes.cast(fake.oracle_backend_create, ctypes.c_void_p)
     lib.m3_provider_set_gpu_factory.argtypes = [ctypes.c_void_p]
     lib.m3_provider_set_gpu_factory(factory)
@@ -298,6 +300,39 @@ def test_no_gpu_falls_back_to_the_cpu_provider(fake):
     fake.oracle_backend_set_create_status(0)
     assert _session_status(g)[0] == m3.OK
     g.free()
+
+
+def test_device_error_reported_by_its_run(fake):
+    """An error the device reports when a list's completion is awaited (the
+    HIP provider's stream wait or completion poll returns it from the
+    list's execute call, as M3_STATUS_INTERNAL with the runtime's text)
+    fails the m3_session_run that queued the list, with that status and
+    message, and leaves the session usable: the next run succeeds and gives
+    the exact result. This is the host side of the path; on the device an
+    error the stream records without stopping its work is seen by the
+    completion-word poll at most 63 completions later, and one that stops
+    the queue after the 1 ms poll limit, by the stream wait."""
+    g, x, y, constant = reference_graph()
+    session = m3.Session(g)
+    g.free()
+    data = np.array([1.0, 2.0, -3.0, 0.25], np.float32)
+    session.write(x, data)
+    session.run()
+    good = session.read(y, np.zeros(4, np.float32))
+    lists = fake.oracle_backend_lists()
+    fake.oracle_backend_fail_list_at(lists + 1, m3.INTERNAL)
+    with pytest.raises(m3.M3Error) as failure:
+        session.run()
+    assert failure.value.status == m3.INTERNAL
+    assert "the device reported an error" in failure.value.message
+    assert fake.oracle_backend_lists() == lists + 1
+    session.run()
+    out = session.read(y, np.zeros(4, np.float32))
+    assert np.array_equal(out.view(np.uint32), good.view(np.uint32))
+    expected = ((c_tanhf(data + constant) * constant).astype(np.float32)
+                + data).astype(np.float32)
+    assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
+    session.free()
 
 
 def test_reference_graph_kat_on_the_cpu_provider(fake):
