@@ -49,6 +49,17 @@ CACHE_DEFEAT_BYTES = 512 << 20  # input bytes between two runs of a session
 # but attaches no timing events, for runs under an external kernel
 # profiler (whose trace then gives the kernel durations)
 EVENTS = True
+# Host pause (seconds) before each run of the event-timed pass: the GPU
+# then idles that much longer before each run's first kernel, as it does
+# under a kernel profiler, which adds its own host work to every dispatch.
+PAUSE = 0.0
+
+
+def pause():
+    if PAUSE > 0.0:
+        end = time.perf_counter() + PAUSE
+        while time.perf_counter() < end:
+            pass
 METRIC = ("achieved HBM GB/s (% of MI355X peak) per op class; "
           "ms per m3_session_run")
 
@@ -229,6 +240,7 @@ class Workload:
         self.runs_before_timed = (max(warmup, len(self.sessions)) + steps +
                                   visits * len(self.sessions))
         for i in range(steps):
+            pause()
             self.sessions[i % len(self.sessions)].run()
         per_kernel = {}
         per_session = []
@@ -589,9 +601,13 @@ def main():
     parser.add_argument("--no-events", action="store_true",
                         help="no timing events in the timed pass (run it "
                              "under a kernel profiler for the durations)")
+    parser.add_argument("--pause-us", type=float, default=0.0,
+                        help="host pause before each run of the timed "
+                             "pass, in microseconds (default none)")
     args = parser.parse_args()
-    global EVENTS
+    global EVENTS, PAUSE
     EVENTS = not args.no_events
+    PAUSE = max(args.pause_us, 0.0) * 1e-6
     if args.gpus != 1:
         print("bench.py measures one GPU: this provider has no multi-GPU "
               "path (each op shards with zero exchange; see the design "
