@@ -287,7 +287,9 @@ int m3_hip_scan_views_collect(m3_hip_device *device, uint32_t ticket,
  * hipFree or other allocating routine and records no timing events. More
  * than M3_HIP_STATIC_SCAN_VIEWS views is M3_HIP_UNSUPPORTED. Every call on
  * one GPU, from any device handle, shares the array and clears the words
- * it uses first: calls that overlap on one GPU race. */
+ * it uses first; a host-side flag per GPU admits one call at a time, and a
+ * call made while another one on the same GPU has not returned is refused
+ * with M3_HIP_UNSUPPORTED ("in use by another call") instead of racing. */
 #define M3_HIP_STATIC_SCAN_VIEWS 64U
 int m3_hip_scan_views_static(m3_hip_device *device, const uint32_t *kinds,
                              const m3_hip_view *views, size_t count,
