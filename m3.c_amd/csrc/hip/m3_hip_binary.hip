@@ -23,7 +23,9 @@
  *   3. when both inputs classify and the output is contiguous and aligned,
  *      the vector kernel runs: each lane handles groups of 4 consecutive
  *      outputs with 16-byte (F32) or 8-byte (F16/BF16) loads and stores,
- *      two groups in flight per lane, grid-stride over the tensor;
+ *      two groups in flight per lane, grid-stride over the tensor; with
+ *      F32 operands and a tensor whose lanes are all resident at once, its
+ *      held form instead (all loads, then the stores after a timed wait);
  *      divisions by I and P use precomputed multiply-shift divisors;
  *   4. anything else runs the general kernel: per-element offsets from the
  *      coalesced stride table.
@@ -214,6 +216,76 @@ __global__ __launch_bounds__(256) void m3_binary_vec_kernel(m3_bin_vec_args a)
     }
 }
 
+/* Groups of four outputs per lane of the held form, and its workgroups
+ * per CU (120 VGPRs: four waves per SIMD, all resident at once). */
+constexpr int kHeldGroups = 12;
+constexpr uint32_t kHeldBlocksPerCu = 4U;
+/* Its wait before the stores, as a multiple of the time the launch's
+ * reads of its full operands take at 8 TB/s. Measured in bench.py on
+ * MUL x[8,1024,1536] * c[1536], alternating libraries on one box: 17.6-17.9
+ * us at 1.0 and 1.19 against 18.1-18.6 us with the streaming kernel (1.4:
+ * 18.5-18.8; eight groups per lane, whose workgroups were not all
+ * resident, 20-31 us). */
+constexpr double kBinaryHoldFactor = 1.1;
+
+/* The held form of the F32 vector kernel, for a launch whose workgroups
+ * are all resident at once: each lane loads its kHeldGroups groups of both
+ * operands, forms the results, and stores them only hold_ticks
+ * (s_memrealtime) after its start, so that the launch's writes do not
+ * compete with its reads still in flight. The wait is bounded by the
+ * clock; results are those of m3_binary_vec_kernel. */
+template <int OP, int K>
+__global__ __launch_bounds__(256) void m3_binary_held_kernel(
+    m3_bin_vec_args a, uint32_t hold_ticks)
+{
+    if (m3_gate_closed(a.list_gate)) {
+        return; /* a check earlier in the list failed */
+    }
+    const uint64_t start = __builtin_amdgcn_s_memrealtime();
+    const uint32_t first = blockIdx.x * kThreads * K + threadIdx.x;
+    uint4 left[K];
+    uint4 right[K];
+
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const uint32_t g = first + (uint32_t)k * kThreads;
+
+        if (g < a.groups) {
+            left[k] = m3_operand_load4<true>(a.left, g * 4U);
+            right[k] = m3_operand_load4<true>(a.right, g * 4U);
+        } else {
+            left[k] = make_uint4(0U, 0U, 0U, 0U);
+            right[k] = left[k];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        left[k].x = m3_binary_f32_bits(OP, left[k].x, right[k].x);
+        left[k].y = m3_binary_f32_bits(OP, left[k].y, right[k].y);
+        left[k].z = m3_binary_f32_bits(OP, left[k].z, right[k].z);
+        left[k].w = m3_binary_f32_bits(OP, left[k].w, right[k].w);
+    }
+    while (__builtin_amdgcn_s_memrealtime() - start < (uint64_t)hold_ticks) {
+        __builtin_amdgcn_s_sleep(2);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const uint32_t g = first + (uint32_t)k * kThreads;
+
+        if (g < a.groups) {
+            m3_store4<true>(a.out, M3N_F32, g * 4U, left[k]);
+        }
+    }
+    /* Tail: the last count % 4 elements. */
+    if (blockIdx.x == 0U && threadIdx.x < a.count - a.groups * 4U) {
+        uint32_t f = a.groups * 4U + threadIdx.x;
+
+        *(uint32_t *)(a.out + (uint64_t)f * 4U) = m3_binary_f32_bits(
+            OP, m3_operand_element<true>(a.left, f),
+            m3_operand_element<true>(a.right, f));
+    }
+}
+
 struct m3_bin_general_args {
     const uint8_t *left;
     const uint8_t *right;
@@ -368,10 +440,31 @@ int m3_launch_binary_op(m3_hip_device *device, const m3_hip_view *left,
                                              : vec.groups,
                                          kThreads * kUnroll, 16U);
 
+        const uint64_t held =
+            ((uint64_t)vec.groups + kThreads * kHeldGroups - 1U) /
+            (kThreads * kHeldGroups);
+        const bool hold = f32 && vec.groups != 0U &&
+                          device->wall_clock_khz != 0U &&
+                          held <= (uint64_t)device->compute_units *
+                                      kHeldBlocksPerCu;
+        /* the full operands' bytes (broadcast ones are read from cache) */
+        const double read_bytes =
+            4.0 * (double)vec.count *
+            (double)((vec.left.mode == M3_BIN_FULL) +
+                     (vec.right.mode == M3_BIN_FULL));
+        const uint32_t hold_ticks = (uint32_t)(
+            kBinaryHoldFactor * read_bytes / 8.0e6 *
+            (double)device->wall_clock_khz / 1000.0);
+
         return m3_hip_launch(
             device, names[OP],
             [&](hipEvent_t start, hipEvent_t stop) {
-                if (f32) {
+                if (hold) {
+                    hipExtLaunchKernelGGL(
+                        (m3_binary_held_kernel<OP, kHeldGroups>),
+                        dim3((uint32_t)held), dim3(kThreads), 0,
+                        device->stream, start, stop, 0U, vec, hold_ticks);
+                } else if (f32) {
                     hipExtLaunchKernelGGL((m3_binary_vec_kernel<OP, true>),
                                           dim3(blocks), dim3(kThreads), 0,
                                           device->stream, start, stop, 0U,

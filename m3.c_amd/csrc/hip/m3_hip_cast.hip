@@ -12,7 +12,9 @@
  *     narrowing of m3_numeric.h. NaN payloads follow the reference rules.
  * The output is contiguous. A contiguous, aligned input runs the vector
  * kernel (four elements per lane per group, two groups in flight, output
- * written with streaming stores);
+ * written with streaming stores), or, for the cheap conversions of a
+ * tensor whose lanes are all resident at once, its held form (all loads,
+ * then the stores after a timed wait);
  * strided inputs run a per-element kernel over the coalesced index space.
  */
 #include "m3_hip_internal.h"
@@ -226,11 +228,111 @@ __global__ __launch_bounds__(256) void m3_copy_bytes_kernel(
     }
 }
 
+/* Groups of four elements per lane of the held form. */
+constexpr int kHeldGroups = 8;
+/* Workgroups per CU that are all resident at once in the held form (its
+ * lanes take at most 64 VGPRs: eight waves per SIMD). */
+constexpr uint32_t kHeldBlocksPerCu = 8U;
+
+/* How long the held form of a conversion waits before its stores, as a
+ * multiple of the time the launch's reads take at 8 TB/s; 0 where it is
+ * not used. Measured in bench.py, alternating libraries on one box
+ * (4096 x 4096): F16 -> F32 and BF16 -> F32 16.7-17.1 us at 1.4 against
+ * 18.0-18.5 us with the streaming kernel (1.19: 17.1-17.5, 1.6: 17.5-17.8);
+ * F32 -> BF16 16.3-16.4 against 16.7-17.0 us at 1.19 (1.4: 18.1). F32 ->
+ * F16, whose conversion takes several times the instructions, measured
+ * slower held at every factor (19.6-21.4 against 17.2-17.4 us): its
+ * conversions, all after the loads, then delay the stores. */
+constexpr double m3_cast_hold_factor(uint32_t in, uint32_t out)
+{
+    return (in == M3N_F16 || in == M3N_BF16) && out == M3N_F32 ? 1.4
+           : in == M3N_F32 && out == M3N_BF16                  ? 1.19
+                                                                : 0.0;
+}
+
+/* The held form of the vector conversion, for a launch whose workgroups
+ * are all resident at once: each lane loads its kHeldGroups groups, forms
+ * their results, and stores them only hold_ticks (s_memrealtime) after its
+ * start, so that the launch's writes do not compete with its reads still
+ * in flight (HBM serves a phase of reads, then one of writes). The wait is
+ * bounded by the clock; results are those of m3_cast_vec_kernel. */
+template <uint32_t IN, uint32_t OUT, int K>
+__global__ __launch_bounds__(256) void m3_cast_held_kernel(
+    const uint8_t *input, uint8_t *output, uint64_t count, uint64_t groups,
+    uint32_t hold_ticks, m3_hip_gate gate)
+{
+    if (m3_gate_closed(gate)) {
+        return; /* a check earlier in the list failed */
+    }
+    const uint64_t start = __builtin_amdgcn_s_memrealtime();
+    using in_io = m3_vec_io<m3_size_of(IN)>;
+    using out_io = m3_vec_io<m3_size_of(OUT)>;
+    const typename in_io::type *in = (const typename in_io::type *)input;
+    typename out_io::type *out = (typename out_io::type *)output;
+    const uint64_t first = (uint64_t)blockIdx.x * kThreads * K + threadIdx.x;
+    typename out_io::type result[K];
+
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const uint64_t g = first + (uint64_t)k * kThreads;
+        uint4 v = make_uint4(0U, 0U, 0U, 0U);
+
+        if (g < groups) {
+            v = in_io::unpack(in_io::load(&in[g]));
+        }
+        result[k] = out_io::pack(make_uint4(m3_convert<IN, OUT>(v.x),
+                                            m3_convert<IN, OUT>(v.y),
+                                            m3_convert<IN, OUT>(v.z),
+                                            m3_convert<IN, OUT>(v.w)));
+    }
+    while (__builtin_amdgcn_s_memrealtime() - start < (uint64_t)hold_ticks) {
+        __builtin_amdgcn_s_sleep(2);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const uint64_t g = first + (uint64_t)k * kThreads;
+
+        if (g < groups) {
+            m3_stream_store(&out[g], result[k]);
+        }
+    }
+    if (blockIdx.x == 0U && threadIdx.x < count - groups * 4U) {
+        uint64_t f = groups * 4U + threadIdx.x;
+        uint32_t raw = m3_size_of(IN) == 4U
+                           ? ((const uint32_t *)input)[f]
+                           : (uint32_t)((const uint16_t *)input)[f];
+        uint32_t r = m3_convert<IN, OUT>(raw);
+
+        if (m3_size_of(OUT) == 4U) {
+            ((uint32_t *)output)[f] = r;
+        } else {
+            ((uint16_t *)output)[f] = (uint16_t)r;
+        }
+    }
+}
+
 template <uint32_t IN, uint32_t OUT>
 void m3_launch_cast_vec(m3_hip_device *device, const uint8_t *input,
                         uint8_t *output, uint64_t count, uint32_t blocks,
                         hipEvent_t start, hipEvent_t stop)
 {
+    constexpr double factor = m3_cast_hold_factor(IN, OUT);
+    const uint64_t groups = count / 4U;
+    const uint64_t held =
+        (groups + kThreads * kHeldGroups - 1U) / (kThreads * kHeldGroups);
+
+    if (factor > 0.0 && groups != 0U && device->wall_clock_khz != 0U &&
+        held <= (uint64_t)device->compute_units * kHeldBlocksPerCu) {
+        const double us = factor * (double)count * m3_size_of(IN) / 8.0e6;
+        const uint32_t ticks =
+            (uint32_t)(us * (double)device->wall_clock_khz / 1000.0);
+
+        hipExtLaunchKernelGGL((m3_cast_held_kernel<IN, OUT, kHeldGroups>),
+                              dim3((uint32_t)held), dim3(kThreads), 0,
+                              device->stream, start, stop, 0U, input, output,
+                              count, groups, ticks, device->gate);
+        return;
+    }
     hipExtLaunchKernelGGL((m3_cast_vec_kernel<IN, OUT>), dim3(blocks),
                           dim3(kThreads), 0, device->stream, start, stop, 0U,
                           input, output, count, count / 4U, device->gate);
