@@ -1544,8 +1544,44 @@ __device__ __forceinline__ float4 m3_wide_load(const uint8_t *in, uint32_t c,
                                    -INFINITY);
 }
 
+/* One wave's share of a row's reductions for the wide kernel: maximum,
+ * count of +inf and 1 + the last column that is not -inf over this lane's
+ * columns first + 256j .. +3, reduced across the wave and posted by lane 0
+ * into the workgroup's part arrays. */
+template <int Q>
+__device__ __forceinline__ void m3_wide_partials(const float4 (&x)[Q],
+                                                 uint32_t first,
+                                                 uint32_t lane,
+                                                 uint32_t wave,
+                                                 float *part_max,
+                                                 uint32_t *part_inf,
+                                                 uint32_t *part_last)
+{
+    float m = -INFINITY;
+    uint32_t infinities = 0U;
+    uint32_t last = 0U;
+
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+        const float t = fmaxf(fmaxf(x[j].x, x[j].y), fmaxf(x[j].z, x[j].w));
+
+        m = fmaxf(m, t);
+        infinities += (x[j].x == INFINITY) + (x[j].y == INFINITY) +
+                      (x[j].z == INFINITY) + (x[j].w == INFINITY);
+        last = t != -INFINITY ? first + 256U * j + 4U : last;
+    }
+    m = m3_wave_max(m);
+    infinities = m3_wave_sum(infinities);
+    last = m3_wave_max_u32(last);
+    if (lane == 0U) {
+        part_max[wave] = m;
+        part_inf[wave] = infinities;
+        part_last[wave] = last;
+    }
+}
+
 template <int Q, int NW, bool F32IO>
-__global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
+__global__ __launch_bounds__(64 * NW, Q <= 8 ? 4 : 2) void m3_softmax_wide_kernel(
     m3_softmax_args a)
 {
     if (m3_gate_closed(a.list_gate)) {
@@ -1584,6 +1620,11 @@ __global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
                                            in_dtype);
         }
     }
+    /* the first row's reductions; each later row's run while the walk of
+     * the row before it does */
+    m3_wide_partials<Q>(ahead, first, lane, wave, part_max, part_inf,
+                        part_last);
+    __syncthreads();
     while (row < a.rows) {
         /* the per-block columns are recomputed each row, not kept live
          * across the loop */
@@ -1608,32 +1649,12 @@ __global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
             }
         }
         uint8_t *out = a.output + row * out_pitch;
-        /* maximum, +inf count, 1 + the last column that is not -inf */
-        float m = -INFINITY;
-        uint32_t infinities = 0U;
-        uint32_t last = 0U;
+        /* maximum, +inf count, 1 + the last column that is not -inf, from
+         * the waves' parts (posted before the last barrier) */
+        float m = part_max[0];
+        uint32_t infinities = part_inf[0];
+        uint32_t last = part_last[0];
 
-#pragma unroll
-        for (int j = 0; j < Q; ++j) {
-            const float t = fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w));
-
-            m = fmaxf(m, t);
-            infinities += (v[j].x == INFINITY) + (v[j].y == INFINITY) +
-                          (v[j].z == INFINITY) + (v[j].w == INFINITY);
-            last = t != -INFINITY ? first + 256U * j + 4U : last;
-        }
-        m = m3_wave_max(m);
-        infinities = m3_wave_sum(infinities);
-        last = m3_wave_max_u32(last);
-        if (lane == 0U) {
-            part_max[wave] = m;
-            part_inf[wave] = infinities;
-            part_last[wave] = last;
-        }
-        __syncthreads();
-        m = part_max[0];
-        infinities = part_inf[0];
-        last = part_last[0];
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
             m = fmaxf(m, part_max[w]);
@@ -1661,7 +1682,12 @@ __global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
                     m3_softmax_store4<F32IO>(out, c, out_dtype, p);
                 }
             }
-            __syncthreads(); /* the part_* words are reused */
+            __syncthreads(); /* every wave has read the part_* words */
+            if (next < a.rows) {
+                m3_wide_partials<Q>(ahead, first, lane, wave, part_max,
+                                    part_inf, part_last);
+            }
+            __syncthreads();
             row = next;
             continue;
         }
@@ -1769,6 +1795,11 @@ __global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
                 const uint32_t word = words[64U * chunk + lane];
                 const uint32_t guess = word >> 24U;
                 const uint32_t R = word & 0xFFFFFFU;
+                /* prefix sums of R over the chunk, once: a run from t0
+                 * reaches K + P - P[t0 - 1] at the end of segment l (in
+                 * unsigned arithmetic, so that marked segments before t0
+                 * cancel; each sum is below 2^30) */
+                const uint32_t P = m3_wave_scan_u32(R);
                 uint32_t t0 = 0U;
 
                 while (t0 < 64U) {
@@ -1776,24 +1807,27 @@ __global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
                     const uint32_t E = field < 1U ? 1U : field;
                     const uint32_t base = (E - 1U) << 23U;
                     const uint32_t K = s - base;
+                    const uint32_t offset =
+                        t0 == 0U ? 0U
+                                 : (uint32_t)__builtin_amdgcn_readlane(
+                                       (int)P, (int)(t0 - 1U));
                     const uint64_t from = ~0ULL << t0;
                     const uint64_t good =
                         __ballot(guess == E && R != 0xFFFFFFU) & from;
                     const uint64_t bad = ~good & from;
                     const uint32_t stop =
                         bad != 0ULL ? (uint32_t)__builtin_ctzll(bad) : 64U;
-                    const uint32_t P = m3_wave_scan_u32(
-                        lane >= t0 && lane < stop ? R : 0U);
                     const uint64_t over =
                         __ballot(lane >= t0 && lane < stop &&
-                                 K + P >= 0x1000000U);
+                                 K + (P - offset) >= 0x1000000U);
                     const uint32_t cross =
                         over != 0ULL ? (uint32_t)__builtin_ctzll(over) : stop;
 
                     if (cross > t0) {
                         s = base + K +
-                            (uint32_t)__builtin_amdgcn_readlane(
-                                (int)P, (int)(cross - 1U));
+                            ((uint32_t)__builtin_amdgcn_readlane(
+                                 (int)P, (int)(cross - 1U)) -
+                             offset);
                     }
                     if (cross < 64U) {
                         s = m3_segment_sum_sequential(
@@ -1809,6 +1843,13 @@ __global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
             }
             __builtin_amdgcn_s_setprio(0);
         }
+        /* the next row's reductions: the other waves while wave 0 walks
+         * (its loads have been in flight since this row began), wave 0
+         * after the walk */
+        if (next < a.rows) {
+            m3_wide_partials<Q>(ahead, first, lane, wave, part_max,
+                                part_inf, part_last);
+        }
         __syncthreads();
         const float sum = m3_bits_f32(m3_uniform_u32(carry));
         const double inverse = 1.0 / (double)sum;
@@ -1822,8 +1863,9 @@ __global__ __launch_bounds__(64 * NW) void m3_softmax_wide_kernel(
                                          m3_softmax_scale4(v[j], inverse));
             }
         }
-        /* carry, segments and part_* are reused by the next row */
-        __syncthreads();
+        /* carry is read before the next row's walk writes it (two
+         * barriers later), and values, segments and words are rewritten
+         * only after this barrier */
         row = next;
     }
 }
