@@ -321,8 +321,14 @@ void m3_launch_cast_vec(m3_hip_device *device, const uint8_t *input,
     const uint64_t held =
         (groups + kThreads * kHeldGroups - 1U) / (kThreads * kHeldGroups);
 
-    if (factor > 0.0 && groups != 0U && device->wall_clock_khz != 0U &&
-        held <= (uint64_t)device->compute_units * kHeldBlocksPerCu) {
+    const uint64_t slots =
+        (uint64_t)device->compute_units * kHeldBlocksPerCu;
+
+    /* held only when its workgroups fill at least half of what the device
+     * holds at once (few workgroups of eight groups per lane would leave
+     * most CUs idle) and fit in it */
+    if (factor > 0.0 && device->wall_clock_khz != 0U && 2U * held >= slots &&
+        held <= slots) {
         const double us = factor * (double)count * m3_size_of(IN) / 8.0e6;
         const uint32_t ticks =
             (uint32_t)(us * (double)device->wall_clock_khz / 1000.0);
