@@ -330,6 +330,23 @@ int m3_hip_host_waits(const m3_hip_device *device, uint64_t *waits);
  *   m3_hip_gate_close  waits for the stream once and ends the gating;
  *                      *failed_kind receives 0 when every check passed,
  *                      else 1 + the kind of the first failing check.
+ * A NaN check of a program's output can also be made by the program as it
+ * stores it, in place of m3_hip_gate_check's scan:
+ *   m3_hip_launch_program_checked  launches the program like
+ *                      m3_hip_launch_program; when a gate is open, `kind`
+ *                      is M3_HIP_SCAN_NAN and `checked` is the whole of an
+ *                      operand that the program stores once (contiguous,
+ *                      its address, dtype and element count), the program
+ *                      also records whether a value it stores there is NaN
+ *                      and *fused receives 1, else 0 (then queue the check
+ *                      with m3_hip_gate_check as usual);
+ *   m3_hip_gate_pending  with `armed` 1, every command kernel launched
+ *                      until the call with 0 returns at its start, closing
+ *                      the gate, when the last fused check found a NaN:
+ *                      arm it around the launches of the command whose
+ *                      input was checked (the command right after the
+ *                      program), which gives the order of a failing
+ *                      m3_hip_gate_check queued before that command.
  * No counterpart in the reference's backend interface. */
 int m3_hip_gate_open(m3_hip_device *device, char *message, size_t capacity);
 int m3_hip_gate_check(m3_hip_device *device, uint32_t kind,
@@ -337,6 +354,13 @@ int m3_hip_gate_check(m3_hip_device *device, uint32_t kind,
                       size_t capacity);
 int m3_hip_gate_close(m3_hip_device *device, uint32_t *failed_kind,
                       char *message, size_t capacity);
+int m3_hip_launch_program_checked(m3_hip_device *device,
+                                  const uint32_t *words,
+                                  const void *device_words, size_t word_count,
+                                  uint32_t kind, const m3_hip_view *checked,
+                                  int *fused, char *message, size_t capacity);
+int m3_hip_gate_pending(m3_hip_device *device, int armed, char *message,
+                        size_t capacity);
 
 /* Measurement support: with `enabled` 1, every launch is bracketed by HIP
  * events on the device stream and each run waits on the stream (not on the

@@ -202,6 +202,7 @@ EXPORTS_HIP = [
     "m3_hip_prepare_program", "m3_hip_scan_views_static",
     "m3_hip_scan_views_begin", "m3_hip_scan_views_collect",
     "m3_hip_gate_open", "m3_hip_gate_check", "m3_hip_gate_close",
+    "m3_hip_launch_program_checked", "m3_hip_gate_pending",
     "m3_hip_host_waits", "m3_hip_allocation_count",
 ]
 

@@ -44,15 +44,43 @@ constexpr size_t kTimingSamples = 4096U;
  * stores there (m3_hip_gate_check). word == nullptr: no gate, one uniform
  * branch on a kernel argument. */
 struct m3_hip_gate {
-    const uint32_t *word;
+    uint32_t *word;
     uint32_t epoch;
+    /* The check of this command's input that its producer made as it
+     * stored it (m3_hip_launch_program_checked): *pending holds
+     * pending_epoch when it found an offending value. The command then
+     * closes the gate itself, reports the failure as a failing check does
+     * (report[1] = kind, report[0] = epoch) and returns. pending ==
+     * nullptr: none. */
+    uint32_t *pending;
+    uint32_t pending_epoch;
+    uint32_t *report;
+    uint32_t kind;
 };
 
 __device__ __forceinline__ bool m3_gate_closed(const m3_hip_gate &gate)
 {
-    return gate.word != nullptr &&
-           __hip_atomic_load(gate.word, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT) == gate.epoch;
+    if (gate.word == nullptr) {
+        return false;
+    }
+    if (__hip_atomic_load(gate.word, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT) == gate.epoch) {
+        return true;
+    }
+    if (gate.pending == nullptr ||
+        __hip_atomic_load(gate.pending, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT) != gate.pending_epoch) {
+        return false;
+    }
+    /* every wave of the command stores the same words */
+    __hip_atomic_store(gate.word, gate.epoch, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&gate.report[1], gate.kind, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(&gate.report[0], gate.epoch, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+    __threadfence_system();
+    return true;
 }
 
 struct m3_hip_device {
@@ -90,6 +118,10 @@ struct m3_hip_device {
     uint32_t *host_gate;
     uint32_t gate_epoch;
     uint32_t gate_scan_epoch;
+    /* the check the last m3_hip_launch_program_checked made (its flag
+     * epoch and kind), armed on the gate by m3_hip_gate_pending */
+    uint32_t fused_epoch;
+    uint32_t fused_kind;
     /* how many times the host has waited for the stream (synchronize,
      * scan readback, blocking copies) since the device was opened */
     uint64_t host_waits;
@@ -137,6 +169,11 @@ int m3_hip_fail(char *message, size_t capacity, int code, const char *format,
 /* Maps a HIP error to an m3_hip_code with a message naming `what`. */
 int m3_hip_check(hipError_t status, const char *what, char *message,
                  size_t capacity);
+
+/* The epoch the next check of the open gate stores into its flag word
+ * (gate word 1) when it fails (m3_hip_runtime.hip). */
+int m3_hip_gate_flag_epoch(m3_hip_device *device, uint32_t *epoch,
+                           char *message, size_t capacity);
 
 /* Timing of one kernel launch: when timing is on, begin hands out a pair of
  * events for the dispatch and end queues them for folding (no-ops when

@@ -1266,8 +1266,51 @@ extern "C" int m3_hip_gate_open(m3_hip_device *device, char *message,
         }
         __atomic_store_n(&device->host_gate[0], 0U, __ATOMIC_RELEASE);
     }
+    device->gate = m3_hip_gate{};
     device->gate.word = device->gate_words;
     device->gate.epoch = device->gate_epoch;
+    return M3_HIP_OK;
+}
+
+/* The next epoch of the open gate's check flag (word 1): each check of a
+ * list stores its own epoch there when it fails. When the epochs wrap the
+ * word is cleared again. */
+int m3_hip_gate_flag_epoch(m3_hip_device *device, uint32_t *epoch,
+                           char *message, size_t capacity)
+{
+    device->gate_scan_epoch += 1U;
+    if (device->gate_scan_epoch == 0U) {
+        device->gate_scan_epoch = 1U;
+        const int code = m3_hip_gate_clear(device, 1U, 1U, message, capacity);
+
+        if (code != M3_HIP_OK) {
+            return code;
+        }
+    }
+    *epoch = device->gate_scan_epoch;
+    return M3_HIP_OK;
+}
+
+extern "C" int m3_hip_gate_pending(m3_hip_device *device, int armed,
+                                   char *message, size_t capacity)
+{
+    if (device == nullptr) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "device is null");
+    }
+    if (!armed) {
+        device->gate.pending = nullptr;
+        return M3_HIP_OK;
+    }
+    if (device->gate.word == nullptr || device->fused_epoch == 0U) {
+        return m3_hip_fail(message, capacity, M3_HIP_INVALID,
+                           "no gate is open or no check was fused");
+    }
+    device->gate.pending = device->gate_words + 1U;
+    device->gate.pending_epoch = device->fused_epoch;
+    device->gate.report = device->host_gate;
+    device->gate.kind = device->fused_kind;
+    device->fused_epoch = 0U;
     return M3_HIP_OK;
 }
 
@@ -1287,20 +1330,17 @@ extern "C" int m3_hip_gate_check(m3_hip_device *device, uint32_t kind,
         return m3_hip_fail(message, capacity, M3_HIP_INVALID,
                            "no gate is open on this device");
     }
-    device->gate_scan_epoch += 1U;
-    if (device->gate_scan_epoch == 0U) {
-        device->gate_scan_epoch = 1U;
-        code = m3_hip_gate_clear(device, 1U, 1U, message, capacity);
-        if (code != M3_HIP_OK) {
-            return code;
-        }
+    uint32_t epoch = 0U;
+
+    code = m3_hip_gate_flag_epoch(device, &epoch, message, capacity);
+    if (code != M3_HIP_OK) {
+        return code;
     }
     const m3_scan_gate gate = {device->gate_words, device->host_gate,
                                device->gate.epoch, kind};
 
-    return m3_hip_scan_launch(device, device->gate_words + 1U,
-                              device->gate_scan_epoch, kind, view, gate,
-                              message, capacity);
+    return m3_hip_scan_launch(device, device->gate_words + 1U, epoch, kind,
+                              view, gate, message, capacity);
 }
 
 extern "C" int m3_hip_gate_close(m3_hip_device *device,
@@ -1317,8 +1357,8 @@ extern "C" int m3_hip_gate_close(m3_hip_device *device,
     }
     const uint32_t epoch = device->gate.epoch;
 
-    device->gate.word = nullptr;
-    device->gate.epoch = 0U;
+    device->gate = m3_hip_gate{};
+    device->fused_epoch = 0U;
     int code = m3_hip_synchronize(device, message, capacity);
 
     if (code != M3_HIP_OK) {

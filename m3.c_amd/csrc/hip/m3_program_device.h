@@ -159,6 +159,20 @@ m3_program_load(const unsigned int *operands, unsigned int index,
     return v;
 }
 
+/* 1 when a value that the store of group g writes is NaN: all four of a
+ * whole group, the first count - 4g of the last, partial one (whose other
+ * lanes are not stored). */
+template <bool FULL>
+__device__ __forceinline__ unsigned int m3_program_nan4(
+    m3_program_f32x4 v, unsigned long long g, unsigned long long count)
+{
+    const unsigned long long first = 4ULL * g;
+
+    return (v.x != v.x) | ((FULL || first + 1U < count) && v.y != v.y) |
+           ((FULL || first + 2U < count) && v.z != v.z) |
+           ((FULL || first + 3U < count) && v.w != v.w);
+}
+
 /* Stores are nontemporal for whole groups: program outputs are written
  * once and not read back by the launch. */
 template <bool FULL, unsigned int D>

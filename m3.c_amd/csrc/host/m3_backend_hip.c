@@ -700,6 +700,54 @@ static m3_status m3_hip_check_produced(m3_hip_backend_context *context,
                              : m3_hip_status(code, message, error);
 }
 
+/* The checked input of commands[index + 1] when commands[index] is an
+ * elementwise program that writes it and the check is a NaN check: the
+ * program can make that check as it stores the values
+ * (m3_hip_launch_program_checked). NULL otherwise. */
+static const m3_tensor_view *m3_hip_fusable_check(const m3_command *commands,
+                                                  size_t count, size_t index,
+                                                  uint32_t *kind)
+{
+    const m3_tensor_view *input;
+
+    if (commands[index].kind != M3_OP_ELEMENTWISE_PROGRAM ||
+        index + 1U >= count) {
+        return NULL;
+    }
+    input = m3_hip_checked_input(&commands[index + 1U], kind);
+    if (input == NULL || *kind != M3_HIP_SCAN_NAN ||
+        input->metadata.element_count == 0U ||
+        !m3_hip_writes(&commands[index], input->storage)) {
+        return NULL;
+    }
+    return input;
+}
+
+/* Launches the elementwise program `command` with the NaN check of
+ * `checked` made as it stores it when the program stores all of it
+ * (*fused = true), else plainly (*fused = false). */
+static int m3_hip_enqueue_checked(m3_hip_backend_context *context,
+                                  const m3_command *command,
+                                  const m3_tensor_view *checked,
+                                  uint32_t kind, bool *fused, char *message,
+                                  size_t capacity)
+{
+    const m3_op_elementwise_program *program =
+        &command->descriptor.elementwise_program;
+    m3_hip_view view;
+    int made = 0;
+    int code;
+
+    m3_hip_view_of(checked, &view);
+    code = m3_hip_launch_program_checked(
+        context->device, program->words,
+        (const uint8_t *)m3_storage_handle_internal(program->storage) +
+            program->byte_offset,
+        program->word_count, kind, &view, &made, message, capacity);
+    *fused = code == M3_HIP_OK && made != 0;
+    return code;
+}
+
 static int m3_hip_enqueue(m3_hip_backend_context *context,
                           const m3_command *command, char *message,
                           size_t capacity)
@@ -785,6 +833,7 @@ static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
     size_t i;
     int code = M3_HIP_OK;
     bool gated = false;
+    bool fused = false; /* the command before checked this one's input */
 
     (void)scratch;
     context->settled = false;
@@ -793,13 +842,47 @@ static m3_status m3_hip_execute(void *opaque, const m3_command *commands,
         return status;
     }
     for (i = 0U; i < count && code == M3_HIP_OK; ++i) {
+        uint32_t kind = 0U;
+        const m3_tensor_view *checked;
+
+        if (fused) {
+            /* its check was made as the program before it stored the
+             * input: armed, its kernels close the gate instead of running
+             * when that check failed */
+            m3_hip_forget_outputs(context, &commands[i]);
+            code = m3_hip_gate_pending(context->device, 1, message,
+                                       sizeof(message));
+            if (code == M3_HIP_OK) {
+                const int run = m3_hip_enqueue(context, &commands[i],
+                                               message, sizeof(message));
+
+                code = m3_hip_gate_pending(context->device, 0, NULL, 0U);
+                code = run != M3_HIP_OK ? run : code;
+            }
+            fused = false;
+            continue;
+        }
         status = m3_hip_check_produced(context, commands, i, &gated, error);
         if (status != M3_STATUS_OK) {
             break;
         }
         m3_hip_forget_outputs(context, &commands[i]);
-        code = m3_hip_enqueue(context, &commands[i], message,
-                              sizeof(message));
+        checked = m3_hip_fusable_check(commands, count, i, &kind);
+        if (checked == NULL) {
+            code = m3_hip_enqueue(context, &commands[i], message,
+                                  sizeof(message));
+            continue;
+        }
+        if (!gated) {
+            code = m3_hip_gate_open(context->device, message,
+                                    sizeof(message));
+            gated = code == M3_HIP_OK;
+        }
+        if (code == M3_HIP_OK) {
+            code = m3_hip_enqueue_checked(context, &commands[i], checked,
+                                          kind, &fused, message,
+                                          sizeof(message));
+        }
     }
     if (gated) {
         /* the list's one host wait: the verdict of its produced checks */

@@ -198,3 +198,124 @@ def test_attention_pattern_full_size(gpu):
     session.free()
     expected = attention_oracle(scores, causal)
     assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
+
+
+def scaled_graph(shape, op):
+    """t = (x (op) w) + z, then SOFTMAX(t): the two elementwise nodes fuse
+    into one program that writes t (a graph output), and the program
+    checks the values it stores for NaN in place of a scan of t."""
+    g = m3.Graph()
+    x = g.add_value(m3.INPUT, m3.F32, shape)
+    w = g.add_value(m3.INPUT, m3.F32, shape)
+    z = g.add_value(m3.INPUT, m3.F32, shape)
+    t0 = g.add_inferred(op, [x, w], m3.TEMPORARY, m3.F32)
+    g.add_node(op, [x, w], [t0])
+    t = g.add_inferred(m3.OP_ADD, [t0, z], m3.OUTPUT, m3.F32)
+    g.add_node(m3.OP_ADD, [t0, z], [t])
+    y = g.add_inferred(m3.OP_SOFTMAX, [t], m3.OUTPUT, m3.F32)
+    g.add_node(m3.OP_SOFTMAX, [t], [y])
+    return g, x, w, z, t, y
+
+
+def run_scaled(shape, op, runs, timing=False):
+    """Runs the graph once per (x, w) pair of `runs`, with z = 0; returns,
+    per run, the failure (or None), t, the softmax output and the kernels
+    timed (when `timing`)."""
+    g, x, w, z, t, y = scaled_graph(shape, op)
+    session = m3.Session(g)
+    g.free()
+    session.write(z, np.zeros(shape, np.float32))
+    results = []
+    for xs, ws in runs:
+        session.write(x, xs)
+        session.write(w, ws)
+        if timing:
+            session.timing_enable(True)
+            session.timing_reset()
+        try:
+            session.run()
+            failure = None
+        except m3.M3Error as e:
+            failure = e
+        kernels = session.timing_read() if timing else {}
+        if timing:
+            session.timing_enable(False)
+        results.append((failure, session.read(t, np.zeros(shape, np.float32)),
+                        session.read(y, np.zeros(shape, np.float32)),
+                        kernels))
+    session.free()
+    return results
+
+
+def test_fused_check_passes_with_a_tail_lane_that_would_be_nan(gpu):
+    """15 elements: the program's last group has one lane past the end,
+    whose loads are not data; 0 / 0 there is not a stored value and must
+    not fail the check. The run passes, makes no separate scan, and both
+    outputs equal the oracle."""
+    print("gpu case gate fused_tail_clean", file=sys.stderr, flush=True)
+    shape = (3, 5)
+    rng = np.random.default_rng(11)
+    xs = (rng.random(shape) + 0.5).astype(np.float32)
+    ws = (rng.random(shape) + 0.5).astype(np.float32)
+    ((failure, tout, yout, kernels),) = run_scaled(shape, m3.OP_DIV,
+                                                   [(xs, ws)], timing=True)
+    assert failure is None, failure
+    assert not any(name.startswith("m3_scan_f32") or
+                   name.startswith("m3_scan_strided") for name in kernels), \
+        kernels
+    expected_t = (xs / ws).astype(np.float32) + np.float32(0.0)
+    assert np.array_equal(tout.view(np.uint32), expected_t.view(np.uint32))
+    for r in range(shape[0]):
+        assert np.array_equal(yout[r].view(np.uint32),
+                              softmax_oracle(expected_t[r]).view(np.uint32))
+
+
+@pytest.mark.parametrize("where", [0, 7, 14])
+def test_fused_check_fails_on_a_stored_nan(gpu, where):
+    """A NaN the program stores (0 / 0 at element `where`, the last one of
+    the partial group included) fails the run with OUT_OF_RANGE: the
+    program's output is written in full, the softmax output keeps what the
+    clean run before it wrote."""
+    print("gpu case gate fused_nan at", where, file=sys.stderr, flush=True)
+    shape = (3, 5)
+    xs = np.ones(shape, np.float32)
+    ws = np.full(shape, 2.0, np.float32)
+    bad_x = xs.copy()
+    bad_w = ws.copy()
+    bad_x.reshape(-1)[where] = 0.0
+    bad_w.reshape(-1)[where] = 0.0
+    clean, bad = run_scaled(shape, m3.OP_DIV, [(xs, ws), (bad_x, bad_w)])
+    assert clean[0] is None, clean[0]
+    failure, tout, yout, _ = bad
+    assert failure is not None and failure.status == m3.OUT_OF_RANGE
+    assert "NaN" in failure.message
+    flat = tout.reshape(-1)
+    assert math.isnan(flat[where])
+    assert np.all(np.delete(flat, where) == np.float32(0.5))
+    assert np.array_equal(yout.view(np.uint32), clean[2].view(np.uint32))
+
+
+def test_fused_check_large_program_output_written_in_full(gpu):
+    """A NaN early in a [64, 4096] program output: every group of the
+    program is still stored (its waves do not stop at the check), and the
+    softmax does not run."""
+    print("gpu case gate fused_large", file=sys.stderr, flush=True)
+    shape = (64, 4096)
+    rng = np.random.default_rng(12)
+    xs = rng.standard_normal(shape).astype(np.float32)
+    ws = rng.standard_normal(shape).astype(np.float32)
+    bad_x = xs.copy()
+    bad_w = ws.copy()
+    bad_x[0, 3] = np.inf
+    bad_w[0, 3] = 0.0  # inf * 0 = NaN
+    clean, bad = run_scaled(shape, m3.OP_MUL, [(xs, ws), (bad_x, bad_w)])
+    assert clean[0] is None, clean[0]
+    failure, tout, yout, _ = bad
+    assert failure is not None and failure.status == m3.OUT_OF_RANGE
+    with np.errstate(invalid="ignore"):
+        expected = (bad_x * bad_w).astype(np.float32) + np.float32(0.0)
+    assert math.isnan(tout[0, 3])
+    mask = ~np.isnan(expected)
+    assert np.array_equal(tout[mask].view(np.uint32),
+                          expected[mask].view(np.uint32))
+    assert np.array_equal(yout.view(np.uint32), clean[2].view(np.uint32))
