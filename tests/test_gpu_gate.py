@@ -11,6 +11,7 @@ semantics (every earlier output written, every later one untouched, the
 first failing check decides) and the single wait per run.
 """
 import math
+import os
 import sys
 
 import numpy as np
@@ -200,31 +201,63 @@ def test_attention_pattern_full_size(gpu):
     assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
 
 
-def scaled_graph(shape, op):
-    """t = (x (op) w) + z, then SOFTMAX(t): the two elementwise nodes fuse
-    into one program that writes t (a graph output), and the program
-    checks the values it stores for NaN in place of a scan of t."""
+class environment:
+    """Sets environment variables for the sessions created inside."""
+
+    def __init__(self, **values):
+        self.values = values
+        self.saved = {}
+
+    def __enter__(self):
+        for key, value in self.values.items():
+            self.saved[key] = os.environ.get(key)
+            os.environ[key] = value
+
+    def __exit__(self, *exc):
+        for key, value in self.saved.items():
+            if value is None:
+                del os.environ[key]
+            else:
+                os.environ[key] = value
+
+
+def scaled_graph(shape, op, f16):
+    """t = (x (op) w) + z, or CAST(x (op) w) to F16 with `f16`, then
+    SOFTMAX(t): the two elementwise nodes fuse into one program that writes
+    t (a graph output), and the program checks the values it stores for NaN
+    in place of a scan of t."""
     g = m3.Graph()
     x = g.add_value(m3.INPUT, m3.F32, shape)
     w = g.add_value(m3.INPUT, m3.F32, shape)
     z = g.add_value(m3.INPUT, m3.F32, shape)
     t0 = g.add_inferred(op, [x, w], m3.TEMPORARY, m3.F32)
     g.add_node(op, [x, w], [t0])
-    t = g.add_inferred(m3.OP_ADD, [t0, z], m3.OUTPUT, m3.F32)
-    g.add_node(m3.OP_ADD, [t0, z], [t])
+    if f16:
+        t = g.add_value(m3.OUTPUT, m3.F16, shape)
+        g.add_node(m3.OP_CAST, [t0], [t])
+    else:
+        t = g.add_inferred(m3.OP_ADD, [t0, z], m3.OUTPUT, m3.F32)
+        g.add_node(m3.OP_ADD, [t0, z], [t])
     y = g.add_inferred(m3.OP_SOFTMAX, [t], m3.OUTPUT, m3.F32)
     g.add_node(m3.OP_SOFTMAX, [t], [y])
     return g, x, w, z, t, y
 
 
-def run_scaled(shape, op, runs, timing=False):
-    """Runs the graph once per (x, w) pair of `runs`, with z = 0; returns,
-    per run, the failure (or None), t, the softmax output and the kernels
-    timed (when `timing`)."""
-    g, x, w, z, t, y = scaled_graph(shape, op)
+def run_scaled(shape, op, runs, timing=False, generated=True, f16=False):
+    """Runs the graph once per (x, w) pair of `runs`, with z = 0, the
+    program generated or interpreted; returns, per run, the failure (or
+    None), t (as float32), the softmax output and the kernels timed (when
+    `timing`)."""
+    with environment(M3_HIP_PROGRAM_JIT="1" if generated else "0"):
+        return _run_scaled(shape, op, runs, timing, f16)
+
+
+def _run_scaled(shape, op, runs, timing, f16):
+    g, x, w, z, t, y = scaled_graph(shape, op, f16)
     session = m3.Session(g)
     g.free()
     session.write(z, np.zeros(shape, np.float32))
+    out_type = np.uint16 if f16 else np.float32
     results = []
     for xs, ws in runs:
         session.write(x, xs)
@@ -240,29 +273,35 @@ def run_scaled(shape, op, runs, timing=False):
         kernels = session.timing_read() if timing else {}
         if timing:
             session.timing_enable(False)
-        results.append((failure, session.read(t, np.zeros(shape, np.float32)),
-                        session.read(y, np.zeros(shape, np.float32)),
-                        kernels))
+        traw = session.read(t, np.zeros(shape, out_type))
+        tout = traw.view(np.float16).astype(np.float32) if f16 else traw
+        yout = session.read(y, np.zeros(shape, np.float32))
+        results.append((failure, tout, yout, kernels))
     session.free()
     return results
 
 
-def test_fused_check_passes_with_a_tail_lane_that_would_be_nan(gpu):
+@pytest.mark.parametrize("generated", [True, False])
+def test_fused_check_passes_with_a_tail_lane_that_would_be_nan(gpu,
+                                                               generated):
     """15 elements: the program's last group has one lane past the end,
     whose loads are not data; 0 / 0 there is not a stored value and must
     not fail the check. The run passes, makes no separate scan, and both
     outputs equal the oracle."""
-    print("gpu case gate fused_tail_clean", file=sys.stderr, flush=True)
+    print("gpu case gate fused_tail_clean", generated, file=sys.stderr,
+          flush=True)
     shape = (3, 5)
     rng = np.random.default_rng(11)
     xs = (rng.random(shape) + 0.5).astype(np.float32)
     ws = (rng.random(shape) + 0.5).astype(np.float32)
-    ((failure, tout, yout, kernels),) = run_scaled(shape, m3.OP_DIV,
-                                                   [(xs, ws)], timing=True)
+    ((failure, tout, yout, kernels),) = run_scaled(
+        shape, m3.OP_DIV, [(xs, ws)], timing=True, generated=generated)
     assert failure is None, failure
     assert not any(name.startswith("m3_scan_f32") or
                    name.startswith("m3_scan_strided") for name in kernels), \
         kernels
+    assert ("m3_program" if generated else "m3_program_interpreted") in \
+        kernels, kernels
     expected_t = (xs / ws).astype(np.float32) + np.float32(0.0)
     assert np.array_equal(tout.view(np.uint32), expected_t.view(np.uint32))
     for r in range(shape[0]):
@@ -270,13 +309,16 @@ def test_fused_check_passes_with_a_tail_lane_that_would_be_nan(gpu):
                               softmax_oracle(expected_t[r]).view(np.uint32))
 
 
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("generated", [True, False])
 @pytest.mark.parametrize("where", [0, 7, 14])
-def test_fused_check_fails_on_a_stored_nan(gpu, where):
+def test_fused_check_fails_on_a_stored_nan(gpu, where, generated, f16):
     """A NaN the program stores (0 / 0 at element `where`, the last one of
-    the partial group included) fails the run with OUT_OF_RANGE: the
-    program's output is written in full, the softmax output keeps what the
-    clean run before it wrote."""
-    print("gpu case gate fused_nan at", where, file=sys.stderr, flush=True)
+    the partial group included; F32, or cast to F16 in the program) fails
+    the run with OUT_OF_RANGE: the program's output is written in full, the
+    softmax output keeps what the clean run before it wrote."""
+    print("gpu case gate fused_nan at", where, generated, f16,
+          file=sys.stderr, flush=True)
     shape = (3, 5)
     xs = np.ones(shape, np.float32)
     ws = np.full(shape, 2.0, np.float32)
@@ -284,7 +326,8 @@ def test_fused_check_fails_on_a_stored_nan(gpu, where):
     bad_w = ws.copy()
     bad_x.reshape(-1)[where] = 0.0
     bad_w.reshape(-1)[where] = 0.0
-    clean, bad = run_scaled(shape, m3.OP_DIV, [(xs, ws), (bad_x, bad_w)])
+    clean, bad = run_scaled(shape, m3.OP_DIV, [(xs, ws), (bad_x, bad_w)],
+                            generated=generated, f16=f16)
     assert clean[0] is None, clean[0]
     failure, tout, yout, _ = bad
     assert failure is not None and failure.status == m3.OUT_OF_RANGE
@@ -292,14 +335,16 @@ def test_fused_check_fails_on_a_stored_nan(gpu, where):
     flat = tout.reshape(-1)
     assert math.isnan(flat[where])
     assert np.all(np.delete(flat, where) == np.float32(0.5))
-    assert np.array_equal(yout.view(np.uint32), clean[2].view(np.uint32))
+    assert np.array_equal(yout.view(np.uint8), clean[2].view(np.uint8))
 
 
-def test_fused_check_large_program_output_written_in_full(gpu):
+@pytest.mark.parametrize("generated", [True, False])
+def test_fused_check_large_program_output_written_in_full(gpu, generated):
     """A NaN early in a [64, 4096] program output: every group of the
     program is still stored (its waves do not stop at the check), and the
     softmax does not run."""
-    print("gpu case gate fused_large", file=sys.stderr, flush=True)
+    print("gpu case gate fused_large", generated, file=sys.stderr,
+          flush=True)
     shape = (64, 4096)
     rng = np.random.default_rng(12)
     xs = rng.standard_normal(shape).astype(np.float32)
@@ -308,7 +353,8 @@ def test_fused_check_large_program_output_written_in_full(gpu):
     bad_w = ws.copy()
     bad_x[0, 3] = np.inf
     bad_w[0, 3] = 0.0  # inf * 0 = NaN
-    clean, bad = run_scaled(shape, m3.OP_MUL, [(xs, ws), (bad_x, bad_w)])
+    clean, bad = run_scaled(shape, m3.OP_MUL, [(xs, ws), (bad_x, bad_w)],
+                            generated=generated)
     assert clean[0] is None, clean[0]
     failure, tout, yout, _ = bad
     assert failure is not None and failure.status == m3.OUT_OF_RANGE
