@@ -1445,28 +1445,6 @@ __device__ __forceinline__ float m3_row16_sum_f32(float t)
     return t + m3_dpp_f32<0x140>(0.0F, t);
 }
 
-/* The left-to-right F32 sum continued over 64 consecutive values of LDS
- * starting at `line` (16-byte aligned): lane i of the first DPP row reads
- * values 4i..4i+3 and the running value passes from lane to lane
- * (row_ror:1), so that lane 15 holds the sum after the 64 values. The
- * other rows of the wave perform the same instructions on the same values;
- * only lane 15's result is read. */
-__device__ __forceinline__ uint32_t m3_segment_sum_sequential(
-    uint32_t s_bits, const float *line)
-{
-    const float4 e = *(const float4 *)(line + 4U * (threadIdx.x & 15U));
-    float t = m3_bits_f32(s_bits);
-
-#pragma unroll
-    for (int g = 0; g < 16; ++g) {
-        t = m3_dpp_f32<0x121>(0.0F, t) + e.x;
-        t = t + e.y;
-        t = t + e.z;
-        t = t + e.w;
-    }
-    return (uint32_t)__builtin_amdgcn_readlane((int)m3_f32_bits(t), 15);
-}
-
 /* Inclusive prefix sum over the 64 lanes of a wave (lane l gets the sum of
  * lanes 0..l): row_shr within the 16-lane rows, then row_bcast:15 and
  * row_bcast:31 across them. */
@@ -1488,11 +1466,12 @@ __device__ __forceinline__ uint32_t m3_wave_scan_u32(uint32_t x)
 }
 
 /* Rows of up to 256 NW Q columns (VEC: aligned, a multiple of 4 wide),
- * read once: a workgroup of NW waves holds one row in VGPRs, wave w the
- * contiguous columns [256Qw, 256Q(w+1)); lane l of a wave holds columns
- * 256j + 4l .. +3 of them in block j (j < Q), and DPP row r of the wave
- * (lanes 16r..16r+15) holds the 64 columns 256j + 64r .. of block j, a
- * "segment". Columns past the width read -inf and give e = +0.
+ * read once and written once (m3_softmax_wide_kernel): a workgroup of NW
+ * waves holds one row in VGPRs, wave w the contiguous columns [256Qw,
+ * 256Q(w+1)); lane l of a wave holds columns 256j + 4l .. +3 of them in
+ * block j (j < Q), and DPP row r of the wave (lanes 16r..16r+15) holds the
+ * 64 columns 256j + 64r .. of block j, a "segment". Columns past the width
+ * read -inf and give e = +0.
  *
  * The reference's in-order sum s_{c+1} = RN(s_c + e_c) (src/m3_op_execute_
  * basic.c:124-180) is computed exactly without a chain of `width`
@@ -1508,14 +1487,13 @@ __device__ __forceinline__ uint32_t m3_wave_scan_u32(uint32_t x)
  * estimate of the running sum (F32 totals of the segments before it) and
  * forms R = sum of r over its 64 columns, marking the segment when a
  * column is a tie or its r reaches 2^24. Then a walk over the segments in
- * column order (wave 0's, then 1's, ..., handed on through LDS) keeps the
- * exact s as bits: a segment whose guess matches the binade of s, is not
- * marked and ends inside the binade advances s by R in integer arithmetic;
- * any other segment (the first one, which starts at s = 0; one where s
- * crosses a power of two; a tie; a wrong guess) is summed column by column
- * in order (m3_segment_sum_sequential). Both give the reference's bits; the
- * guesses only decide how often the second form runs (about 3% of the
- * segments for softmax rows of 16,384 normal logits).
+ * column order keeps the exact s as bits: a segment whose guess matches
+ * the binade of s, is not marked and ends inside the binade advances s by
+ * R in integer arithmetic; any other segment (the first one, which starts
+ * at s = 0; one where s crosses a power of two; a tie; a wrong guess) is
+ * summed column by column in order (m3_segment_sum_lanes). Both give the
+ * reference's bits; the guesses only decide how often the second form runs
+ * (about 3% of the segments for softmax rows of 16,384 normal logits).
  *
  * The maximum, the count of +inf and the last column that is not -inf are
  * reduced across the workgroup first; blocks past that column skip the
@@ -1580,77 +1558,156 @@ __device__ __forceinline__ void m3_wide_partials(const float4 (&x)[Q],
     }
 }
 
-template <int Q, int NW, bool F32IO>
-__global__ __launch_bounds__(64 * NW, Q <= 8 ? 4 : 2) void m3_softmax_wide_kernel(
+
+/* The in-order sum continued over one 64-column segment whose values are
+ * in registers: lane i of each DPP row holds the segment's columns 4i ..
+ * 4i+3 in `e`; the running value passes from lane to lane (row_ror:1), so
+ * that lane 15 holds the sum after the 64 values (the other DPP rows repeat
+ * the same additions), and lane 15's result is returned. */
+__device__ __forceinline__ uint32_t m3_segment_sum_lanes(uint32_t s_bits,
+                                                         float4 e)
+{
+    float t = m3_bits_f32(s_bits);
+
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+        t = m3_dpp_f32<0x121>(0.0F, t) + e.x;
+        t = t + e.y;
+        t = t + e.z;
+        t = t + e.w;
+    }
+    return (uint32_t)__builtin_amdgcn_readlane((int)m3_f32_bits(t), 15);
+}
+
+/* Segments per row whose exponentials the wide kernel keeps in LDS. */
+constexpr uint32_t kWideSlots = 48U;
+/* Relative distance from a power of two within which an estimated running
+ * sum counts as possibly on the other side of it. The in-order F32 sum of
+ * n non-negative terms is within (n - 1) 2^-24 of the exact sum, relative,
+ * at most 2^-9 for n <= 32768; the estimates (F32 sums of F32 segment
+ * totals, fewer than 100 dependent additions) are within 2^-17 of it. So
+ * every segment where s crosses a power of two, or whose guessed binade
+ * differs from that of s, has an estimate within this margin of one. */
+constexpr float kWideMargin = 1.0F / 256.0F;
+
+/* Sum of x over the lanes below this one (lane 0: +0), in any order: the
+ * values shifted up one lane (wave_shr:1), then an inclusive scan through
+ * row_shr and row_bcast. */
+__device__ __forceinline__ float m3_wave_exclusive_sum_f32(float x)
+{
+    uint32_t b = (uint32_t)__builtin_amdgcn_update_dpp(
+        0, (int)m3_f32_bits(x), 0x138, 0xF, 0xF, false); /* wave_shr:1 */
+    float t = m3_bits_f32(b);
+
+    t = t + m3_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(
+                0, (int)m3_f32_bits(t), 0x111, 0xF, 0xF, false));
+    t = t + m3_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(
+                0, (int)m3_f32_bits(t), 0x112, 0xF, 0xF, false));
+    t = t + m3_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(
+                0, (int)m3_f32_bits(t), 0x114, 0xF, 0xF, false));
+    t = t + m3_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(
+                0, (int)m3_f32_bits(t), 0x118, 0xF, 0xF, false));
+    t = t + m3_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(
+                0, (int)m3_f32_bits(t), 0x142, 0xA, 0xF, false));
+    t = t + m3_bits_f32((uint32_t)__builtin_amdgcn_update_dpp(
+                0, (int)m3_f32_bits(t), 0x143, 0xC, 0xF, false));
+    return t;
+}
+
+/* The clamped exponent field of a non-negative F32 (1 for zero and the
+ * subnormals, whose ulp is that of the smallest binade). */
+__device__ __forceinline__ uint32_t m3_binade(float x)
+{
+    const uint32_t field = m3_f32_bits(x) >> 23U;
+
+    return field < 1U ? 1U : field;
+}
+
+/* The long-row kernel described above. One row per workgroup at a time,
+ * no loads ahead in registers and about 15 KB of LDS, so that four
+ * workgroups share a CU and one's walk overlaps the others' loads and
+ * exponentials. Each row goes through: the loads and the maximum (barrier),
+ * the exponentials and the segment totals (barrier), the words, each wave
+ * then posting a ready tag, the walk by wave 0, each 64-segment chunk as
+ * soon as the waves holding it have posted (barrier), the scale and the
+ * stores.
+ *
+ * The walk sums column by column only the first segment, the segments
+ * where s crosses a power of two, marked segments and segments whose
+ * guessed binade is wrong; all of these lie where the estimated running
+ * sum is within kWideMargin of a power of two at the segment's start or
+ * end, or crosses one inside it, or the segment is marked. The data waves
+ * stage exactly those segments' exponentials in kWideSlots LDS lines; a
+ * segment the walk needs that is not staged (more than kWideSlots
+ * candidates in the row) has its exponentials formed again from the input
+ * by the walking wave, the same expf of the same operands, so that the
+ * bits never depend on the prediction. */
+template <int Q, int NW, bool F32IO, int WAVES_PER_EU>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
     m3_softmax_args a)
 {
+    static_assert(4 * Q <= 64, "one segment of a wave per lane");
+    static_assert((NW * Q) % 16 == 0, "whole 64-segment chunks");
     if (m3_gate_closed(a.list_gate)) {
         return; /* a check earlier in the list failed */
     }
+    constexpr uint32_t kSegments = (uint32_t)(NW * Q * 4);
+    constexpr uint32_t kWaveSegments = (uint32_t)(4 * Q);
     __shared__ uint64_t exp_table[32];
     __shared__ float part_max[NW];
     __shared__ uint32_t part_inf[NW];
     __shared__ uint32_t part_last[NW];
-    __shared__ float segments[NW][Q][4];
-    __shared__ uint32_t words[NW * Q * 4];
+    __shared__ float totals[NW][kWaveSegments];
+    __shared__ uint32_t words[kSegments];
+    __shared__ uint8_t slot_of[kSegments];
+    __shared__ uint32_t ready[NW];
+    __shared__ uint32_t slot_count;
     __shared__ uint32_t carry;
-    extern __shared__ float values[]; /* e of the row, 256 NW Q floats */
-    const uint32_t lane = threadIdx.x & 63U;
-    const uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
-    const uint32_t drow = lane >> 4U;
+    __shared__ float4 staged[kWideSlots][16];
     const uint32_t width = a.width;
     const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
     const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
     const uint64_t out_pitch =
         (uint64_t)width * (out_dtype == M3N_F32 ? 4U : 2U);
-    /* first column of this lane in block 0 */
-    uint32_t first = wave * 256U * Q + 4U * lane;
-    uint64_t row = blockIdx.x;
-    float4 ahead[Q]; /* the next row's columns, loading */
+    uint32_t tag = 0U; /* rows this workgroup has begun */
 
     if (threadIdx.x < 32U) {
         exp_table[threadIdx.x] = m3_expf_table[threadIdx.x];
     }
-    {
-        const uint8_t *in = m3_softmax_row(a, row);
-
-#pragma unroll
-        for (int j = 0; j < Q; ++j) {
-            ahead[j] = m3_wide_load<F32IO>(in, first + 256U * j, width,
-                                           in_dtype);
-        }
+    if (threadIdx.x < (uint32_t)NW) {
+        ready[threadIdx.x] = 0U;
     }
-    /* the first row's reductions; each later row's run while the walk of
-     * the row before it does */
-    m3_wide_partials<Q>(ahead, first, lane, wave, part_max, part_inf,
-                        part_last);
-    __syncthreads();
-    while (row < a.rows) {
-        /* the per-block columns are recomputed each row, not kept live
-         * across the loop */
-        asm volatile("" : "+v"(first));
+    for (uint64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+        /* the lane's columns and masks are formed again each row, not kept
+         * live (in spilled registers) across the loop */
+        uint32_t thread = threadIdx.x;
+        uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
+
+        asm volatile("" : "+v"(thread));
+        asm volatile("" : "+s"(wave));
+        const uint32_t lane = thread & 63U;
+        const uint32_t drow = lane >> 4U;
+        /* first column of this lane in block 0 */
+        const uint32_t first = wave * 256U * Q + 4U * lane;
+        const uint8_t *in = m3_softmax_row(a, row);
+        uint8_t *out = a.output + row * out_pitch;
         float4 v[Q];
 
+        ++tag;
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
-            v[j] = ahead[j];
+            v[j] = m3_wide_load<F32IO>(in, first + 256U * j, width, in_dtype);
         }
-        const uint64_t next = row + gridDim.x;
-
-        /* the next row's loads go out now and arrive while this row is
-         * computed */
-        if (next < a.rows) {
-            const uint8_t *in = m3_softmax_row(a, next);
-
-#pragma unroll
-            for (int j = 0; j < Q; ++j) {
-                ahead[j] = m3_wide_load<F32IO>(in, first + 256U * j, width,
-                                               in_dtype);
-            }
+        /* maximum, +inf count and 1 + the last column that is not -inf
+         * (counting the +inf entries of every row, not only of rows whose
+         * maximum is +inf, keeps this kernel out of spilled registers) */
+        m3_wide_partials<Q>(v, first, lane, wave, part_max, part_inf,
+                            part_last);
+        if (threadIdx.x == 0U) {
+            slot_count = 0U;
         }
-        uint8_t *out = a.output + row * out_pitch;
-        /* maximum, +inf count, 1 + the last column that is not -inf, from
-         * the waves' parts (posted before the last barrier) */
+        __syncthreads();
         float m = part_max[0];
         uint32_t infinities = part_inf[0];
         uint32_t last = part_last[0];
@@ -1683,12 +1740,6 @@ __global__ __launch_bounds__(64 * NW, Q <= 8 ? 4 : 2) void m3_softmax_wide_kerne
                 }
             }
             __syncthreads(); /* every wave has read the part_* words */
-            if (next < a.rows) {
-                m3_wide_partials<Q>(ahead, first, lane, wave, part_max,
-                                    part_inf, part_last);
-            }
-            __syncthreads();
-            row = next;
             continue;
         }
         /* e_j; blocks wholly past the last column that is not -inf are
@@ -1703,110 +1754,164 @@ __global__ __launch_bounds__(64 * NW, Q <= 8 ? 4 : 2) void m3_softmax_wide_kerne
             } else {
                 v[j] = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        /* e in LDS, in column order, for the segments the walk sums column
-         * by column; estimates: the F32 total of each segment (any
-         * order) */
+        /* estimates: the F32 total of each segment (any order); this
+         * wave's segment 4j + r (block j, DPP row r) at totals[wave][4j+r] */
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
-            *(float4 *)(values + first + 256U * j) = v[j];
             const float t = m3_row16_sum_f32(((v[j].x + v[j].y) + v[j].z) +
                                              v[j].w);
 
             if ((lane & 15U) == 0U) {
-                segments[wave][j][drow] = t;
+                totals[wave][4U * j + drow] = t;
             }
         }
         __syncthreads();
-        /* the estimated running sum at this wave's first column */
-        float before = 0.0F;
+        /* Per segment, one per lane (lane l: this wave's segment l): the
+         * estimated running sum at its start (the totals before it, in
+         * any order) and at its end, the guessed binade E of s at its start
+         * and whether s may cross a power of two in it or lie on the other
+         * side of one from the estimate (`near`). */
+        uint32_t E_lane;
+        uint64_t near;
+        {
+            float before = 0.0F;
 
-        for (uint32_t i = lane; i < wave * Q * 4U; i += 64U) {
-            before += (&segments[0][0][0])[i];
+            for (uint32_t i = lane; i < wave * kWaveSegments; i += 64U) {
+                before += (&totals[0][0])[i];
+            }
+            before = m3_bits_f32(m3_wave_reduce(
+                m3_f32_bits(before), 0U, [](uint32_t x, uint32_t y) {
+                    return m3_f32_bits(m3_bits_f32(x) + m3_bits_f32(y));
+                }));
+            const float own =
+                lane < kWaveSegments ? totals[wave][lane] : 0.0F;
+            const float start = before + m3_wave_exclusive_sum_f32(own);
+            const float end = start + own;
+
+            E_lane = m3_binade(start);
+            near = __ballot(lane < kWaveSegments &&
+                            m3_binade(start * (1.0F - kWideMargin)) !=
+                                m3_binade(end * (1.0F + kWideMargin)));
         }
-        before = m3_bits_f32(m3_wave_reduce(
-            m3_f32_bits(before), 0U, [](uint32_t x, uint32_t y) {
-                return m3_f32_bits(m3_bits_f32(x) + m3_bits_f32(y));
-            }));
-        /* per segment: the guessed binade (as the clamped exponent field
-         * E of s) and R, packed as (E << 24) | R; R = 0xFFFFFF marks a
-         * segment that must be summed column by column. The lanes of a DPP
-         * row form the same estimate from the same values. */
+        /* per segment: R = sum of RN_int(e / ulp) at the guessed binade,
+         * marked (R = 0xFFFFFF) when a column is a tie, R reaches 2^24 - 1
+         * or E is past the F32 range; word = (E << 24) | R. A segment is a
+         * candidate for the column-by-column sum when it is marked or near
+         * (bit 4j + DPP row, mod 64, of candidates[j / 16]). */
+        constexpr int kGroups = (Q + 15) / 16;
+        uint64_t candidates[kGroups];
+
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            candidates[g] = 0ULL;
+        }
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
-            const float s0 = segments[wave][j][0];
-            const float s1 = segments[wave][j][1];
-            const float s2 = segments[wave][j][2];
-            const float s3 = segments[wave][j][3];
-            float estimate = before;
-
-            estimate = drow > 0U ? estimate + s0 : estimate;
-            estimate = drow > 1U ? estimate + s1 : estimate;
-            estimate = drow > 2U ? estimate + s2 : estimate;
-            before = ((before + s0) + s1 + s2) + s3;
-            const uint32_t field = m3_f32_bits(estimate) >> 23U;
-            const uint32_t E = field < 1U ? 1U : field;
+            const uint32_t E = (uint32_t)__builtin_amdgcn_ds_bpermute(
+                (int)(4U * (4U * j + drow)), (int)E_lane);
             const int shift = 150 - (int)E;
-            const float f[4] = {__builtin_ldexpf(v[j].x, shift),
-                                __builtin_ldexpf(v[j].y, shift),
-                                __builtin_ldexpf(v[j].z, shift),
-                                __builtin_ldexpf(v[j].w, shift)};
-            /* r = RN_int(f) summed as F32 (exact below 2^24; a sum at or
-             * above 2^24 stays there and ends the segment's fast form); a
-             * tie (f - r = +-1/2) marks the segment */
-            float R = 0.0F;
-            bool mark = E > 150U;
-
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float r = __builtin_rintf(f[q]);
-
-                mark = mark || __builtin_fabsf(f[q] - r) == 0.5F;
-                R += r;
-            }
-            R = m3_row16_sum_f32(R);
+            const float f0 = __builtin_ldexpf(v[j].x, shift);
+            const float f1 = __builtin_ldexpf(v[j].y, shift);
+            const float f2 = __builtin_ldexpf(v[j].z, shift);
+            const float f3 = __builtin_ldexpf(v[j].w, shift);
+            const float r0 = __builtin_rintf(f0);
+            const float r1 = __builtin_rintf(f1);
+            const float r2 = __builtin_rintf(f2);
+            const float r3 = __builtin_rintf(f3);
+            /* |f - RN_int(f)| <= 1/2, equal only at a tie */
+            const float off = fmaxf(
+                fmaxf(__builtin_fabsf(f0 - r0), __builtin_fabsf(f1 - r1)),
+                fmaxf(__builtin_fabsf(f2 - r2), __builtin_fabsf(f3 - r3)));
+            const float R = m3_row16_sum_f32(((r0 + r1) + r2) + r3);
+            const uint64_t ties = __ballot(off == 0.5F);
+            const bool mark = ((ties >> (16U * drow)) & 0xFFFFULL) != 0ULL ||
+                              !(R < 16777215.0F) || E > 150U;
             const uint64_t marks = __ballot(mark);
 
-            mark = ((marks >> (16U * drow)) & 0xFFFFULL) != 0ULL ||
-                   !(R < 16777215.0F);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint64_t bit =
+                    ((marks >> (16U * d)) | (near >> (4U * j + d))) & 1ULL;
+
+                candidates[j / 16] |= bit << (4U * (j % 16) + d);
+            }
             if ((lane & 15U) == 0U) {
-                words[wave * Q * 4U + 4U * j + drow] =
+                words[wave * kWaveSegments + 4U * j + drow] =
                     (E << 24U) | (mark ? 0xFFFFFFU : (uint32_t)R);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
-        /* The walk, by wave 0, over the 16 Q segments in column order (the
-         * segment t holds columns 64t .. 64t+63), 64 at a time, lane l
-         * holding segment 64 c + l. From the exact s, the segments whose
-         * guess matches s's binade and that are not marked form a run;
-         * prefix sums of their R give K at every segment end, and the run
-         * advances s in one step up to the first segment where K would
-         * reach 2^24. That segment, or the first one not in the run, is
-         * summed column by column; the next run starts after it. */
+        /* LDS lines for this wave's candidates, then their exponentials */
+        uint32_t count = 0U;
+
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            count += (uint32_t)__builtin_popcountll(candidates[g]);
+        }
+        uint32_t base = 0U;
+
+        if (lane == 0U && count != 0U) {
+            base = atomicAdd(&slot_count, count);
+        }
+        base = m3_uniform_u32(base);
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint64_t group = candidates[j / 16];
+            const uint32_t bit = 4U * (j % 16) + drow;
+            const uint32_t slot =
+                base +
+                (uint32_t)__builtin_popcountll(group & ((1ULL << bit) - 1ULL));
+            const bool keep =
+                ((group >> bit) & 1ULL) != 0ULL && slot < kWideSlots;
+
+            if (keep) {
+                staged[slot][lane & 15U] = v[j];
+            }
+            if ((lane & 15U) == 0U) {
+                slot_of[wave * kWaveSegments + 4U * j + drow] =
+                    keep ? (uint8_t)slot : 0xFFU;
+            }
+            if (j % 16 == 15) {
+                base += (uint32_t)__builtin_popcountll(group);
+            }
+        }
+        /* this wave's words, slots and lines are written: the walk may
+         * read them */
+        if (lane == 0U) {
+            __hip_atomic_store(&ready[wave], tag, __ATOMIC_RELEASE,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        /* The walk by wave 0, as in the wide kernel, each 64-segment chunk
+         * as soon as the waves holding it have posted its words; a segment
+         * summed column by column reads its staged line, or forms its
+         * exponentials again when it has none. */
         if (wave == 0U) {
             uint32_t s = 0U;
 
-            /* the walk is the row's critical path: it goes first on its
-             * SIMD */
             __builtin_amdgcn_s_setprio(3);
+            for (uint32_t chunk = 0U; chunk < kSegments / 64U; ++chunk) {
+                const uint32_t w0 = 64U * chunk / kWaveSegments;
+                const uint32_t w1 = (64U * chunk + 63U) / kWaveSegments;
 
-            for (uint32_t chunk = 0U; chunk < (uint32_t)(NW * Q) / 16U;
-                 ++chunk) {
+                for (uint32_t w = w0 > 1U ? w0 : 1U; w <= w1; ++w) {
+                    while (__hip_atomic_load(&ready[w], __ATOMIC_ACQUIRE,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP) !=
+                           tag) {
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                }
                 const uint32_t word = words[64U * chunk + lane];
                 const uint32_t guess = word >> 24U;
                 const uint32_t R = word & 0xFFFFFFU;
-                /* prefix sums of R over the chunk, once: a run from t0
-                 * reaches K + P - P[t0 - 1] at the end of segment l (in
-                 * unsigned arithmetic, so that marked segments before t0
-                 * cancel; each sum is below 2^30) */
                 const uint32_t P = m3_wave_scan_u32(R);
                 uint32_t t0 = 0U;
 
                 while (t0 < 64U) {
-                    const uint32_t field = s >> 23U;
-                    const uint32_t E = field < 1U ? 1U : field;
-                    const uint32_t base = (E - 1U) << 23U;
-                    const uint32_t K = s - base;
+                    const uint32_t E = m3_binade(m3_bits_f32(s));
+                    const uint32_t base_bits = (E - 1U) << 23U;
+                    const uint32_t K = s - base_bits;
                     const uint32_t offset =
                         t0 == 0U ? 0U
                                  : (uint32_t)__builtin_amdgcn_readlane(
@@ -1824,14 +1929,32 @@ __global__ __launch_bounds__(64 * NW, Q <= 8 ? 4 : 2) void m3_softmax_wide_kerne
                         over != 0ULL ? (uint32_t)__builtin_ctzll(over) : stop;
 
                     if (cross > t0) {
-                        s = base + K +
+                        s = base_bits + K +
                             ((uint32_t)__builtin_amdgcn_readlane(
                                  (int)P, (int)(cross - 1U)) -
                              offset);
                     }
                     if (cross < 64U) {
-                        s = m3_segment_sum_sequential(
-                            s, values + 64U * (64U * chunk + cross));
+                        const uint32_t t = 64U * chunk + cross;
+                        const uint32_t slot = slot_of[t];
+                        float4 e;
+
+                        if (slot != 0xFFU) {
+                            e = staged[slot][lane & 15U];
+                        } else {
+                            const uint32_t c = 64U * t + 4U * (lane & 15U);
+
+                            e = m3_wide_load<F32IO>(in, c, width, in_dtype);
+                            if (64U * t < last) {
+                                e.x = m3_expf_with_table(e.x - m, exp_table);
+                                e.y = m3_expf_with_table(e.y - m, exp_table);
+                                e.z = m3_expf_with_table(e.z - m, exp_table);
+                                e.w = m3_expf_with_table(e.w - m, exp_table);
+                            } else {
+                                e = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+                            }
+                        }
+                        s = m3_segment_sum_lanes(s, e);
                         t0 = cross + 1U;
                     } else {
                         t0 = 64U;
@@ -1843,17 +1966,9 @@ __global__ __launch_bounds__(64 * NW, Q <= 8 ? 4 : 2) void m3_softmax_wide_kerne
             }
             __builtin_amdgcn_s_setprio(0);
         }
-        /* the next row's reductions: the other waves while wave 0 walks
-         * (its loads have been in flight since this row began), wave 0
-         * after the walk */
-        if (next < a.rows) {
-            m3_wide_partials<Q>(ahead, first, lane, wave, part_max,
-                                part_inf, part_last);
-        }
         __syncthreads();
         const float sum = m3_bits_f32(m3_uniform_u32(carry));
         const double inverse = 1.0 / (double)sum;
-
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
             const uint32_t c = first + 256U * j;
@@ -1863,10 +1978,9 @@ __global__ __launch_bounds__(64 * NW, Q <= 8 ? 4 : 2) void m3_softmax_wide_kerne
                                          m3_softmax_scale4(v[j], inverse));
             }
         }
-        /* carry is read before the next row's walk writes it (two
-         * barriers later), and values, segments and words are rewritten
-         * only after this barrier */
-        row = next;
+        /* the next row writes part_* and totals (read before the last
+         * barrier), words, slot_of and staged (read by the walk, before
+         * it), and carry only after two more barriers */
     }
 }
 
@@ -1890,50 +2004,24 @@ void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                           dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
-/* The wide kernel's shape: NW waves per workgroup, Q float4 per lane; a
- * row of up to 256 NW Q columns per workgroup. */
-constexpr int kWideWaves = 8;
-
-/* Workgroups of the wide kernel that one CU holds at once (from its
- * register and LDS use), asked of the runtime once per instance. */
-template <int Q, bool F32IO>
-uint32_t m3_wide_per_cu()
+/* Waves per SIMD the wide kernel is built for: four (at most 128 VGPRs)
+ * for four-wave workgroups of up to 64 values per lane and for eight-wave
+ * workgroups of 48 or 64, five (96 VGPRs) for eight-wave workgroups of 40. */
+template <int Q, int NW>
+constexpr int m3_wide_waves_per_eu()
 {
-    static const uint32_t blocks = [] {
-        constexpr uint32_t lds = 1024U * kWideWaves * Q;
-        int n = 0;
-
-        if (lds > 65536U) {
-            (void)hipFuncSetAttribute(
-                (const void *)m3_softmax_wide_kernel<Q, kWideWaves, F32IO>,
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        }
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &n, m3_softmax_wide_kernel<Q, kWideWaves, F32IO>,
-                64 * kWideWaves, lds) != hipSuccess ||
-            n < 1) {
-            (void)hipGetLastError();
-            n = 1;
-        }
-        return (uint32_t)n;
-    }();
-    return blocks;
+    return NW == 8 && Q <= 10 ? 5 : 4;
 }
 
-/* The wide kernel's grid is what the device holds at once (each workgroup
- * then loops over rows, the next row's loads in flight while it computes
- * one), at most one workgroup per row. */
-template <int Q, bool F32IO>
+template <int Q, int NW, bool F32IO>
 void m3_launch_wide(dim3 grid, hipStream_t stream, hipEvent_t start,
                     hipEvent_t stop, m3_softmax_args args)
 {
-    hipExtLaunchKernelGGL((m3_softmax_wide_kernel<Q, kWideWaves, F32IO>),
-                          grid, dim3(64 * kWideWaves),
-                          1024U * kWideWaves * Q, stream, start, stop, 0U,
+    hipExtLaunchKernelGGL((m3_softmax_wide_kernel<Q, NW, F32IO,
+                                                  m3_wide_waves_per_eu<Q, NW>()>),
+                          grid, dim3(64 * NW), 0, stream, start, stop, 0U,
                           args);
 }
-
-typedef uint32_t (*m3_wide_occupancy)();
 
 template <bool F32IO, bool VEC>
 void m3_launch_stream(dim3 grid, hipStream_t stream, hipEvent_t start,
@@ -2242,29 +2330,28 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
         /* VEC rows of 2049..32768 columns: a workgroup per row at a time,
          * each row read once, the in-order sum in parallel. */
         if (vec && width > 2048U && width <= 32768U) {
-            /* Q float4 per lane, even, the smallest whose 2048 Q columns
-             * hold the row */
-#define M3_WIDE_ENTRY(Q)                                                      \
-    {{&m3_launch_wide<Q, false>, &m3_launch_wide<Q, true>},                   \
-     {&m3_wide_per_cu<Q, false>, &m3_wide_per_cu<Q, true>}}
+            /* the smallest row class that holds the width: NW waves of Q
+             * float4 per lane, 256 NW Q columns; one workgroup per row (the
+             * hardware hands a CU's next row to whichever of its workgroups
+             * ends first) */
+#define M3_WIDE_ENTRY(Q, NW)                                                  \
+    {1024U * (Q) * (NW) / 4U,                                                 \
+     {&m3_launch_wide<Q, NW, false>, &m3_launch_wide<Q, NW, true>}}
             static const struct {
+                uint32_t columns;
                 m3_softmax_launcher launch[2];
-                m3_wide_occupancy occupancy[2];
-            } wide[] = {M3_WIDE_ENTRY(2),  M3_WIDE_ENTRY(4),
-                        M3_WIDE_ENTRY(6),  M3_WIDE_ENTRY(8),
-                        M3_WIDE_ENTRY(10), M3_WIDE_ENTRY(12),
-                        M3_WIDE_ENTRY(16)};
+            } classes[] = {M3_WIDE_ENTRY(4, 4),  M3_WIDE_ENTRY(8, 4),
+                           M3_WIDE_ENTRY(12, 4), M3_WIDE_ENTRY(16, 4),
+                           M3_WIDE_ENTRY(10, 8), M3_WIDE_ENTRY(12, 8),
+                           M3_WIDE_ENTRY(16, 8)};
 #undef M3_WIDE_ENTRY
-            static const uint32_t wide_q[] = {2U, 4U, 6U, 8U, 10U, 12U, 16U};
             uint32_t which = 0U;
 
-            while (2048U * wide_q[which] < width) {
+            while (classes[which].columns < width) {
                 ++which;
             }
-            const uint64_t resident = (uint64_t)device->compute_units *
-                                      wide[which].occupancy[f32]();
-            const dim3 grid((uint32_t)(rows < resident ? rows : resident));
-            const m3_softmax_launcher launcher = wide[which].launch[f32];
+            const dim3 grid((uint32_t)(rows < kMaxGrid ? rows : kMaxGrid));
+            const m3_softmax_launcher launcher = classes[which].launch[f32];
 
             return m3_hip_launch(
                 device, "m3_softmax_rows_wide",
