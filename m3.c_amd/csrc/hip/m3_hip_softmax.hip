@@ -1614,6 +1614,16 @@ __device__ __forceinline__ float m3_wave_exclusive_sum_f32(float x)
     return t;
 }
 
+/* Index of the lowest set bit of a wave-uniform mask, 64 when there is
+ * none (one scalar instruction; s_ff1 gives 0xFFFFFFFF for zero). */
+__device__ __forceinline__ uint32_t m3_first_set(uint64_t mask)
+{
+    uint32_t index;
+
+    asm("s_ff1_i32_b64 %0, %1" : "=s"(index) : "s"(mask));
+    return index < 64U ? index : 64U;
+}
+
 /* The clamped exponent field of a non-negative F32 (1 for zero and the
  * subnormals, whose ulp is that of the smallest binade). */
 __device__ __forceinline__ uint32_t m3_binade(float x)
@@ -1883,10 +1893,15 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
             __hip_atomic_store(&ready[wave], tag, __ATOMIC_RELEASE,
                                __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        /* The walk by wave 0, as in the wide kernel, each 64-segment chunk
-         * as soon as the waves holding it have posted its words; a segment
-         * summed column by column reads its staged line, or forms its
-         * exponentials again when it has none. */
+        /* The walk by wave 0, each 64-segment chunk as soon as the waves
+         * holding it have posted its words. The state (s, the run's start
+         * t0, the prefix sum before it) stays in scalar registers; a step
+         * takes two vector compares (the segments whose guess is s's binade,
+         * the segment ends where K would reach 2^24) and three reads of a
+         * lane (the prefix sums around the run's end and the next
+         * segment's LDS line), so that it waits little behind the other
+         * waves' vector work. A segment summed column by column reads its
+         * staged line, or forms its exponentials again when it has none. */
         if (wave == 0U) {
             uint32_t s = 0U;
 
@@ -1903,62 +1918,75 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
                     }
                 }
                 const uint32_t word = words[64U * chunk + lane];
+                const uint32_t line = slot_of[64U * chunk + lane];
                 const uint32_t guess = word >> 24U;
                 const uint32_t R = word & 0xFFFFFFU;
+                /* prefix sums of R over the chunk: a run from t0 reaches
+                 * K + P - offset at the end of segment l, offset = P[t0 - 1]
+                 * (unsigned, so that marked segments before t0 cancel;
+                 * every sum is below 2^30) */
                 const uint32_t P = m3_wave_scan_u32(R);
+                const uint64_t unmarked = __ballot(R != 0xFFFFFFU);
                 uint32_t t0 = 0U;
+                uint32_t offset = 0U;
 
                 while (t0 < 64U) {
                     const uint32_t E = m3_binade(m3_bits_f32(s));
-                    const uint32_t base_bits = (E - 1U) << 23U;
-                    const uint32_t K = s - base_bits;
-                    const uint32_t offset =
-                        t0 == 0U ? 0U
-                                 : (uint32_t)__builtin_amdgcn_readlane(
-                                       (int)P, (int)(t0 - 1U));
+                    const uint32_t K = s - ((E - 1U) << 23U);
+                    const uint32_t threshold = 0x1000000U - K + offset;
+                    const uint64_t match = __ballot(guess == E);
+                    const uint64_t reach = __ballot(P >= threshold);
                     const uint64_t from = ~0ULL << t0;
-                    const uint64_t good =
-                        __ballot(guess == E && R != 0xFFFFFFU) & from;
-                    const uint64_t bad = ~good & from;
-                    const uint32_t stop =
-                        bad != 0ULL ? (uint32_t)__builtin_ctzll(bad) : 64U;
-                    const uint64_t over =
-                        __ballot(lane >= t0 && lane < stop &&
-                                 K + (P - offset) >= 0x1000000U);
+                    const uint64_t bad = ~(match & unmarked) & from;
+                    const uint32_t stop = m3_first_set(bad);
+                    const uint64_t below =
+                        stop >= 64U ? ~0ULL : (1ULL << stop) - 1ULL;
+                    /* over's bits lie below stop */
+                    const uint64_t over = reach & from & below;
+                    const uint32_t first_over = m3_first_set(over);
                     const uint32_t cross =
-                        over != 0ULL ? (uint32_t)__builtin_ctzll(over) : stop;
+                        first_over < stop ? first_over : stop;
 
-                    if (cross > t0) {
-                        s = base_bits + K +
-                            ((uint32_t)__builtin_amdgcn_readlane(
-                                 (int)P, (int)(cross - 1U)) -
-                             offset);
+                    if (cross >= 64U) {
+                        /* the run reaches the chunk's end */
+                        s += (uint32_t)__builtin_amdgcn_readlane((int)P, 63) -
+                             offset;
+                        break;
                     }
-                    if (cross < 64U) {
-                        const uint32_t t = 64U * chunk + cross;
-                        const uint32_t slot = slot_of[t];
-                        float4 e;
+                    /* the run [t0, cross) (possibly empty), then segment
+                     * `cross` column by column */
+                    const uint32_t before =
+                        cross == 0U ? 0U
+                                    : (uint32_t)__builtin_amdgcn_readlane(
+                                          (int)P, (int)(cross - 1U));
+                    const uint32_t after =
+                        (uint32_t)__builtin_amdgcn_readlane((int)P,
+                                                            (int)cross);
+                    const uint32_t slot =
+                        (uint32_t)__builtin_amdgcn_readlane((int)line,
+                                                            (int)cross);
+                    const uint32_t t = 64U * chunk + cross;
+                    float4 e;
 
-                        if (slot != 0xFFU) {
-                            e = staged[slot][lane & 15U];
-                        } else {
-                            const uint32_t c = 64U * t + 4U * (lane & 15U);
-
-                            e = m3_wide_load<F32IO>(in, c, width, in_dtype);
-                            if (64U * t < last) {
-                                e.x = m3_expf_with_table(e.x - m, exp_table);
-                                e.y = m3_expf_with_table(e.y - m, exp_table);
-                                e.z = m3_expf_with_table(e.z - m, exp_table);
-                                e.w = m3_expf_with_table(e.w - m, exp_table);
-                            } else {
-                                e = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
-                            }
-                        }
-                        s = m3_segment_sum_lanes(s, e);
-                        t0 = cross + 1U;
+                    s += before - offset;
+                    if (slot != 0xFFU) {
+                        e = staged[slot][lane & 15U];
                     } else {
-                        t0 = 64U;
+                        const uint32_t c = 64U * t + 4U * (lane & 15U);
+
+                        e = m3_wide_load<F32IO>(in, c, width, in_dtype);
+                        if (64U * t < last) {
+                            e.x = m3_expf_with_table(e.x - m, exp_table);
+                            e.y = m3_expf_with_table(e.y - m, exp_table);
+                            e.z = m3_expf_with_table(e.z - m, exp_table);
+                            e.w = m3_expf_with_table(e.w - m, exp_table);
+                        } else {
+                            e = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
+                        }
                     }
+                    s = m3_segment_sum_lanes(s, e);
+                    offset = after;
+                    t0 = cross + 1U;
                 }
             }
             if (lane == 0U) {
@@ -1969,6 +1997,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
         __syncthreads();
         const float sum = m3_bits_f32(m3_uniform_u32(carry));
         const double inverse = 1.0 / (double)sum;
+
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
             const uint32_t c = first + 256U * j;
