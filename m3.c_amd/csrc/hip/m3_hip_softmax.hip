@@ -1634,8 +1634,9 @@ __device__ __forceinline__ uint32_t m3_binade(float x)
 }
 
 /* The long-row kernel described above. One row per workgroup at a time,
- * no loads ahead in registers and about 15 KB of LDS, so that four
- * workgroups share a CU and one's walk overlaps the others' loads and
+ * no loads ahead in registers and about 15 KB of LDS, so that several
+ * workgroups share a CU (four of four waves up to 16,384 columns, two of
+ * eight waves beyond) and one's walk overlaps the others' loads and
  * exponentials. Each row goes through: the loads and the maximum (barrier),
  * the exponentials and the segment totals (barrier), the words, each wave
  * then posting a ready tag, the walk by wave 0, each 64-segment chunk as
@@ -1764,6 +1765,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
             } else {
                 v[j] = make_float4(0.0F, 0.0F, 0.0F, 0.0F);
             }
+            /* one block at a time: interleaving them costs registers */
             __builtin_amdgcn_sched_barrier(0);
         }
         /* estimates: the F32 total of each segment (any order); this
