@@ -1676,6 +1676,12 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
     __shared__ uint32_t slot_count;
     __shared__ uint32_t carry;
     __shared__ float4 staged[kWideSlots][16];
+    /* The walking wave's own values while it walks, so that its registers
+     * serve the walk and the kernel fits in 96 VGPRs (five workgroups of
+     * four waves per CU); the eight-wave classes, two workgroups per CU
+     * either way, keep them in registers. */
+    constexpr bool kPark = NW == 4;
+    __shared__ float4 parked[kPark ? Q : 1][64];
     const uint32_t width = a.width;
     const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
     const uint32_t out_dtype = F32IO ? (uint32_t)M3N_F32 : a.out_dtype;
@@ -1736,10 +1742,14 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
             /* zeros, or 1/k on the k +inf entries */
             const float one_over_count =
                 m == INFINITY ? 1.0F / (float)infinities : 0.0F;
+            /* columns formed again here (this branch is rare), not kept
+             * live from the loads */
+            uint32_t column = first;
 
+            asm volatile("" : "+v"(column));
 #pragma unroll
             for (int j = 0; j < Q; ++j) {
-                const uint32_t c = first + 256U * j;
+                const uint32_t c = column + 256U * j;
                 float4 p;
 
                 p.x = v[j].x == INFINITY ? one_over_count : 0.0F;
@@ -1906,7 +1916,18 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
          * staged line, or forms its exponentials again when it has none. */
         if (wave == 0U) {
             uint32_t s = 0U;
+            /* the lane index (and the LDS addresses made from it) formed
+             * again here, not kept in registers through the row */
+            uint32_t wl = threadIdx.x & 63U;
 
+            asm volatile("" : "+v"(wl));
+
+            if (kPark) {
+#pragma unroll
+                for (int j = 0; j < Q; ++j) {
+                    parked[kPark ? j : 0][wl] = v[j];
+                }
+            }
             __builtin_amdgcn_s_setprio(3);
             for (uint32_t chunk = 0U; chunk < kSegments / 64U; ++chunk) {
                 const uint32_t w0 = 64U * chunk / kWaveSegments;
@@ -1919,8 +1940,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
                         __builtin_amdgcn_s_sleep(1);
                     }
                 }
-                const uint32_t word = words[64U * chunk + lane];
-                const uint32_t line = slot_of[64U * chunk + lane];
+                const uint32_t word = words[64U * chunk + wl];
+                const uint32_t line = slot_of[64U * chunk + wl];
                 const uint32_t guess = word >> 24U;
                 const uint32_t R = word & 0xFFFFFFU;
                 /* prefix sums of R over the chunk: a run from t0 reaches
@@ -1972,9 +1993,9 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
 
                     s += before - offset;
                     if (slot != 0xFFU) {
-                        e = staged[slot][lane & 15U];
+                        e = staged[slot][wl & 15U];
                     } else {
-                        const uint32_t c = 64U * t + 4U * (lane & 15U);
+                        const uint32_t c = 64U * t + 4U * (wl & 15U);
 
                         e = m3_wide_load<F32IO>(in, c, width, in_dtype);
                         if (64U * t < last) {
@@ -1991,18 +2012,28 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
                     t0 = cross + 1U;
                 }
             }
-            if (lane == 0U) {
+            if (wl == 0U) {
                 carry = s;
             }
             __builtin_amdgcn_s_setprio(0);
+            if (kPark) {
+#pragma unroll
+                for (int j = 0; j < Q; ++j) {
+                    v[j] = parked[kPark ? j : 0][wl];
+                }
+            }
         }
         __syncthreads();
         const float sum = m3_bits_f32(m3_uniform_u32(carry));
         const double inverse = 1.0 / (double)sum;
+        /* the store addresses are formed here: keeping the loads' 64-bit
+         * offsets live through the row costs 32 VGPRs */
+        uint32_t column = first;
 
+        asm volatile("" : "+v"(column));
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
-            const uint32_t c = first + 256U * j;
+            const uint32_t c = column + 256U * j;
 
             if (c < width) {
                 m3_softmax_store4<F32IO>(out, c, out_dtype,
@@ -2035,13 +2066,17 @@ void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                           dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
-/* Waves per SIMD the wide kernel is built for: four (at most 128 VGPRs)
- * for four-wave workgroups of up to 64 values per lane and for eight-wave
- * workgroups of 48 or 64, five (96 VGPRs) for eight-wave workgroups of 40. */
-template <int Q, int NW>
+/* Waves per SIMD the wide kernel is built for: five (at most 96 VGPRs;
+ * five workgroups per CU) for four-wave workgroups (16-bit I/O: of up to
+ * 48 values per lane) and for eight-wave workgroups of 40, four (128
+ * VGPRs) for the rest, which would spill registers at 96. */
+template <int Q, int NW, bool F32IO>
 constexpr int m3_wide_waves_per_eu()
 {
-    return NW == 8 && Q <= 10 ? 5 : 4;
+    return NW == 4 && Q <= 4   ? 8
+           : NW == 4 && Q <= 8 ? 6
+           : (NW == 4 && (F32IO || Q <= 12)) || (NW == 8 && Q <= 10) ? 5
+                                                                    : 4;
 }
 
 template <int Q, int NW, bool F32IO>
@@ -2049,7 +2084,7 @@ void m3_launch_wide(dim3 grid, hipStream_t stream, hipEvent_t start,
                     hipEvent_t stop, m3_softmax_args args)
 {
     hipExtLaunchKernelGGL((m3_softmax_wide_kernel<Q, NW, F32IO,
-                                                  m3_wide_waves_per_eu<Q, NW>()>),
+                                                  m3_wide_waves_per_eu<Q, NW, F32IO>()>),
                           grid, dim3(64 * NW), 0, stream, start, stop, 0U,
                           args);
 }
