@@ -1614,6 +1614,20 @@ __device__ __forceinline__ float m3_wave_exclusive_sum_f32(float x)
     return t;
 }
 
+/* This lane's index in its wave (0..63), from the lane masks: two vector
+ * instructions, without the work-item id, formed where it is called (a
+ * volatile statement, so that the compiler neither hoists it out of a loop
+ * nor keeps it in a spilled register). */
+__device__ __forceinline__ uint32_t m3_lane_index()
+{
+    uint32_t index;
+
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\t"
+                 "v_mbcnt_hi_u32_b32 %0, -1, %0"
+                 : "=v"(index));
+    return index;
+}
+
 /* Index of the lowest set bit of a wave-uniform mask, 64 when there is
  * none (one scalar instruction; s_ff1 gives 0xFFFFFFFF for zero). */
 __device__ __forceinline__ uint32_t m3_first_set(uint64_t mask)
@@ -1695,15 +1709,15 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
     if (threadIdx.x < (uint32_t)NW) {
         ready[threadIdx.x] = 0U;
     }
+    const uint32_t wave_index = m3_uniform_u32(threadIdx.x >> 6U);
     for (uint64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
         /* the lane's columns and masks are formed again each row, not kept
          * live (in spilled registers) across the loop */
-        uint32_t thread = threadIdx.x;
-        uint32_t wave = m3_uniform_u32(threadIdx.x >> 6U);
+        uint32_t lane = m3_lane_index();
+        uint32_t wave = wave_index;
 
-        asm volatile("" : "+v"(thread));
+        asm volatile("" : "+v"(lane));
         asm volatile("" : "+s"(wave));
-        const uint32_t lane = thread & 63U;
         const uint32_t drow = lane >> 4U;
         /* first column of this lane in block 0 */
         const uint32_t first = wave * 256U * Q + 4U * lane;
@@ -1721,7 +1735,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
          * maximum is +inf, keeps this kernel out of spilled registers) */
         m3_wide_partials<Q>(v, first, lane, wave, part_max, part_inf,
                             part_last);
-        if (threadIdx.x == 0U) {
+        if (wave == 0U && lane == 0U) {
             slot_count = 0U;
         }
         __syncthreads();
@@ -1918,7 +1932,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
             uint32_t s = 0U;
             /* the lane index (and the LDS addresses made from it) formed
              * again here, not kept in registers through the row */
-            uint32_t wl = threadIdx.x & 63U;
+            uint32_t wl = m3_lane_index();
 
             asm volatile("" : "+v"(wl));
 
