@@ -1648,9 +1648,9 @@ __device__ __forceinline__ uint32_t m3_binade(float x)
 }
 
 /* The long-row kernel described above. One row per workgroup at a time,
- * no loads ahead in registers and about 15 KB of LDS, so that several
- * workgroups share a CU (four of four waves up to 16,384 columns, two of
- * eight waves beyond) and one's walk overlaps the others' loads and
+ * no loads ahead in registers and 15-31 KB of LDS, so that several
+ * workgroups share a CU (five to eight of four waves up to 16,384 columns,
+ * two of eight waves beyond) and one's walk overlaps the others' loads and
  * exponentials. Each row goes through: the loads and the maximum (barrier),
  * the exponentials and the segment totals (barrier), the words, each wave
  * then posting a ready tag, the walk by wave 0, each 64-segment chunk as
