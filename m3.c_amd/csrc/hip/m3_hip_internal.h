@@ -97,6 +97,10 @@ struct m3_hip_device {
     /* M3_HIP_SOFTMAX_HOLD_US at open (negative when unset): how long after
      * its start a wave of the lane-row softmax holds its stores */
     float softmax_hold_us;
+    /* M3_HIP_SOFTMAX_WIDE_GRID at open (0 when unset): at most this many
+     * workgroups in a launch of the long-row softmax, each then taking
+     * several rows in turn */
+    uint32_t softmax_wide_grid;
     /* device flags for data scans (a view's word holds the epoch of the
      * last scan that found an offending element in it), the epoch of the
      * next scan, and the flags' host mirror in coherent pinned memory */

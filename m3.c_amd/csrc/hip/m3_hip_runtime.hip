@@ -302,6 +302,7 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
         int rate = 0;
         const char *late = std::getenv("M3_HIP_SOFTMAX_LATE_US");
         const char *hold = std::getenv("M3_HIP_SOFTMAX_HOLD_US");
+        const char *wide = std::getenv("M3_HIP_SOFTMAX_WIDE_GRID");
 
         device->wall_clock_khz =
             hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate,
@@ -314,6 +315,10 @@ extern "C" int m3_hip_device_open(int ordinal, m3_hip_device **device_output,
         device->softmax_hold_us =
             hold != nullptr && hold[0] != '\0' ? std::strtof(hold, nullptr)
                                                 : -1.0F;
+        device->softmax_wide_grid =
+            wide != nullptr && wide[0] != '\0'
+                ? (uint32_t)std::strtoul(wide, nullptr, 10)
+                : 0U;
     }
     code = m3_hip_check(hipStreamCreateWithFlags(&device->stream,
                                                  hipStreamNonBlocking),

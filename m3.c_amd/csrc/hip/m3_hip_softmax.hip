@@ -2430,7 +2430,12 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
             while (classes[which].columns < width) {
                 ++which;
             }
-            const dim3 grid((uint32_t)(rows < kMaxGrid ? rows : kMaxGrid));
+            const uint64_t cap =
+                device->softmax_wide_grid != 0U &&
+                        device->softmax_wide_grid < kMaxGrid
+                    ? device->softmax_wide_grid
+                    : kMaxGrid;
+            const dim3 grid((uint32_t)(rows < cap ? rows : cap));
             const m3_softmax_launcher launcher = classes[which].launch[f32];
 
             return m3_hip_launch(

@@ -13,6 +13,7 @@ exact integers), a late maximum (tiny sums over a long prefix), values that
 underflow to subnormal e, special rows (all -inf, +inf entries), 16-bit
 input and output, padded and in-place rows.
 """
+import os
 import sys
 
 import numpy as np
@@ -181,6 +182,41 @@ def test_wide_rows_unstaged_segments(hip, width):
             [ViewSpec(0, m3.F32, (rows, width)),
              ViewSpec(1, m3.F32, (rows, width))],
             "softmax wide unstaged w=%d" % width)
+
+
+@pytest.fixture(scope="module")
+def hip_capped(gpu):
+    """A HIP backend whose long-row softmax launches at most 37 workgroups
+    (M3_HIP_SOFTMAX_WIDE_GRID, read when the device opens), so that each
+    workgroup takes several rows in turn: its LDS words, lines, slot count
+    and ready tags are used again from row to row, which launches of one
+    workgroup per row (up to 2^20 rows) never do."""
+    saved = os.environ.get("M3_HIP_SOFTMAX_WIDE_GRID")
+    os.environ["M3_HIP_SOFTMAX_WIDE_GRID"] = "37"
+    try:
+        fixture = HipFixture()
+    finally:
+        if saved is None:
+            del os.environ["M3_HIP_SOFTMAX_WIDE_GRID"]
+        else:
+            os.environ["M3_HIP_SOFTMAX_WIDE_GRID"] = saved
+    yield fixture
+    fixture.close()
+
+
+@pytest.mark.parametrize("dtypes", [(m3.F32, m3.F32), (m3.BF16, m3.F32)])
+@pytest.mark.parametrize("width", [2052, 8192, 16384, 32768])
+def test_wide_rows_several_per_workgroup(hip_capped, dtypes, width):
+    """150 rows of every kind (special rows among them) on 37 workgroups:
+    each workgroup sums four or five rows one after another."""
+    rng = np.random.default_rng(26000 + width + 7 * dtypes[0])
+    rows = 150
+    logits = wide_rows(rng, rows, width)
+    compare(hip_capped, [source_of(logits, dtypes[0]),
+                         np.zeros(logits.nbytes, np.uint8)],
+            [ViewSpec(0, dtypes[0], (rows, width)),
+             ViewSpec(1, dtypes[1], (rows, width))],
+            "softmax wide, 37 workgroups %s w=%d" % (dtypes, width))
 
 
 def test_wide_rows_full_size(hip):
