@@ -1648,10 +1648,10 @@ __device__ __forceinline__ uint32_t m3_binade(float x)
 }
 
 /* The long-row kernel described above. One row per workgroup at a time,
- * no loads ahead in registers and 15-31 KB of LDS, so that several
- * workgroups share a CU (five to eight of four waves up to 16,384 columns,
- * two of eight waves beyond) and one's walk overlaps the others' loads and
- * exponentials. Each row goes through: the loads and the maximum (barrier),
+ * no loads ahead in registers and 13-31 KB of LDS, so that several
+ * workgroups share a CU (eight to twelve of two waves up to 8,192 columns,
+ * four or five of four waves up to 16,384, two of eight waves beyond) and
+ * one's walk overlaps the others' loads and exponentials. Each row goes through: the loads and the maximum (barrier),
  * the exponentials and the segment totals (barrier), the words, each wave
  * then posting a ready tag, the walk by wave 0, each 64-segment chunk as
  * soon as the waves holding it have posted (barrier), the scale and the
@@ -1692,8 +1692,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
     __shared__ float4 staged[kWideSlots][16];
     /* The walking wave's own values while it walks, so that its registers
      * serve the walk and the kernel fits in 96 VGPRs (five workgroups of
-     * four waves per CU); the eight-wave classes, two workgroups per CU
-     * either way, keep them in registers. */
+     * four waves per CU); the two- and eight-wave classes keep them in
+     * registers, their occupancy the same either way. */
     constexpr bool kPark = NW == 4;
     __shared__ float4 parked[kPark ? Q : 1][64];
     const uint32_t width = a.width;
@@ -2080,16 +2080,17 @@ void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                           dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
-/* Waves per SIMD the wide kernel is built for: five (at most 96 VGPRs;
- * five workgroups per CU) for four-wave workgroups (16-bit I/O: of up to
- * 48 values per lane) and for eight-wave workgroups of 40, four (128
- * VGPRs) for the rest, which would spill registers at 96. */
+/* Waves per SIMD the wide kernel is built for: six (at most 80 VGPRs;
+ * twelve workgroups per CU) for two-wave workgroups of 32 values per lane,
+ * five (at most 96) for two- and four-wave workgroups of 64 values per
+ * lane with F32 I/O (ten and five workgroups per CU), four-wave ones of 48
+ * and eight-wave ones of 40, four (128 VGPRs) for the rest, which would
+ * spill registers at 96. */
 template <int Q, int NW, bool F32IO>
 constexpr int m3_wide_waves_per_eu()
 {
-    return NW == 4 && Q <= 4   ? 8
-           : NW == 4 && Q <= 8 ? 6
-           : (NW == 4 && (F32IO || Q <= 12)) || (NW == 8 && Q <= 10) ? 5
+    return NW <= 4 && Q <= 8 ? 6
+           : (NW <= 4 && (F32IO || Q <= 12)) || (NW == 8 && Q <= 10) ? 5
                                                                     : 4;
 }
 
@@ -2420,7 +2421,7 @@ extern "C" int m3_hip_launch_softmax(m3_hip_device *device,
             static const struct {
                 uint32_t columns;
                 m3_softmax_launcher launch[2];
-            } classes[] = {M3_WIDE_ENTRY(4, 4),  M3_WIDE_ENTRY(8, 4),
+            } classes[] = {M3_WIDE_ENTRY(8, 2),  M3_WIDE_ENTRY(16, 2),
                            M3_WIDE_ENTRY(12, 4), M3_WIDE_ENTRY(16, 4),
                            M3_WIDE_ENTRY(10, 8), M3_WIDE_ENTRY(12, 8),
                            M3_WIDE_ENTRY(16, 8)};
