@@ -1692,9 +1692,10 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
     __shared__ float4 staged[kWideSlots][16];
     /* The walking wave's own values while it walks, so that its registers
      * serve the walk and the kernel fits in 96 VGPRs (five workgroups of
-     * four waves per CU); the two- and eight-wave classes keep them in
-     * registers, their occupancy the same either way. */
-    constexpr bool kPark = NW == 4;
+     * four waves per CU; eight waves of 48 values with F32 I/O: 80 VGPRs,
+     * three per CU); the other classes keep them in registers, their
+     * occupancy the same either way. */
+    constexpr bool kPark = NW == 4 || (NW == 8 && Q == 12 && F32IO);
     __shared__ float4 parked[kPark ? Q : 1][64];
     const uint32_t width = a.width;
     const uint32_t in_dtype = F32IO ? (uint32_t)M3N_F32 : a.in_dtype;
@@ -2080,16 +2081,18 @@ void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                           dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
-/* Waves per SIMD the wide kernel is built for: six (at most 80 VGPRs;
- * twelve workgroups per CU) for two-wave workgroups of 32 values per lane,
- * five (at most 96) for two- and four-wave workgroups of 64 values per
- * lane with F32 I/O (ten and five workgroups per CU), four-wave ones of 48
- * and eight-wave ones of 40, four (128 VGPRs) for the rest, which would
- * spill registers at 96. */
+/* Waves per SIMD the wide kernel is built for: six (at most 80 VGPRs)
+ * for two-wave workgroups of 32 values per lane (twelve per CU) and for
+ * eight-wave ones of 48 with F32 I/O (three per CU, the walking wave's
+ * values parked in LDS: faster than two per CU, where for eight-wave
+ * workgroups of 40 three per CU measured slower); five (at most 96) for
+ * two- and four-wave workgroups of 64 values per lane with F32 I/O (ten
+ * and five per CU), four-wave ones of 48 and eight-wave ones of 40; four
+ * (128 VGPRs) for the rest, which would spill registers at 96. */
 template <int Q, int NW, bool F32IO>
 constexpr int m3_wide_waves_per_eu()
 {
-    return NW <= 4 && Q <= 8 ? 6
+    return (NW <= 4 && Q <= 8) || (NW == 8 && Q == 12 && F32IO) ? 6
            : (NW <= 4 && (F32IO || Q <= 12)) || (NW == 8 && Q <= 10) ? 5
                                                                     : 4;
 }
