@@ -1649,9 +1649,10 @@ __device__ __forceinline__ uint32_t m3_binade(float x)
 
 /* The long-row kernel described above. One row per workgroup at a time,
  * no loads ahead in registers and 13-31 KB of LDS, so that several
- * workgroups share a CU (eight to twelve of two waves up to 8,192 columns,
- * four or five of four waves up to 16,384, two of eight waves beyond) and
- * one's walk overlaps the others' loads and exponentials. Each row goes through: the loads and the maximum (barrier),
+ * workgroups share a CU (eight to twelve of two waves up to 8,192
+ * columns, four to six of four waves up to 16,384, two or three of eight
+ * waves beyond) and one's walk overlaps the others' loads and
+ * exponentials. Each row goes through: the loads and the maximum (barrier),
  * the exponentials and the segment totals (barrier), the words, each wave
  * then posting a ready tag, the walk by wave 0, each 64-segment chunk as
  * soon as the waves holding it have posted (barrier), the scale and the
@@ -2083,16 +2084,17 @@ void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
 
 /* Waves per SIMD the wide kernel is built for: six (at most 80 VGPRs)
  * for two-wave workgroups of 32 values per lane (twelve per CU) and for
- * eight-wave ones of 48 with F32 I/O (three per CU, the walking wave's
- * values parked in LDS: faster than two per CU, where for eight-wave
- * workgroups of 40 three per CU measured slower); five (at most 96) for
- * two- and four-wave workgroups of 64 values per lane with F32 I/O (ten
- * and five per CU), four-wave ones of 48 and eight-wave ones of 40; four
- * (128 VGPRs) for the rest, which would spill registers at 96. */
+ * four- and eight-wave ones of 48 with F32 I/O (six and three per CU, the
+ * walking wave's values parked in LDS: faster than five and two per CU,
+ * where for eight-wave workgroups of 40 three per CU measured slower);
+ * five (at most 96) for two- and four-wave workgroups of 64 values per
+ * lane with F32 I/O (ten and five per CU), four-wave ones of 48 with
+ * 16-bit I/O and eight-wave ones of 40; four (128 VGPRs) for the rest,
+ * which would spill registers at 96. */
 template <int Q, int NW, bool F32IO>
 constexpr int m3_wide_waves_per_eu()
 {
-    return (NW <= 4 && Q <= 8) || (NW == 8 && Q == 12 && F32IO) ? 6
+    return (NW <= 4 && Q <= 8) || (Q == 12 && F32IO) ? 6
            : (NW <= 4 && (F32IO || Q <= 12)) || (NW == 8 && Q <= 10) ? 5
                                                                     : 4;
 }
