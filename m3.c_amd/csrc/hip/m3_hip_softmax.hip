@@ -1649,7 +1649,7 @@ __device__ __forceinline__ uint32_t m3_binade(float x)
 
 /* The long-row kernel described above. One row per workgroup at a time,
  * no loads ahead in registers and 13-31 KB of LDS, so that several
- * workgroups share a CU (eight to twelve of two waves up to 8,192
+ * workgroups share a CU (eight to sixteen of two waves up to 8,192
  * columns, four to six of four waves up to 16,384, two or three of eight
  * waves beyond) and one's walk overlaps the others' loads and
  * exponentials. Each row goes through: the loads and the maximum (barrier),
@@ -1663,8 +1663,8 @@ __device__ __forceinline__ uint32_t m3_binade(float x)
  * guessed binade is wrong; all of these lie where the estimated running
  * sum is within kWideMargin of a power of two at the segment's start or
  * end, or crosses one inside it, or the segment is marked. The data waves
- * stage exactly those segments' exponentials in kWideSlots LDS lines; a
- * segment the walk needs that is not staged (more than kWideSlots
+ * stage exactly those segments' exponentials in kSlots LDS lines; a
+ * segment the walk needs that is not staged (more than kSlots
  * candidates in the row) has its exponentials formed again from the input
  * by the walking wave, the same expf of the same operands, so that the
  * bits never depend on the prediction. */
@@ -1690,7 +1690,10 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
     __shared__ uint32_t ready[NW];
     __shared__ uint32_t slot_count;
     __shared__ uint32_t carry;
-    __shared__ float4 staged[kWideSlots][16];
+    /* rows of one 64-segment chunk keep 32 lines, which lets seven
+     * two-wave workgroups share a CU */
+    constexpr uint32_t kSlots = kSegments <= 64U ? 32U : kWideSlots;
+    __shared__ float4 staged[kSlots][16];
     /* The walking wave's own values while it walks, so that its registers
      * serve the walk and the kernel fits in 96 VGPRs (five workgroups of
      * four waves per CU; eight waves of 48 values with F32 I/O: 80 VGPRs,
@@ -1902,7 +1905,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void m3_softmax_wide_kernel(
                 base +
                 (uint32_t)__builtin_popcountll(group & ((1ULL << bit) - 1ULL));
             const bool keep =
-                ((group >> bit) & 1ULL) != 0ULL && slot < kWideSlots;
+                ((group >> bit) & 1ULL) != 0ULL && slot < kSlots;
 
             if (keep) {
                 staged[slot][lane & 15U] = v[j];
@@ -2082,19 +2085,21 @@ void m3_launch_lane_rows(dim3 grid, hipStream_t stream, hipEvent_t start,
                           dim3(kThreads), 0, stream, start, stop, 0U, args);
 }
 
-/* Waves per SIMD the wide kernel is built for: six (at most 80 VGPRs)
- * for two-wave workgroups of 32 values per lane (twelve per CU) and for
- * four- and eight-wave ones of 48 with F32 I/O (six and three per CU, the
- * walking wave's values parked in LDS: faster than five and two per CU,
- * where for eight-wave workgroups of 40 three per CU measured slower);
- * five (at most 96) for two- and four-wave workgroups of 64 values per
- * lane with F32 I/O (ten and five per CU), four-wave ones of 48 with
- * 16-bit I/O and eight-wave ones of 40; four (128 VGPRs) for the rest,
- * which would spill registers at 96. */
+/* Waves per SIMD the wide kernel is built for: seven (at most 72 VGPRs;
+ * the compiler takes eight when 64 suffice) for two-wave workgroups of 32
+ * values per lane, whose 9 KB of LDS let fourteen to sixteen share a CU;
+ * six (at most 80) for four- and eight-wave workgroups of 48 with F32 I/O
+ * (six and three per CU, the walking wave's values parked in LDS: faster
+ * than five and two per CU, where for eight-wave workgroups of 40 three
+ * per CU measured slower); five (at most 96) for two- and four-wave
+ * workgroups of 64 values per lane with F32 I/O (ten and five per CU),
+ * four-wave ones of 48 with 16-bit I/O and eight-wave ones of 40; four
+ * (128 VGPRs) for the rest, which would spill registers at 96. */
 template <int Q, int NW, bool F32IO>
 constexpr int m3_wide_waves_per_eu()
 {
-    return (NW <= 4 && Q <= 8) || (Q == 12 && F32IO) ? 6
+    return NW == 2 && Q == 8 ? 7
+           : Q == 12 && F32IO ? 6
            : (NW <= 4 && (F32IO || Q <= 12)) || (NW == 8 && Q <= 10) ? 5
                                                                     : 4;
 }
